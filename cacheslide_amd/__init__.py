@@ -1,0 +1,44 @@
+"""MI355X-native CacheSlide reuse-attention hot path.
+
+Drop-in counterparts of the reference's cacheslide_vllm modules for CCPE
+attention (position, attention), WCA (wca, policy) and SLIDE slot management
+(slide, paged), computing on hand-written gfx950 kernels in
+_lib/libcacheslide_hip.so; plus fused paged-cache entry points (ccpe) and
+batched relocation (relocate).
+"""
+
+from .attention import CanonicalPositionPolicy, SelectedAssociationPolicy
+from .config import CacheSlideSettings
+from .contracts import RequestPlan
+from .paged import NativePagedKV
+from .policy import WCAConfig
+from .position import (
+    CCPEPositionError,
+    CCPEProfile,
+    ChunkIdentity,
+    CoPE,
+    CoPEPositionTrace,
+    cope_attention,
+    validate_contextual_path,
+)
+from .slide import LayerSlotMap, SlotWrite, coalesce_slot_writes
+from .storage import CacheCapacityError, CacheIntegrityError, StaleCompletionError
+from .wca import (
+    WCANumericalError,
+    WCAState,
+    WCAUpdate,
+    adaptation_weight,
+    mean_head_cosine,
+    squared_deviation,
+)
+
+__version__ = "0.1.0"
+
+__all__ = [
+    "CCPEPositionError", "CCPEProfile", "CacheCapacityError", "CacheIntegrityError",
+    "CacheSlideSettings", "CanonicalPositionPolicy", "ChunkIdentity", "CoPE",
+    "CoPEPositionTrace", "LayerSlotMap", "NativePagedKV", "RequestPlan",
+    "SelectedAssociationPolicy", "SlotWrite", "StaleCompletionError", "WCAConfig",
+    "WCANumericalError", "WCAState", "WCAUpdate", "adaptation_weight", "coalesce_slot_writes",
+    "cope_attention", "mean_head_cosine", "squared_deviation", "validate_contextual_path",
+]

@@ -1,0 +1,166 @@
+"""CCPE coordinate and WCA visibility policies (src/cacheslide_vllm/attention.py:18-72).
+
+Both policies keep the reference's callable interface, evaluated by kernels.
+``cope_attention`` recognises them and lowers them to kernel data instead of
+calling them per query chunk:
+
+* CanonicalPositionPolicy -> per-row profile row index, per-key fixed ordinal,
+  the profile's canonical [H, F, F] tensor and the strict-validation switch;
+* SelectedAssociationPolicy -> per-row "selected" and per-key "fixed" flags.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+from torch import Tensor
+
+from . import _hip
+from ._hip import call, ptr, vref
+from .contracts import RequestPlan
+from .position import ChunkIdentity, validate_contextual_path
+
+
+class _LoweredCanonical:
+    """Kernel inputs for one CanonicalPositionPolicy over one call's coordinates."""
+
+    def __init__(self, policy: "CanonicalPositionPolicy", device, query_positions, key_positions):
+        fixed = policy.plan.fixed_indices
+        ordinal = {pos: i for i, pos in enumerate(fixed)}
+        profile = policy.profile
+        known = {pos: index for index, pos in enumerate(profile.query_positions.tolist())}
+        size = (max(fixed) + 1) if fixed else 1
+        q_table = [-1] * size
+        k_table = [-1] * size
+        self.unknown = False
+        for pos, o in ordinal.items():
+            k_table[pos] = o
+            if o in known:
+                q_table[pos] = known[o]
+            else:
+                q_table[pos] = -2
+                self.unknown = True
+        q_dev = torch.tensor(q_table, dtype=torch.long, device=device)
+        k_dev = torch.tensor(k_table, dtype=torch.long, device=device)
+        self.q_rows = torch.empty(query_positions.shape[0], dtype=torch.long, device=device)
+        self.k_ord = torch.empty(key_positions.shape[0], dtype=torch.long, device=device)
+        stream = _hip.stream_of(device)
+        call("cs_mapping_gather", ptr(q_dev), size, ptr(query_positions), ptr(self.q_rows),
+             query_positions.shape[0], stream)
+        call("cs_mapping_gather", ptr(k_dev), size, ptr(key_positions), ptr(self.k_ord),
+             key_positions.shape[0], stream)
+        self._tables = (q_dev, k_dev)
+        self.canonical = policy._canonical_on(device)
+        chunks = tuple(ChunkIdentity(*entry) for entry in policy.plan.fixed_layout)
+        self.reason = profile.lookup_reason(
+            chunks, None, None, policy.checkpoint_id, profile.trained_profile_version
+        )
+
+    def raise_lookup_error(self) -> None:
+        """The ValueError profile.lookup raises for a chunk with fixed rows."""
+        if self.reason:
+            raise ValueError(self.reason)
+        if self.unknown and -2 in self.q_rows.cpu().tolist():
+            raise ValueError("CCPE profile has no contextual trace for these query positions")
+
+
+@dataclass(frozen=True)
+class CanonicalPositionPolicy:
+    """Replace fixed-query x fixed-key positions with calibrated profile values.
+
+    ``strict_contextual`` validates the hybrid path (validate_contextual_path)
+    and raises CCPEPositionError; ``mixed_bias_override`` does not check.
+    """
+
+    plan: RequestPlan
+    profile: object
+    checkpoint_id: str
+    mode: str = "strict_contextual"
+    _device_cache: dict = field(default_factory=dict, compare=False, repr=False)
+
+    def __post_init__(self):
+        if not isinstance(self.mode, str) or self.mode not in {
+            "strict_contextual",
+            "mixed_bias_override",
+        }:
+            raise ValueError("unknown CCPE position policy")
+
+    def _canonical_on(self, device) -> Tensor:
+        key = str(device)
+        if key not in self._device_cache:
+            self._device_cache[key] = self.profile.canonical_positions.to(device)
+        return self._device_cache[key]
+
+    def _lower(self, device, query_positions: Tensor, key_positions: Tensor) -> _LoweredCanonical:
+        return _LoweredCanonical(self, device, query_positions, key_positions)
+
+    def __call__(self, contextual: Tensor, queries: Tensor, keys: Tensor) -> Tensor:
+        """attention.py:32-57: substitute, then validate in strict mode."""
+        ordinal = {position: i for i, position in enumerate(self.plan.fixed_indices)}
+        query_list = queries.tolist()
+        rows = [i for i, p in enumerate(query_list) if p in ordinal]
+        if not rows:
+            return contextual
+        chunks = tuple(ChunkIdentity(*entry) for entry in self.plan.fixed_layout)
+        canonical = self.profile.lookup(
+            chunks,
+            torch.tensor([ordinal[query_list[i]] for i in rows]),
+            checkpoint_id=self.checkpoint_id,
+            trained_profile_version=self.profile.trained_profile_version,
+            device=contextual.device,
+            dtype=contextual.dtype,
+        )
+        key_list = keys.tolist()
+        columns = [i for i, p in enumerate(key_list) if p in ordinal]
+        device = _hip.require_device(contextual)
+        result = contextual.clone()
+        if columns:
+            row_idx = torch.tensor(rows, dtype=torch.long, device=device)
+            row_ord = torch.arange(len(rows), dtype=torch.long, device=device)
+            col_idx = torch.tensor(columns, dtype=torch.long, device=device)
+            col_ord = torch.tensor([ordinal[key_list[i]] for i in columns], dtype=torch.long,
+                                   device=device)
+            call("cs_canonical_substitute", vref(result), vref(canonical), ptr(row_idx),
+                 ptr(row_ord), len(rows), ptr(col_idx), ptr(col_ord), len(columns),
+                 _hip.stream_of(device))
+        if self.mode == "strict_contextual":
+            validate_contextual_path(result, queries, keys)
+        elif self.mode != "mixed_bias_override":
+            raise ValueError("unknown CCPE position policy")
+        return result
+
+
+@dataclass(frozen=True)
+class SelectedAssociationPolicy:
+    """visible(q, k) = not selected(q) or not fixed(k) or q == k (attention.py:60-72)."""
+
+    fixed_indices: tuple[int, ...]
+    selected_indices: Tensor
+
+    def _sets(self, device) -> tuple[Tensor, Tensor]:
+        fixed = torch.tensor(self.fixed_indices, dtype=torch.long, device=device)
+        selected = self.selected_indices.to(device=device, dtype=torch.long).contiguous()
+        return fixed, selected
+
+    def _lower(self, device, query_positions: Tensor, key_positions: Tensor) -> tuple[Tensor, Tensor]:
+        fixed, selected = self._sets(device)
+        sel_rows = torch.empty(query_positions.shape[0], dtype=torch.uint8, device=device)
+        fixed_keys = torch.empty(key_positions.shape[0], dtype=torch.uint8, device=device)
+        stream = _hip.stream_of(device)
+        call("cs_isin", ptr(query_positions), query_positions.shape[0], ptr(selected),
+             selected.numel(), ptr(sel_rows), stream)
+        call("cs_isin", ptr(key_positions), key_positions.shape[0], ptr(fixed), fixed.numel(),
+             ptr(fixed_keys), stream)
+        return sel_rows, fixed_keys
+
+    def __call__(self, queries: Tensor, keys: Tensor) -> Tensor:
+        device = _hip.require_device(queries, keys)
+        fixed, selected = self._sets(device)
+        nq, nk = queries.shape[0], keys.shape[0]
+        buffer = torch.empty(nq * nk + nq + nk, dtype=torch.uint8, device=device)
+        q = queries.to(torch.long).contiguous()
+        k = keys.to(torch.long).contiguous()
+        call("cs_selected_visibility", ptr(q), nq, ptr(k), nk, ptr(fixed), fixed.numel(),
+             ptr(selected), selected.numel(), ptr(buffer), _hip.stream_of(device))
+        return buffer[: nq * nk].view(torch.bool).view(nq, nk)

@@ -1,0 +1,341 @@
+/*
+ * cacheslide_hip.h -- C ABI of libcacheslide_hip.so, the gfx950 (MI355X) kernels
+ * behind the cacheslide_amd Python package.
+ *
+ * Every entry point takes plain device pointers, element strides and sizes, a
+ * hipStream_t passed as void*, and returns an int status (CS_OK == 0).  On a
+ * nonzero status cs_last_error() returns a message for the calling thread.
+ * No entry point allocates device memory; scratch space is passed in by the
+ * caller.  Data-dependent conditions that the reference reports as Python
+ * exceptions (nonfinite values, invalid contextual paths, ...) are written as
+ * bits into a caller-supplied int32 device flag word, so the host can raise the
+ * reference's exception after one readback.
+ *
+ * Reference interfaces replaced (paths relative to the CacheSlide repository):
+ *   src/cacheslide_vllm/position.py   cope_attention, CoPE, validate_contextual_path
+ *   src/cacheslide_vllm/attention.py  CanonicalPositionPolicy, SelectedAssociationPolicy
+ *   src/cacheslide_vllm/wca.py        squared_deviation, adaptation_weight,
+ *                                     mean_head_cosine, WCAState
+ *   src/cacheslide_vllm/paged.py      NativePagedKV._write_slots / gather
+ *   src/cacheslide_vllm/slide.py      LayerSlotMap._fresh_slot (free-slot order)
+ */
+#ifndef CACHESLIDE_HIP_H
+#define CACHESLIDE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types of a view. */
+enum cs_dtype { CS_F32 = 0, CS_F16 = 1, CS_BF16 = 2, CS_F64 = 3, CS_I32 = 4, CS_I64 = 5, CS_U8 = 6 };
+
+/* Return codes. */
+enum cs_status {
+  CS_OK = 0,
+  CS_EINVAL = 1,       /* argument error: shapes, dtypes, null pointers */
+  CS_ELAUNCH = 2,      /* a HIP launch or runtime call failed */
+  CS_EUNSUPPORTED = 3, /* valid arguments outside a kernel's supported range */
+  CS_ECAPACITY = 4     /* not enough free slots (CacheCapacityError) */
+};
+
+/* A strided device tensor of up to 6 dimensions; strides are in elements.
+ * A view whose data pointer is NULL is "absent". */
+typedef struct cs_view {
+  void* data;
+  int32_t dtype;
+  int32_t ndim;
+  int64_t shape[6];
+  int64_t stride[6];
+} cs_view;
+
+const char* cs_version(void);
+const char* cs_last_error(void);
+
+/* ------------------------------------------------------------------------ *
+ * Flag bits written by the attention / validation kernels (int32 word).
+ * ------------------------------------------------------------------------ */
+enum cs_flag {
+  CS_FLAG_Q_NONFINITE = 1 << 0,       /* position.py:117-124 (_rows "query") */
+  CS_FLAG_K_NONFINITE = 1 << 1,       /* _rows "key" */
+  CS_FLAG_V_NONFINITE = 1 << 2,       /* _rows "value" */
+  CS_FLAG_QPOS_NEGATIVE = 1 << 3,     /* position.py:127-137 */
+  CS_FLAG_QPOS_DUPLICATE = 1 << 4,
+  CS_FLAG_KPOS_NEGATIVE = 1 << 5,
+  CS_FLAG_KPOS_DUPLICATE = 1 << 6,
+  CS_FLAG_KPOS_UNSORTED = 1 << 7,     /* position.py:178-179 */
+  CS_FLAG_LOGIT_NONFINITE = 1 << 8,   /* position.py:162-163 */
+  CS_FLAG_POS_INVALID = 1 << 9,       /* position.py:323-334 (bias positions) */
+  CS_FLAG_SCORE_NONFINITE = 1 << 10,  /* position.py:519-520 */
+  CS_FLAG_E_NONFINITE = 1 << 11,
+  CS_FLAG_POS_NONFINITE = 1 << 12,    /* validate: positions not finite */
+  CS_FLAG_BLOCK_INVALID = 1 << 13,    /* a block-table entry outside the cache */
+  /* strict contextual-path checks, position.py:99-114, in the reference's order */
+  CS_FLAG_PATH_NEGATIVE = 1 << 16,
+  CS_FLAG_PATH_AVAILABLE = 1 << 17,
+  CS_FLAG_PATH_INCREASING = 1 << 18,
+  CS_FLAG_PATH_GAP = 1 << 19
+};
+
+/* ------------------------------------------------------------------------ *
+ * Input checks (position.py:117-137, 178-179).  Writes CS_FLAG_* bits.
+ * ------------------------------------------------------------------------ */
+
+/* Nonfinite scan of a floating view; ORs `bit` into *flags. */
+int cs_check_finite(const cs_view* x, int32_t bit, int32_t* flags, void* stream);
+
+/* int64 positions [n]: negative, duplicate and (keys only) not strictly
+ * increasing.  The quadratic duplicate scan runs only when the order check
+ * found a descent.  Bits are the query or key variants selected by `is_key`;
+ * bit 24 is used internally for query order. */
+int cs_check_positions(const int64_t* pos, int64_t n, int32_t is_key,
+                       int32_t* flags, void* stream);
+
+/* Positions tensor [H, q, k] used as CoPE coordinates: ORs CS_FLAG_POS_INVALID
+ * when an entry is nonfinite, < 0 or > max_positions-1 (position.py:323-334,
+ * 504-516), and CS_FLAG_POS_NONFINITE when an entry is nonfinite. */
+int cs_check_bias_positions(const cs_view* positions, int64_t max_positions,
+                            int32_t* flags, void* stream);
+
+/* ------------------------------------------------------------------------ *
+ * CCPE attention, generic path (any float dtype, any head dims, masks,
+ * fixed positions, lowered policies, position output).
+ * Replaces position.py:404-560 cope_attention (and with out == NULL the
+ * contextual-position computation of position.py:295-307).
+ *
+ *   q [nq, Hq, D], k [nk, Hkv, D], v [nk, Hkv, Dv]   same float dtype
+ *   e [D, P]                                         CoPE table (any float)
+ *   qpos [nq], kpos [nk]                             int64 device
+ *   attn_mask, vis_mask [Hm, nq, nk] uint8 (Hm = 1 or Hq; stride 0 broadcast)
+ *   sel_rows [nq], fixed_keys [nk] uint8 : SelectedAssociationPolicy lowering
+ *       visible = !sel_rows[r] || !fixed_keys[j] || qpos[r] == kpos[j]
+ *   fixed_pos [Hq, nq, nk]                           replaces contextual positions
+ *   canonical [Hq, F, F] with q_ord [nq], k_ord [nk] (int64, -1 = not fixed):
+ *       CanonicalPositionPolicy lowering; strict != 0 runs the path checks and
+ *       ORs CS_FLAG_PATH_* into chunk_flags[r / chunk_rows], plus bit 30 for a
+ *       chunk holding a fixed query row (the policy validates only those).
+ *   out [nq, Hq, Dv] (dtype of v) or NULL;  pos_out [Hq, nq, nk] or NULL.
+ * ------------------------------------------------------------------------ */
+typedef struct cs_ccpe_args {
+  cs_view q, k, v, e;
+  const int64_t* qpos;
+  const int64_t* kpos;
+  cs_view attn_mask, vis_mask;
+  const uint8_t* sel_rows;
+  const uint8_t* fixed_keys;
+  cs_view fixed_pos;
+  cs_view canonical;
+  const int64_t* q_ord;
+  const int64_t* k_ord;
+  int32_t strict;
+  int32_t chunk_rows;
+  int32_t* chunk_flags;
+  cs_view out;
+  cs_view pos_out;
+  int32_t* flags;
+} cs_ccpe_args;
+
+int cs_ccpe_attention(const cs_ccpe_args* args, void* stream);
+
+/* CoPE.contextual_positions (position.py:295-307) on explicit logits [H,q,k]
+ * and a gate mask allowed [Hm,q,k] uint8: sigmoid gates, fp64 reverse cumulative
+ * sum rounded once to out's dtype, clamp(0, P-1).  ORs CS_FLAG_LOGIT_NONFINITE
+ * when an allowed logit is nonfinite. */
+int cs_contextual_positions(const cs_view* logits, const cs_view* allowed,
+                            int64_t max_positions, cs_view* out, int32_t* flags, void* stream);
+
+/* Logits matrix (position.py:157-164): out[h,r,j] = q[r,h] . k[j, h/G] / sqrt(D)
+ * for every (query, key) pair, causal or not (CoPE.position_trace). */
+int cs_ccpe_logits(const cs_view* q, const cs_view* k, cs_view* out, int32_t* flags,
+                   void* stream);
+
+/* CoPE.positional_bias (position.py:309-344): bias[h,r,j] from positions
+ * [Hq, nq, nk] and query rows q [nq, Hq, D]; out dtype = accumulation dtype. */
+int cs_cope_positional_bias(const cs_view* q, const cs_view* e, const cs_view* positions,
+                            cs_view* out, int32_t* flags, void* stream);
+
+/* validate_contextual_path (position.py:28-114) on a positions tensor [H,q,k];
+ * attn_mask optional [Hm,q,k] uint8.  ORs CS_FLAG_PATH_* into *flags. */
+int cs_validate_contextual_path(const cs_view* positions, const int64_t* qpos,
+                                const int64_t* kpos, const cs_view* attn_mask,
+                                double atol, int32_t* flags, void* stream);
+
+/* SelectedAssociationPolicy.__call__ (attention.py:65-72): bool mask [nq, nk]
+ * in out[0 .. nq*nk); out must have nq*nk + nq + nk bytes (the tail holds the
+ * row/column membership flags). */
+int cs_selected_visibility(const int64_t* queries, int64_t nq, const int64_t* keys,
+                           int64_t nk, const int64_t* fixed, int64_t nfixed,
+                           const int64_t* selected, int64_t nselected, uint8_t* out,
+                           void* stream);
+
+/* out[i] = values[i] is in set[0..m) (torch.isin). */
+int cs_isin(const int64_t* values, int64_t n, const int64_t* set, int64_t m, uint8_t* out,
+            void* stream);
+
+/* CanonicalPositionPolicy substitution (attention.py:46-50):
+ * result[h, rows[i], cols[c]] = canonical[h, q_ord_rows[i], k_ord_cols[c]]. */
+int cs_canonical_substitute(cs_view* result, const cs_view* canonical,
+                            const int64_t* rows, const int64_t* row_ordinals, int64_t nrows,
+                            const int64_t* cols, const int64_t* col_ordinals, int64_t ncols,
+                            void* stream);
+
+/* ------------------------------------------------------------------------ *
+ * CCPE fast paths: bf16, D = Dv = 128, key positions 0..nk-1, no masks.
+ * K/V are read either from dense [nk, Hkv, 128] views or from the paged
+ * cache [blocks, Hkv, block_size, 256] (K = [..., :128], V = [..., 128:]) via
+ * an int32 block table [B, max_blocks].
+ * ------------------------------------------------------------------------ */
+typedef struct cs_kv_source {
+  /* paged form (block_table != NULL) */
+  const void* cache;          /* bf16 base of [blocks, Hkv, block_size, 2*128] */
+  int64_t s_block, s_head, s_offset; /* element strides; dim stride must be 1 */
+  int32_t block_size;
+  int64_t num_blocks;
+  const int32_t* block_table; /* [B, max_blocks] */
+  int64_t bt_stride;          /* elements between rows of block_table */
+  /* dense form (block_table == NULL): k,v [B][nk, Hkv, 128] */
+  const void* k;
+  const void* v;
+  int64_t k_s_batch, k_s_tok, k_s_head;
+  int64_t v_s_batch, v_s_tok, v_s_head;
+} cs_kv_source;
+
+/* Prefill (position.py:404-560 for q >> 1) on MFMA.
+ *   q [B, nq, Hq, 128] bf16 (strides q_s_batch/q_s_tok/q_s_head, dim stride 1)
+ *   qpos [B, nq] int64 (any order, each < nk_b is not required: keys 0..min(qpos,nk-1))
+ *   nk [B] int32 key counts; e [128, P] fp32 contiguous (P <= 256)
+ *   out [B, nq, Hq, 128] bf16 contiguous */
+int cs_ccpe_prefill_bf16(const void* q, int64_t q_s_batch, int64_t q_s_tok, int64_t q_s_head,
+                         const int64_t* qpos, int64_t qpos_s_batch, int32_t batch, int32_t nq,
+                         int32_t hq, int32_t hkv, const int32_t* nk, const cs_kv_source* kv,
+                         const float* e, int32_t max_positions, void* out, int32_t* flags,
+                         void* stream);
+
+/* Decode (q = 1 row per request at position nk[b]-1) with speculative
+ * split-K: splits are aligned to the last key; a split whose right-hand gate
+ * mass is below P-1 is recomputed exactly.  workspace must hold
+ * cs_ccpe_decode_workspace_bytes(batch, hq, max_nk, split) bytes.
+ *   q [B, Hq, 128] bf16 (q_s_batch, q_s_head), out [B, Hq, 128] bf16. */
+int64_t cs_ccpe_decode_workspace_bytes(int32_t batch, int32_t hq, int32_t max_nk,
+                                       int32_t split);
+int cs_ccpe_decode_bf16(const void* q, int64_t q_s_batch, int64_t q_s_head, int32_t batch,
+                        int32_t hq, int32_t hkv, const int32_t* nk, int32_t max_nk,
+                        const cs_kv_source* kv, const float* e, int32_t max_positions,
+                        int32_t split, void* workspace, void* out, int32_t* flags,
+                        void* stream);
+
+/* ------------------------------------------------------------------------ *
+ * SLIDE slot kernels (paged.py:205-240, 433-472; slide.py:103-112).
+ * cache [blocks, H, bs, 2D] any dtype; side_k/side_v [S, H, D] (may be absent).
+ * A slot s < blocks*bs is native (block s/bs, offset s%bs); s >= blocks*bs is
+ * sidecar row s - blocks*bs.  slots [n] int64 device.
+ * ------------------------------------------------------------------------ */
+int cs_slot_scatter(const cs_view* cache, const cs_view* side_k, const cs_view* side_v,
+                    const int64_t* slots, const int64_t* rows, int64_t n,
+                    const cs_view* key, const cs_view* value, void* stream);
+int cs_slot_gather(const cs_view* cache, const cs_view* side_k, const cs_view* side_v,
+                   const int64_t* slots, const int64_t* rows, int64_t n,
+                   cs_view* key, cs_view* value, void* stream);
+
+/* Relocation on a stacked cache [L, blocks, H, bs, 2D]: copy whole token
+ * records (all layers, heads, K and V) from src_slots[i] to dst_slots[i].
+ * Source and destination sets must be disjoint. */
+int cs_slot_copy(const cs_view* cache, const int64_t* src_slots, const int64_t* dst_slots,
+                 int64_t n, void* stream);
+/* Whole-page copy on a stacked cache [L, blocks, H, bs, 2D]. */
+int cs_page_copy(const cs_view* cache, const int64_t* src_blocks, const int64_t* dst_blocks,
+                 int64_t n, void* stream);
+
+/* Token -> slot maps (int64): map[tokens[i]] = slots[i]; out[i] = map[tokens[i]]. */
+int cs_mapping_scatter(int64_t* map, int64_t map_len, const int64_t* tokens,
+                       const int64_t* slots, int64_t n, void* stream);
+int cs_mapping_gather(const int64_t* map, int64_t map_len, const int64_t* tokens,
+                      int64_t* out, int64_t n, void* stream);
+
+/* Free-slot bitmap (bit set = free), nbits slots in ceil(nbits/32) words.
+ * release: set bits of slots[0..n).  acquire: take the `count` lowest free
+ * slots in ascending order (LayerSlotMap._fresh_slot order), clear them and
+ * write them to out; if fewer than count are free nothing changes and
+ * *status_out = CS_ECAPACITY (device int32). */
+int cs_freelist_release(uint32_t* bitmap, int64_t nbits, const int64_t* slots, int64_t n,
+                        void* stream);
+int cs_freelist_acquire(uint32_t* bitmap, int64_t nbits, int64_t count, int64_t* out,
+                        int32_t* status_out, void* stream);
+
+/* ------------------------------------------------------------------------ *
+ * WCA (wca.py:55-304).  fp64 throughout; per-token sums are exact
+ * (double-double accumulation of the fp64 squares, rounded once).
+ * ------------------------------------------------------------------------ */
+
+/* err[t] = sum_{h,d} (new - old)^2 and norm[t] = sum_{h,d} old^2 for rows
+ * t of old [T, H, D] selected by old_rows (NULL = identity) and new [n, H, D].
+ * ORs 1 into *flags when an input is nonfinite, 2 when err overflows and 16
+ * when norm overflows. */
+int cs_wca_score(const cs_view* old_rows_src, const int64_t* old_rows, const cs_view* fresh,
+                 double* err, double* norm, int32_t* flags, void* stream);
+
+/* alpha = err / (norm + eps), optionally clamped to [0, 1]; ORs 2 into *flags
+ * when err or norm + eps is nonfinite and 4 when the quotient is nonfinite. */
+int cs_wca_alpha(const double* err, const double* norm, int64_t n, double eps, int32_t clamp,
+                 double* alpha, int32_t* flags, void* stream);
+
+/* WCAState._promote (wca.py:202-215): available = candidate & ~selected &
+ * ~removed; slots = max(0, budget - #selected).  Takes the min(slots,
+ * #available) available tokens with the largest key[t] (ties: lower index
+ * first), sets selected[t] = 1 and writes them in that order to promoted[0..k).
+ * scratch and promoted hold n int64 each; *count_out (device) receives k.
+ * n <= 1<<24.  Single workgroup. */
+int cs_wca_promote(const double* key, const uint8_t* candidate, const uint8_t* removed,
+                   uint8_t* selected, int64_t n, int64_t budget, int64_t* scratch,
+                   int64_t* promoted, int64_t* count_out, void* stream);
+
+/* Ascending indices t with a[t] | b[t] (b may be NULL) -> out[0..*count)
+ * (WCAState.active_indices / selected_indices, wca.py:193-200). */
+int cs_mask_nonzero(const uint8_t* a, const uint8_t* b, int64_t n, int64_t* out, int64_t* count,
+                    void* stream);
+
+/* fused = w * new + (1 - w) * old in fp64 (no contraction), stored in the
+ * cache dtype (fp64 -> fp32 -> 16-bit, as torch converts); w = 1 where
+ * mandatory[i].  rows [a] index old (NULL = identity); fused_k/v [a,H,D].
+ * ORs 8 into *flags when a fused value is nonfinite in the cache dtype. */
+int cs_wca_blend(const cs_view* old_k, const cs_view* old_v, const int64_t* rows,
+                 const cs_view* new_k, const cs_view* new_v, const double* weight,
+                 const uint8_t* mandatory, cs_view* fused_k, cs_view* fused_v,
+                 int32_t* flags, void* stream);
+
+/* mean_head_cosine (wca.py:96-112) of a [n, H, D] and rows b_rows of b
+ * (NULL = identity) -> out [n]. */
+int cs_wca_head_cosine(const cs_view* a, const cs_view* b, const int64_t* b_rows, double eps,
+                       double* out, void* stream);
+
+/* WCAState.initialize masks (wca.py:161-171): candidate = reused & (err > 0);
+ * counts[0] = #reused, counts[1] = #candidates (device int64); ORs 32 into
+ * *flags when a token is neither reused nor mandatory. */
+int cs_wca_init_masks(const double* err, const uint8_t* reused, const uint8_t* mandatory,
+                      int64_t n, uint8_t* candidate, int64_t* counts, int32_t* flags,
+                      void* stream);
+
+/* Weight actually used per active row (wca.py:257-265):
+ * used[i] = 1 if mandatory[rows[i]] else (previous_layer ? alpha[rows[i]] : next[i]). */
+int cs_wca_used_alpha(const double* alpha, const double* next, const int64_t* rows,
+                      const uint8_t* mandatory, int64_t a, int32_t previous_layer,
+                      double* used, void* stream);
+
+/* Gate removal (wca.py:277-287): ascending rows[i] with selected[rows[i]] and
+ * metric < threshold (metric = cosine, or 1 - cosine when distance_mode). */
+int cs_wca_gate(const double* cosine, const int64_t* rows, const uint8_t* selected, int64_t a,
+                int32_t distance_mode, double threshold, int64_t* removed, int64_t* count,
+                void* stream);
+
+/* Commit (wca.py:289-293): alpha[rows[i]] = next[i]; removed tokens are cleared
+ * from selected and candidate and set in removed_mask. */
+int cs_wca_commit(double* alpha, const double* next, const int64_t* rows, int64_t a,
+                  const int64_t* removed, int64_t nrem, uint8_t* selected, uint8_t* candidate,
+                  uint8_t* removed_mask, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CACHESLIDE_HIP_H */

@@ -1,0 +1,51 @@
+"""The C-ABI library loads on the CPU and exports every declared entry point.
+
+No kernels are launched here (no GPU is needed to dlopen the library).
+"""
+
+import ctypes
+import re
+from pathlib import Path
+
+from cacheslide_amd import _hip
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "cacheslide_hip.h"
+
+
+def declared_symbols() -> set[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(cs_[a-z0-9_]+)\s*\(", text))
+
+
+def test_header_declares_entry_points():
+    names = declared_symbols()
+    assert {"cs_ccpe_attention", "cs_ccpe_prefill_bf16", "cs_ccpe_decode_bf16",
+            "cs_slot_scatter", "cs_slot_gather", "cs_wca_promote"} <= names
+    assert len(names) >= 30
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _hip.load()
+    for name in sorted(declared_symbols()):
+        assert hasattr(lib, name), name
+        assert isinstance(getattr(lib, name), ctypes._CFuncPtr)
+
+
+def test_binding_covers_every_declared_symbol():
+    assert declared_symbols() == set(_hip.SIGNATURES)
+
+
+def test_version_and_error_strings():
+    lib = _hip.load()
+    assert lib.cs_version().startswith(b"cacheslide_hip")
+    assert isinstance(lib.cs_last_error(), bytes)
+
+
+def test_argument_errors_need_no_device():
+    # null arguments are rejected before any HIP call
+    lib = _hip.load()
+    status = lib.cs_ccpe_attention(None, None)
+    assert status == _hip.CS_EINVAL
+    assert b"null" in lib.cs_last_error()
+    assert lib.cs_ccpe_decode_workspace_bytes(2, 4, 1000, 256) == 2 * 4 * 4 * (8 + 4 + 4 + 4 * 128)

@@ -1,0 +1,242 @@
+"""WCA kernels on the MI355X vs the reference's known answers (tests/test_wca.py)
+and the fp64 oracle (bit-exact deviations, weights, selections and blends)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from cacheslide_amd import (
+    WCAConfig,
+    WCANumericalError,
+    WCAState,
+    adaptation_weight,
+    mean_head_cosine,
+    squared_deviation,
+)
+from oracle import wca as orc
+from tests._helpers import seeded
+
+pytestmark = pytest.mark.gpu
+
+
+def make_state(device, config=None):
+    # tests/test_wca.py:14-20
+    cached = torch.ones(6, 1, 2, device=device)
+    fresh = torch.tensor([5, 4, 3, 2, 1, 100.0], device=device)[:, None, None].expand_as(cached).contiguous()
+    reused = torch.tensor([True, True, True, True, True, False], device=device)
+    state = WCAState.initialize(cached, fresh, reused, ~reused, config)
+    return state, cached, fresh, reused, ~reused
+
+
+def test_budget_and_selection(device):
+    # tests/test_wca.py:23-32
+    state, _, _, reused, mandatory = make_state(device)
+    assert state.budget == 2
+    assert state.selected_indices.tolist() == [0, 1]
+    assert state.active_indices.tolist() == [0, 1, 5]
+    assert state.candidate_mask.tolist() == [True, True, True, True, False, False]
+    reused[:] = False
+    assert state.reused_mask.sum() == 5
+
+
+def test_zero_errors_and_ties(device):
+    # tests/test_wca.py:35-43
+    cached = torch.ones(7, 2, 3, device=device)
+    mask = torch.ones(7, dtype=torch.bool, device=device)
+    state = WCAState.initialize(cached, cached + 1, mask, ~mask)
+    assert state.selected_indices.tolist() == [0, 1]
+    assert torch.equal(squared_deviation(cached, cached + 1).cpu(), torch.full((7,), 6.0, dtype=torch.float64))
+    empty = WCAState.initialize(cached, cached, mask, ~mask)
+    assert empty.budget == 0 and empty.active_indices.numel() == 0
+
+
+def test_weight_known_answers(device):
+    # tests/test_wca.py:46-60
+    cached = torch.zeros(1, 1, 2, dtype=torch.float16, device=device)
+    fresh = torch.ones_like(cached)
+    alpha = adaptation_weight(cached, fresh, epsilon=0.5)
+    assert alpha.dtype == torch.float64 and alpha.item() == 4
+    assert adaptation_weight(cached, fresh, epsilon=0.5, clamp=True).item() == 1
+    assert adaptation_weight(cached, cached).item() == 0
+    huge = torch.full((1, 1, 2), 1e30, device=device)
+    assert adaptation_weight(huge, 2 * huge).item() == pytest.approx(1.0)
+    with pytest.raises(WCANumericalError, match="overflow"):
+        adaptation_weight(torch.zeros(1, 1, 1, dtype=torch.float64, device=device),
+                          torch.full((1, 1, 1), 1e308, dtype=torch.float64, device=device))
+
+
+@pytest.mark.parametrize("mode, expected_alpha", [("previous_layer", 4), ("same_layer", 1)])
+def test_weight_order(device, mode, expected_alpha):
+    # tests/test_wca.py:63-85
+    cached = torch.ones(2, 1, 1, device=device)
+    reused = torch.tensor([True, False], device=device)
+    state = WCAState.initialize(cached, torch.tensor([3.0, 9.0], device=device)[:, None, None], reused,
+                                ~reused, WCAConfig(correction_fraction=1, epsilon=1e-20, weight_update=mode))
+    result = state.update(2, cached, cached * 2, torch.tensor([2.0, 7.0], device=device)[:, None, None],
+                          torch.tensor([4.0, 8.0], device=device)[:, None, None])
+    assert result.alpha.tolist() == pytest.approx([expected_alpha, 1])
+    assert result.fused_k[:, 0, 0].tolist() == pytest.approx([1 + expected_alpha, 7])
+    assert result.fused_v[:, 0, 0].tolist() == pytest.approx([2 + 2 * expected_alpha, 8])
+    assert state.alpha[0].item() == pytest.approx(1)
+
+
+def test_literal_gate(device):
+    # tests/test_wca.py:88-101
+    state, cached, _, _, _ = make_state(device, WCAConfig(gate_interval=2))
+    rows = state.active_indices
+    result = state.update(2, cached, cached, -cached[rows], cached[rows])
+    assert result.removed_indices.tolist() == [0, 1]
+    assert result.promoted_indices.tolist() == [2, 3]
+    assert result.next_indices.tolist() == [2, 3, 5]
+    assert not state.candidate_mask[:2].any()
+    rows = state.active_indices
+    state.update(3, cached, cached, -cached[rows], cached[rows])
+    result = state.update(4, cached, cached, -cached[rows], cached[rows])
+    assert result.removed_indices.tolist() == [2, 3]
+    assert result.promoted_indices.numel() == 0
+    assert result.next_indices.tolist() == [5]
+
+
+def test_distance_gate(device):
+    # tests/test_wca.py:104-114
+    literal, cached, _, _, _ = make_state(device)
+    distance, _, _, _, _ = make_state(device, WCAConfig(convergence_mode="distance_lt"))
+    for layer in (2, 3, 4):
+        for state in (literal, distance):
+            rows = state.active_indices
+            result = state.update(layer, cached, cached, cached[rows], cached[rows])
+            if layer < 4:
+                assert result.removed_indices.numel() == 0
+    assert literal.selected_indices.tolist() == [0, 1]
+    assert distance.selected_indices.tolist() == [2, 3]
+
+
+def test_cosine_zero_heads(device):
+    # tests/test_wca.py:117-120
+    a = torch.tensor([[[1.0, 0], [0, 1]], [[0, 0], [0, 0]]], device=device)
+    b = torch.tensor([[[1.0, 0], [0, -1]], [[1, 1], [1, 1]]], device=device)
+    assert mean_head_cosine(a, b).tolist() == [0, 0]
+
+
+def test_sparse_identity_validation(device):
+    # tests/test_wca.py:123-134
+    first, cached, _, _, _ = make_state(device, WCAConfig(gate_interval=2))
+    second, _, _, _, _ = make_state(device, WCAConfig(gate_interval=2))
+    rows = first.active_indices
+    first.update(2, cached, cached, -cached[rows], cached[rows])
+    assert second.selected_indices.tolist() == [0, 1]
+    with pytest.raises(ValueError, match="computed_indices"):
+        second.update(2, cached, cached, cached[rows], cached[rows], rows.flip(0))
+    with pytest.raises(ValueError, match="consecutively"):
+        second.update(3, cached, cached, cached[rows], cached[rows])
+    with pytest.raises(ValueError, match="shape, dtype"):
+        second.update(2, cached, cached, cached, cached)
+
+
+def test_mandatory_rows_fresh(device):
+    # tests/test_wca.py:137-144
+    cached = torch.ones(3, 1, 1, device=device)
+    reused = torch.tensor([True, True, False], device=device)
+    mandatory = torch.tensor([False, True, True], device=device)
+    state = WCAState.initialize(cached, cached + 2, reused, mandatory)
+    result = state.update(2, cached, cached, cached * 2, cached * 3)
+    assert result.fused_k[1:, 0, 0].tolist() == [2, 2]
+    assert result.fused_v[1:, 0, 0].tolist() == [3, 3]
+
+
+def test_invalid_masks_and_transactional_overflow(device):
+    # tests/test_wca.py:147-168
+    cached = torch.ones(1, 1, 1, device=device)
+    with pytest.raises(ValueError, match="mandatory"):
+        WCAState.initialize(cached, cached, torch.tensor([False], device=device),
+                            torch.tensor([False], device=device))
+    with pytest.raises(WCANumericalError, match="finite"):
+        adaptation_weight(cached, cached * torch.nan)
+    half = torch.zeros(1, 1, 1, dtype=torch.float16, device=device)
+    state = WCAState.initialize(half, half + 1, torch.tensor([True], device=device),
+                                torch.tensor([False], device=device))
+    initial = {n: getattr(state, n).clone() for n in ("alpha", "candidate_mask", "selected_mask", "removed_mask")}
+    with pytest.raises(WCANumericalError, match="overflow"):
+        state.update(2, half, half, half + 1, half + 1)
+    assert state.last_layer == 1
+    assert state.selected_indices.tolist() == [0]
+    for name, value in initial.items():
+        assert torch.equal(getattr(state, name), value)
+
+
+def test_float64_overflow_messages(device):
+    # tests/test_wca.py:221-231
+    zero = torch.zeros(1, 1, 1, dtype=torch.float64, device=device)
+    huge = torch.full_like(zero, 1e308)
+    with pytest.raises(WCANumericalError, match="deviation overflow"):
+        squared_deviation(zero, huge)
+    with pytest.raises(WCANumericalError, match="weight overflow"):
+        adaptation_weight(huge, huge)
+    with pytest.raises(WCANumericalError, match="weight overflow"):
+        adaptation_weight(zero, zero + 1, epsilon=1e-320)
+
+
+# ------------------------------------------------------------ seeded vs oracle
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_wca_trajectory_bit_exact_vs_oracle(device, dtype):
+    """Eight layers of WCA on drifted bf16 KV: deviations, weights, selections,
+    removals/promotions and fused K/V identical to the fp64 oracle."""
+    T, H, D = 700, 8, 128
+    name = "bfloat16" if dtype == torch.bfloat16 else "float32"
+    fresh = seeded((T, H, D), 200, dtype=dtype)
+    cached = (fresh.double() + seeded((T, H, D), 201, scale=0.05).double()).to(dtype)
+    reused = torch.ones(T, dtype=torch.bool)
+    reused[600:640] = False
+    mandatory = ~reused
+    mandatory[-1] = True
+    cfg = dict(fraction=0.15, gate_interval=2, threshold=0.999)
+    ost = orc.State(cached.double().numpy(), fresh.double().numpy(), reused.numpy(), mandatory.numpy(),
+                    dtype=name, **cfg)
+    dst = WCAState.initialize(cached.to(device), fresh.to(device), reused.to(device), mandatory.to(device),
+                              WCAConfig(correction_fraction=0.15, gate_interval=2, convergence_threshold=0.999))
+    np.testing.assert_array_equal(dst.initial_deviation.cpu().numpy(), ost.initial)
+    np.testing.assert_array_equal(dst.alpha.cpu().numpy(), ost.alpha)
+    assert dst.selected_indices.tolist() == np.flatnonzero(ost.selected).tolist()
+    for layer in range(2, 10):
+        ck = seeded((T, H, D), 300 + layer, dtype=dtype)
+        cv = seeded((T, H, D), 400 + layer, dtype=dtype)
+        idx = ost.active
+        rk = (ck[idx].double() + seeded((len(idx), H, D), 500 + layer, scale=0.3).double()).to(dtype)
+        rv = (cv[idx].double() + seeded((len(idx), H, D), 600 + layer, scale=0.3).double()).to(dtype)
+        o_idx, ofk, ofv, oused, orem, oprom, onext = ost.update(
+            layer, ck.double().numpy(), cv.double().numpy(), rk.double().numpy(), rv.double().numpy())
+        res = dst.update(layer, ck.to(device), cv.to(device), rk.to(device), rv.to(device))
+        assert res.indices.tolist() == o_idx.tolist()
+        np.testing.assert_array_equal(res.alpha.cpu().numpy(), oused)
+        np.testing.assert_array_equal(res.fused_k.double().cpu().numpy(), ofk)
+        np.testing.assert_array_equal(res.fused_v.double().cpu().numpy(), ofv)
+        assert res.removed_indices.tolist() == orem.tolist()
+        assert res.promoted_indices.tolist() == oprom.tolist()
+        assert res.next_indices.tolist() == onext.tolist()
+        np.testing.assert_array_equal(dst.alpha.cpu().numpy(), ost.alpha)
+
+
+def test_promotion_ties_and_large_budget(device):
+    """Many equal deviations: the stable order (descending, lower index first)."""
+    T = 5000
+    rng = np.random.default_rng(12)
+    levels = rng.integers(0, 6, T).astype(np.float64)  # heavy ties
+    fresh = torch.from_numpy(np.sqrt(levels)[:, None, None]).float()
+    cached = torch.zeros((T, 1, 1))
+    reused = torch.ones(T, dtype=torch.bool)
+    mandatory = torch.zeros(T, dtype=torch.bool)
+    mandatory[-1] = True
+    ost = orc.State(cached.double().numpy(), fresh.double().numpy(), reused.numpy(), mandatory.numpy(),
+                    fraction=0.4)
+    dst = WCAState.initialize(cached.to(device), fresh.to(device), reused.to(device), mandatory.to(device),
+                              WCAConfig(correction_fraction=0.4))
+    assert dst.budget == ost.budget
+    assert dst.selected_indices.tolist() == np.flatnonzero(ost.selected).tolist()
+    fresh_order = ost.promote  # the promoted order is checked through _promote below
+    dst.selected_mask.zero_()
+    ost.selected[:] = False
+    promoted_dev = dst._promote().tolist()
+    promoted_orc = fresh_order().tolist()
+    assert promoted_dev == promoted_orc
