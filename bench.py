@@ -1,0 +1,297 @@
+#!/usr/bin/env python3
+"""Benchmark of the CCPE reuse-attention hot path on one MI355X.
+
+Workload (the headline configuration): single-layer CCPE prefill attention at
+Mistral-7B head shape -- batch 8 x (4 chunks x 1024 tokens), 32 query / 8 KV
+heads, head dim 128, bf16, Q/K/V ~ N(0, 1), CoPE table [128, 64] ~ N(0, 0.02),
+paged KV with block size 16 and seeded random-permutation block tables.  One
+step is one launch of the fused MFMA prefill kernel over the whole batch,
+reading K/V through the block table.
+
+Also reported: the decode kernel at the 64-request x 32k-context shape (one
+layer's distinct KV, 8.6 GB, per call), and the CPU baseline (the numpy
+oracle, bounded sample, same op order as the reference).
+
+Prints one JSON line.  Only one GPU is used: --gpus above 1 exits.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "CCPE decode tok/s + HBM TB/s %peak; prefill TFLOP/s %MFMA peak, 1 MI355X"
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+
+
+def seed_gen(cfg: int, j: int):
+    import torch
+
+    return torch.Generator("cpu").manual_seed(1000 * cfg + j)
+
+
+def prefill_flops(b, hq, n, d, p) -> float:
+    """4 B Hq D N(N+1)/2 (QK^T and PV over the causal triangle) + 2 B Hq N D P (Q.E)."""
+    return 4.0 * b * hq * d * n * (n + 1) / 2 + 2.0 * b * hq * n * d * p
+
+
+def traffic_from_profiles(name: str):
+    """HBM bytes per launch recorded in profiles/<name>.md ('traffic_bytes_per_launch: N')."""
+    path = ROOT / "profiles" / f"{name}.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            try:
+                return float(line.split(":", 1)[1].strip())
+            except ValueError:
+                return None
+    return None
+
+
+def build_prefill(device):
+    import torch
+
+    from cacheslide_amd import _hip
+    from cacheslide_amd.paged import HipSlotMover
+
+    B, CH, L, HQ, HKV, D, P, BS = 8, 4, 1024, 32, 8, 128, 64, 16
+    N = CH * L
+    q = torch.randn((B, N, HQ, D), generator=seed_gen(2, 0)).to(torch.bfloat16)
+    k = torch.randn((B, N, HKV, D), generator=seed_gen(2, 1)).to(torch.bfloat16)
+    v = torch.randn((B, N, HKV, D), generator=seed_gen(2, 2)).to(torch.bfloat16)
+    e = torch.randn((D, P), generator=seed_gen(2, 3)) * 0.02
+    nblocks = B * N // BS
+    table = torch.randperm(nblocks, generator=seed_gen(2, 4)).to(torch.int32).view(B, N // BS)
+    cache = torch.empty((nblocks, HKV, BS, 2 * D), dtype=torch.bfloat16, device=device)
+    mover = HipSlotMover()
+    tok = torch.arange(N)
+    for b in range(B):
+        slots = (table[b, tok // BS].long() * BS + tok % BS).tolist()
+        mover.scatter(cache, None, None, slots, k[b].to(device), v[b].to(device))
+    torch.cuda.synchronize()
+    inputs = dict(
+        q=q.to(device), cache=cache, table=table.to(device), e=e.to(device).contiguous(),
+        qpos=torch.arange(N, device=device).repeat(B, 1).contiguous(),
+        nk=torch.full((B,), N, dtype=torch.int32, device=device),
+        out=torch.empty((B, N, HQ, D), dtype=torch.bfloat16, device=device),
+        flags=_hip.new_flags(device),
+    )
+    shape = dict(B=B, N=N, HQ=HQ, HKV=HKV, D=D, P=P, BS=BS)
+    host = dict(q=q, k=k, v=v, e=e)
+    return inputs, shape, host
+
+
+def prefill_launcher(inputs, shape, device):
+    from cacheslide_amd import _hip
+    from cacheslide_amd.ccpe import _paged_source
+
+    lib = _hip.load()
+    src = _paged_source(inputs["cache"], inputs["table"])
+    q, qpos = inputs["q"], inputs["qpos"]
+    args = (
+        _hip.ptr(q), q.stride(0), q.stride(1), q.stride(2), _hip.ptr(qpos), qpos.stride(0),
+        shape["B"], shape["N"], shape["HQ"], shape["HKV"], _hip.ptr(inputs["nk"]), src,
+        _hip.ptr(inputs["e"]), shape["P"], _hip.ptr(inputs["out"]), _hip.ptr(inputs["flags"]),
+        _hip.stream_of(device),
+    )
+
+    def step():
+        status = lib.cs_ccpe_prefill_bf16(*args)
+        if status:
+            _hip.check(status, "cs_ccpe_prefill_bf16")
+
+    return step
+
+
+def time_steps(step, steps: int, warmup: int):
+    import torch
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        step()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps  # ms
+
+
+def spot_check_prefill(inputs, host, shape):
+    """A few rows of batch 0 / GQA group 0 against the oracle (guards the number)."""
+    import numpy as np
+
+    from oracle import ccpe as orc
+
+    rows = [0, 777, shape["N"] - 1]
+    out = inputs["out"][0, rows, :4].float().cpu().numpy()
+    k = host["k"][0, :, :1].float().numpy()
+    v = host["v"][0, :, :1].float().numpy()
+    worst = 0.0
+    for i, r in enumerate(rows):
+        q = host["q"][0, r : r + 1, :4].float().numpy()
+        exp = orc.cope_attention(q, k[: r + 1], v[: r + 1], host["e"].numpy(), np.array([r]))
+        worst = max(worst, float(np.abs(out[i] - exp[0]).max()))
+    return worst
+
+
+def cpu_baseline(host, shape, heads: int):
+    """Oracle (numpy, reference op order, 64-row query chunks) on batch item 0 and
+    the first `heads` query heads of KV head 0 (one GQA group), all N rows."""
+    import numpy as np
+
+    from oracle import ccpe as orc
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:  # pragma: no cover - informational only
+        threads = 1
+    N, D, P = shape["N"], shape["D"], shape["P"]
+    q = host["q"][0, :, :heads].float().numpy()
+    k = host["k"][0, :, :1].float().numpy()
+    v = host["v"][0, :, :1].float().numpy()
+    e = host["e"].numpy()
+    t0 = time.perf_counter()
+    orc.cope_attention(q, k, v, e, np.arange(N), query_chunk_size=64)
+    seconds = time.perf_counter() - t0
+    flops = prefill_flops(1, heads, N, D, P)
+    return {
+        "value": round(flops / seconds / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"oracle/ccpe.py cope_attention (numpy, query_chunk_size 64) on batch item 0, "
+                  f"{heads} of 32 query heads (one GQA group), all {N} rows: "
+                  f"{flops / 1e9:.1f} GFLOP in {seconds:.2f} s on os.cpu_count()={os.cpu_count()}",
+    }
+
+
+def decode_measure(device, steps: int, warmup: int):
+    """Decode kernel at 64 requests x 32k context (position 32768), 32q/8kv, d 128,
+    one layer's distinct KV (8.6 GB)."""
+    import torch
+
+    from cacheslide_amd import CoPE, _hip
+    from cacheslide_amd.ccpe import _paged_source, decode_workspace
+
+    B, CTX, HQ, HKV, D, P, BS, SPLIT = 64, 32769, 32, 8, 128, 64, 16, 512
+    per = (CTX + BS - 1) // BS
+    nblocks = B * per
+    gen = torch.Generator(device=device).manual_seed(5005)
+    cache = torch.empty((nblocks, HKV, BS, 2 * D), dtype=torch.bfloat16, device=device)
+    cache.normal_(generator=gen)
+    table = torch.randperm(nblocks, generator=seed_gen(5, 1)).to(torch.int32).view(B, per).to(device)
+    q = torch.randn((B, HQ, D), generator=seed_gen(5, 2)).to(torch.bfloat16).to(device)
+    cope = CoPE(D, P, device=device)
+    with torch.no_grad():
+        cope.position_embeddings.copy_(torch.randn((D, P), generator=seed_gen(5, 3)) * 0.02)
+    nk = torch.full((B,), CTX, dtype=torch.int32, device=device)
+    ws = decode_workspace(B, HQ, CTX, SPLIT, device)
+    out = torch.empty((B, HQ, D), dtype=torch.bfloat16, device=device)
+    flags = _hip.new_flags(device)
+    src = _paged_source(cache, table)
+    lib = _hip.load()
+    e = cope.position_embeddings.detach()
+    args = (_hip.ptr(q), q.stride(0), q.stride(1), B, HQ, HKV, _hip.ptr(nk), CTX, src, _hip.ptr(e), P,
+            SPLIT, _hip.ptr(ws), _hip.ptr(out), _hip.ptr(flags), _hip.stream_of(device))
+
+    def step():
+        status = lib.cs_ccpe_decode_bf16(*args)
+        if status:
+            _hip.check(status, "cs_ccpe_decode_bf16")
+
+    ms = time_steps(step, steps, warmup)
+    kv_bytes = B * CTX * HKV * D * 2 * 2
+    gbs = kv_bytes / (ms * 1e-3) / 1e9
+    del cache
+    torch.cuda.empty_cache()
+    return {
+        "workload": "ccpe_decode_paged: 64 requests x 32769 keys, 32q/8kv heads, head_dim 128, "
+                    "P=64, block 16, split 512, one layer of distinct KV",
+        "ms_per_call": round(ms, 4),
+        "kv_bytes_per_call": kv_bytes,
+        "achieved_GBs": round(gbs, 1),
+        "hbm_frac": round(gbs / PEAK_HBM_GBS, 4),
+        "tok_per_s_attention_32_layers": round(B / (32 * ms * 1e-3), 1),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--cpu-heads", type=int, default=2)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(run with --gpus 1)", file=sys.stderr)
+        return 2
+    import torch
+
+    device = torch.device("cuda", 0)
+    inputs, shape, host = build_prefill(device)
+    step = prefill_launcher(inputs, shape, device)
+    ms = time_steps(step, args.steps, args.warmup)
+    flops = prefill_flops(shape["B"], shape["HQ"], shape["N"], shape["D"], shape["P"])
+    tflops = flops / (ms * 1e-3) / 1e12
+    check_err = spot_check_prefill(inputs, host, shape)
+    if check_err > 2e-2:
+        print(f"prefill spot check failed: max abs error {check_err}", file=sys.stderr)
+        return 1
+    record = {
+        "metric": METRIC,
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded N(0,1) Q/K/V, CoPE table N(0,0.02), random-permutation block tables",
+        "config": {
+            "workload": "ccpe_prefill_paged: batch 8 x 4 chunks x 1024 tokens, 32q/8kv heads, "
+                        "head_dim 128, CoPE P=64, paged KV block 16",
+            "batch": shape["B"],
+            "tokens_per_request": shape["N"],
+            "flop_per_step": flops,
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(tflops, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+            "traffic": traffic_from_profiles("ccpe_prefill_paged_mistral7b"),
+        },
+        "spot_check_max_abs_err": round(check_err, 5),
+    }
+    del inputs
+    torch.cuda.empty_cache()
+    if not args.no_decode:
+        record["decode"] = decode_measure(device, max(5, args.steps // 5), 2)
+    if not args.no_cpu_baseline:
+        record["cpu_baseline"] = cpu_baseline(host, shape, args.cpu_heads)
+    print(json.dumps(record), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -52,10 +52,25 @@ class _LoweredCanonical:
              key_positions.shape[0], stream)
         self._tables = (q_dev, k_dev)
         self.canonical = policy._canonical_on(device)
+        self.profile_rows = len(known)
+        self.fixed_count = len(fixed)
         chunks = tuple(ChunkIdentity(*entry) for entry in policy.plan.fixed_layout)
         self.reason = profile.lookup_reason(
             chunks, None, None, policy.checkpoint_id, profile.trained_profile_version
         )
+
+    def fits(self, heads: int) -> bool:
+        """The canonical tensor covers every (head, profile row, fixed ordinal) the kernel reads."""
+        c = self.canonical
+        return (
+            c.ndim == 3
+            and c.shape[0] == heads
+            and c.shape[1] == self.profile_rows
+            and c.shape[2] >= self.fixed_count
+        )
+
+    def any_fixed_row(self) -> bool:
+        return bool((self.q_rows != -1).any().item())
 
     def raise_lookup_error(self) -> None:
         """The ValueError profile.lookup raises for a chunk with fixed rows."""

@@ -21,14 +21,14 @@ from . import _hip
 from ._hip import call, ptr
 
 
-def _check_e(cope, device) -> Tensor:
+def _check_e(cope, device, max_positions: int = 256) -> Tensor:
     e = cope.position_embeddings.detach()
     if e.device != device:
         raise ValueError("query and learned embeddings must share a device")
     if e.dtype != torch.float32 or not e.is_contiguous() or e.shape[0] != 128:
         raise ValueError("the fused kernels need a contiguous float32 [128, P] CoPE table")
-    if not 2 <= cope.max_positions <= 256:
-        raise ValueError("the fused kernels support 2 <= max_positions <= 256")
+    if not 2 <= cope.max_positions <= max_positions:
+        raise ValueError(f"this fused kernel supports 2 <= max_positions <= {max_positions}")
     return e
 
 
@@ -103,7 +103,7 @@ def ccpe_prefill_paged(
         raise ValueError("context_lens must be int32 [batch]")
     if query_positions.shape != (b, nq) or query_positions.dtype != torch.long or query_positions.stride(1) != 1:
         raise ValueError("query_positions must be int64 [batch, rows]")
-    e = _check_e(cope, device)
+    e = _check_e(cope, device, max_positions=128)
     src = _paged_source(cache, block_table)
     flags = _hip.new_flags(device)
     out = torch.empty((b, nq, hq, 128), dtype=torch.bfloat16, device=device)

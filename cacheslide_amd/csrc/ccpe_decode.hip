@@ -103,7 +103,8 @@ __global__ void __launch_bounds__(kThreads) decode_split_kernel(decode_params p,
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int G = p.group;
   const int nk = p.nk[b];
-  const int splits = (nk + p.split - 1) / p.split;
+  int splits = (nk + p.split - 1) / p.split;
+  if (splits > p.smax) splits = p.smax;  // the workspace holds smax splits
   if (r >= splits) return;
   const int64_t hi = static_cast<int64_t>(nk) - static_cast<int64_t>(r) * p.split;
   const int64_t lo = hi - p.split > 0 ? hi - p.split : 0;
@@ -246,6 +247,7 @@ __global__ void __launch_bounds__(kThreads) decode_split_kernel(decode_params p,
         double tile_total = __shfl(s, 0, 64);
         float pos = static_cast<float>(carry + s);
         pos = pos < top ? pos : top;
+        pos = pos > 0.f ? pos : 0.f;  // also maps NaN to 0: table reads stay in range
         float fl = floorf(pos);
         int lo_i = static_cast<int>(fl);
         int hi_i = lo_i + 1 < p.npos - 1 ? lo_i + 1 : p.npos - 1;
@@ -369,7 +371,8 @@ __global__ void decode_combine_kernel(decode_params p) {
   const int b = bh / p.hq, h = bh % p.hq;
   const int d = threadIdx.x;  // 128 threads
   const int nk = p.nk[b];
-  const int splits = (nk + p.split - 1) / p.split;
+  int splits = (nk + p.split - 1) / p.split;
+  if (splits > p.smax) splits = p.smax;
   float M = -INFINITY;
   for (int r = 0; r < splits; ++r) M = fmaxf(M, p.mx[ws_index(p, b, h, r)]);
   float L = 0.f, O = 0.f;

@@ -45,7 +45,11 @@ constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kKStride = kD + 8;       // bf16 per K row in LDS (272 B)
 constexpr int kVStride = kTileN + 8;   // bf16 per V^T row in LDS (144 B)
-constexpr int kMaxPos = 256;
+// The per-wave QE tables live in LDS next to the K / V^T tiles; P <= 128 keeps
+// the workgroup at <= 101 KB, under the 160 KB a gfx950 workgroup may use.
+constexpr int kMaxPos = 128;
+constexpr size_t kStaticLds = sizeof(uint16_t) * (kTileN * kKStride + kD * kVStride) + 16;
+constexpr size_t kLdsLimit = 160 * 1024;
 
 struct kv_addr {
   const uint16_t* cache;
@@ -357,6 +361,7 @@ __global__ void __launch_bounds__(kThreads, 2) ccpe_prefill_kernel(prefill_param
           int R = 4 * mt + 2 * (v / 8) + g;
           float pos = carry + excl[R] + gsuf[mt][v];
           pos = pos < top ? pos : top;
+          pos = pos > 0.f ? pos : 0.f;  // also maps NaN to 0: table reads stay in range
           float fl = floorf(pos);
           int lo = static_cast<int>(fl);
           int hi = lo + 1 < p.npos - 1 ? lo + 1 : p.npos - 1;
@@ -524,6 +529,10 @@ extern "C" int cs_ccpe_prefill_bf16(const void* q, int64_t q_s_batch, int64_t q_
   CS_REQUIRE(total < (1ll << 31), "grid too large");
   p.total_wg = static_cast<int32_t>(total);
   size_t smem = sizeof(float) * kWaves * 32 * p.tab_stride;
+  if (smem + kStaticLds > kLdsLimit) {
+    set_error("prefill LDS %zu bytes exceeds the workgroup limit", smem + kStaticLds);
+    return CS_EUNSUPPORTED;
+  }
   hipLaunchKernelGGL(ccpe_prefill_kernel, dim3(p.total_wg), dim3(kThreads), smem,
                      as_stream(stream), p);
   CS_LAUNCH_CHECK("ccpe_prefill");

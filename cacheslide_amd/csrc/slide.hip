@@ -47,6 +47,8 @@ inline int pick_width(int64_t row_bytes, std::initializer_list<const void*> ptrs
 struct kv_rows {  // [rows, H, D] view of key or value, in bytes
   char* base;
   int64_t s_row, s_head;  // bytes
+  int64_t n_rows;
+  int64_t step;  // bytes between consecutive chunks along D
 };
 
 struct paged {  // [blocks, H, bs, 2D] cache + optional sidecar, in bytes
@@ -56,7 +58,9 @@ struct paged {  // [blocks, H, bs, 2D] cache + optional sidecar, in bytes
   char* side_k;
   char* side_v;
   int64_t side_rows, side_s_row, side_s_head;
-  int64_t d_bytes;  // bytes of one K (or V) row of one head
+  int64_t v_off;      // bytes from a record's K half to its V half
+  int64_t c_step;     // bytes between chunks along D in the cache
+  int64_t side_step;  // ... and in the sidecar
 };
 
 // One work item = one chunk of one (row, head, K|V) record.
@@ -77,15 +81,16 @@ __global__ void slot_move_kernel(paged pg, kv_rows key, kv_rows value, const int
     int64_t slot = slots[i];
     int64_t r = rows ? rows[i] : i;
     const kv_rows& src = kv ? value : key;
-    char* dense = src.base + r * src.s_row + h * src.s_head + c * W;
+    if (r < 0 || r >= src.n_rows) continue;
+    char* dense = src.base + r * src.s_row + h * src.s_head + c * src.step;
     char* paged_ptr;
     if (slot >= 0 && slot < pg.native) {
       int64_t blk = slot / pg.bs, off = slot % pg.bs;
-      paged_ptr = pg.cache + blk * pg.s_block + h * pg.s_head + off * pg.s_off + kv * pg.d_bytes +
-                  c * W;
+      paged_ptr = pg.cache + blk * pg.s_block + h * pg.s_head + off * pg.s_off + kv * pg.v_off +
+                  c * pg.c_step;
     } else if (slot >= pg.native && slot < pg.native + pg.side_rows && pg.side_k) {
       char* side = kv ? pg.side_v : pg.side_k;
-      paged_ptr = side + (slot - pg.native) * pg.side_s_row + h * pg.side_s_head + c * W;
+      paged_ptr = side + (slot - pg.native) * pg.side_s_row + h * pg.side_s_head + c * pg.side_step;
     } else {
       continue;  // out-of-range slots are rejected on the host; never touch memory
     }
@@ -116,18 +121,20 @@ int slot_move(const cs_view* cache, const cs_view* side_k, const cs_view* side_v
   CS_REQUIRE(cache->shape[3] % 2 == 0 && key->shape[1] == heads && key->shape[2] == d &&
                  value->shape[1] == heads && value->shape[2] == d,
              "key/value must be [rows, %lld, %lld]", (long long)heads, (long long)d);
-  CS_REQUIRE(cache->stride[3] == 1 && key->stride[2] == 1 && value->stride[2] == 1,
-             "innermost dimension must be contiguous");
   bool side = present(side_k) && present(side_v);
   if (side) {
     CS_REQUIRE(side_k->ndim == 3 && side_v->ndim == 3 && side_k->shape[1] == heads &&
                    side_k->shape[2] == d && side_v->shape[0] == side_k->shape[0] &&
-                   side_k->stride[2] == 1 && side_v->stride[2] == 1 &&
+                   side_k->stride[2] == side_v->stride[2] &&
                    side_k->stride[0] == side_v->stride[0] && side_k->stride[1] == side_v->stride[1] &&
                    side_k->dtype == cache->dtype && side_v->dtype == cache->dtype,
                "sidecar must be [S, %lld, %lld] with matching strides", (long long)heads,
                (long long)d);
   }
+  // Innermost strides may be arbitrary (the reference indexes actual strides);
+  // contiguous rows move in wide chunks, strided ones element by element.
+  const bool contiguous = cache->stride[3] == 1 && key->stride[2] == 1 && value->stride[2] == 1 &&
+                          (!side || side_k->stride[2] == 1);
   if (n == 0) return CS_OK;
   paged pg{};
   pg.cache = static_cast<char*>(cache->data);
@@ -137,7 +144,7 @@ int slot_move(const cs_view* cache, const cs_view* side_k, const cs_view* side_v
   pg.blocks = cache->shape[0];
   pg.bs = cache->shape[2];
   pg.native = pg.blocks * pg.bs;
-  pg.d_bytes = d * es;
+  pg.v_off = d * cache->stride[3] * es;
   if (side) {
     pg.side_k = static_cast<char*>(side_k->data);
     pg.side_v = static_cast<char*>(side_v->data);
@@ -145,13 +152,23 @@ int slot_move(const cs_view* cache, const cs_view* side_k, const cs_view* side_v
     pg.side_s_row = side_k->stride[0] * es;
     pg.side_s_head = side_k->stride[1] * es;
   }
-  kv_rows kr{static_cast<char*>(key->data), key->stride[0] * es, key->stride[1] * es};
-  kv_rows vr{static_cast<char*>(value->data), value->stride[0] * es, value->stride[1] * es};
-  int w = pick_width(pg.d_bytes,
-                     {pg.cache, pg.cache + pg.d_bytes, pg.side_k, pg.side_v, kr.base, vr.base},
-                     {pg.s_block, pg.s_head, pg.s_off, pg.side_s_row, pg.side_s_head, kr.s_row,
-                      kr.s_head, vr.s_row, vr.s_head});
-  int64_t chunks = pg.d_bytes / w;
+  kv_rows kr{static_cast<char*>(key->data), key->stride[0] * es, key->stride[1] * es, key->shape[0], 0};
+  kv_rows vr{static_cast<char*>(value->data), value->stride[0] * es, value->stride[1] * es,
+             value->shape[0], 0};
+  const int64_t row_bytes = d * es;
+  int w = es;
+  if (contiguous) {
+    w = pick_width(row_bytes, {pg.cache, pg.cache + pg.v_off, pg.side_k, pg.side_v, kr.base, vr.base},
+                   {pg.s_block, pg.s_head, pg.s_off, pg.side_s_row, pg.side_s_head, kr.s_row,
+                    kr.s_head, vr.s_row, vr.s_head});
+    pg.c_step = pg.side_step = kr.step = vr.step = w;
+  } else {
+    pg.c_step = cache->stride[3] * es;
+    pg.side_step = side ? side_k->stride[2] * es : 0;
+    kr.step = key->stride[2] * es;
+    vr.step = value->stride[2] * es;
+  }
+  int64_t chunks = row_bytes / w;
   int64_t total = n * heads * 2 * chunks;
   const int threads = 256;
   int grid = grid_for(total, threads);

@@ -596,6 +596,15 @@ def cope_attention(
     lowered = None
     if canonical is not None:
         lowered = canonical._lower(device, query_positions, key_positions)
+        if lowered.reason or not lowered.fits(hq):
+            # A profile that does not match the plan is only an error when some
+            # query row is fixed; it is never handed to the kernel.
+            if lowered.any_fixed_row():
+                ck.finish()
+                lowered.raise_lookup_error()
+                raise ValueError("CCPE profile shape does not match the fixed tokens and heads")
+            canonical = None
+    if canonical is not None:
         keep.append(lowered)
         args.canonical = _hip.view(lowered.canonical)
         args.q_ord = ptr(lowered.q_rows)
@@ -645,8 +654,11 @@ def _fast_path_ok(query, key, value, e, cope, amask, visibility_mask, fixed_posi
         return False
     if canonical is not None or selected is not None or return_positions:
         return False
-    if e.dtype != torch.float32 or not e.is_contiguous() or cope.max_positions > 256:
+    if e.dtype != torch.float32 or not e.is_contiguous() or cope.max_positions > 128:
         return False
+    for t in (query, key, value):
+        if t.stride(2) != 1 or t.data_ptr() % 16 or t.stride(0) % 8 or t.stride(1) % 8:
+            return False
     group = query.shape[1] // key.shape[1]
     return group in (1, 2) or group % 4 == 0
 

@@ -34,7 +34,8 @@ def tolerance(dtype: torch.dtype) -> dict:
     if dtype == torch.float64:
         return {"atol": 1e-10, "rtol": 1e-10}
     if dtype == torch.float32:
-        return {"atol": 2e-5, "rtol": 2e-5}
+        # fp32 dot products in a different order, amplified by softmax
+        return {"atol": 1e-4, "rtol": 1e-4}
     return {"atol": BF16_ATOL, "rtol": BF16_RTOL}
 
 

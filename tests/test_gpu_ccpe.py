@@ -480,16 +480,18 @@ def test_mfma_prefill_dense_matches_oracle(device, hq, hkv, n):
     assert_close_bf16(actual, expected)
 
 
-def test_mfma_prefill_large_table_and_sparse_rows(device):
-    # unsorted sparse query rows, P = 256 (4 position tiles), strong table
+@pytest.mark.parametrize("npos", [128, 256])
+def test_prefill_large_table_and_sparse_rows(device, npos):
+    # unsorted sparse query rows and a strong table; P = 128 runs the MFMA kernel
+    # (4 position tiles), P = 256 exceeds its LDS budget and runs the generic kernel
     n, hq, hkv = 900, 4, 1
     q = seeded((n, hq, 128), 31, dtype=torch.bfloat16)
     k = seeded((n, hkv, 128), 32, dtype=torch.bfloat16)
     v = seeded((n, hkv, 128), 33, dtype=torch.bfloat16)
-    e = seeded((128, 256), 34, scale=0.2)
+    e = seeded((128, npos), 34, scale=0.2)
     rows = np.random.default_rng(3).permutation(n)[:300]
     expected = orc.cope_attention(acc_np(q)[rows], acc_np(k), acc_np(v), e.numpy(), rows)
-    cope = cope_on(device, 128, 256, table=e)
+    cope = cope_on(device, 128, npos, table=e)
     actual = cope_attention(q[rows].to(device), k.to(device), v.to(device), cope,
                             torch.from_numpy(rows).to(device))
     assert_close_bf16(actual, expected)
