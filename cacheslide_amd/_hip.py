@@ -94,6 +94,7 @@ class CsKvSource(ctypes.Structure):
         ("num_blocks", ctypes.c_int64),
         ("block_table", ctypes.c_void_p),
         ("bt_stride", ctypes.c_int64),
+        ("bt_cols", ctypes.c_int64),
         ("k", ctypes.c_void_p),
         ("v", ctypes.c_void_p),
         ("k_s_batch", ctypes.c_int64),

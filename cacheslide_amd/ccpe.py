@@ -46,6 +46,7 @@ def _paged_source(cache: Tensor, block_table: Tensor) -> _hip.CsKvSource:
     src.num_blocks = cache.shape[0]
     src.block_table = block_table.data_ptr()
     src.bt_stride = block_table.stride(0)
+    src.bt_cols = block_table.shape[1]
     if block_table.stride(1) != 1:
         raise ValueError("block_table rows must be contiguous")
     return src

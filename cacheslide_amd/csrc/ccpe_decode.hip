@@ -13,10 +13,11 @@
 // the per-split (max, sum, accumulator) triples.
 //
 // Inside a split, each of the 4 wavefronts owns a contiguous quarter of the
-// keys.  Pass 1 streams K (16 lanes x 16 B per key row) and leaves the logits
-// of the whole GQA group in LDS; pass 2 turns them into scores (constant bias,
-// or an exact right-to-left wave scan with the carry), and pass 3 streams V and
-// accumulates P.V.
+// keys.  Speculative splits stream K and V once with an online softmax
+// (decode_spec_kernel).  Exact splits (decode_split_kernel): pass 1 streams K
+// (16 lanes x 16 B per key row) and leaves the logits of the whole GQA group in
+// LDS; pass 2 turns them into scores with an exact right-to-left wave scan from
+// the carry; pass 3 streams V and accumulates P.V.
 
 #include "common.h"
 
@@ -33,10 +34,10 @@ constexpr int kMaxSplit = 1024;
 struct kv_addr {
   const uint16_t* cache;
   int64_t s_block, s_head, s_offset;
-  int32_t block_size;
+  int32_t block_size, bs_shift;  // bs_shift >= 0 when block_size is a power of two
   int64_t num_blocks;
   const int32_t* block_table;
-  int64_t bt_stride;
+  int64_t bt_stride, bt_cols;
   const uint16_t* k;
   const uint16_t* v;
   int64_t k_sb, k_st, k_sh, v_sb, v_st, v_sh;
@@ -62,13 +63,17 @@ struct decode_params {
 __device__ inline const uint16_t* kv_row(const kv_addr& a, int b, int kvh, int64_t j, bool is_v,
                                          bool* bad) {
   if (a.block_table) {
-    int64_t bi = j / a.block_size;
-    int32_t blk = a.block_table[b * a.bt_stride + bi];
+    const int64_t bi = a.bs_shift >= 0 ? (j >> a.bs_shift) : j / a.block_size;
+    if (bi >= a.bt_cols) {
+      *bad = true;
+      return nullptr;
+    }
+    const int32_t blk = a.block_table[b * a.bt_stride + bi];
     if (blk < 0 || blk >= a.num_blocks) {
       *bad = true;
       return nullptr;
     }
-    int64_t off = j % a.block_size;
+    const int64_t off = a.bs_shift >= 0 ? (j & ((int64_t(1) << a.bs_shift) - 1)) : j % a.block_size;
     return a.cache + blk * a.s_block + kvh * a.s_head + off * a.s_offset + (is_v ? kD : 0);
   }
   return is_v ? a.v + b * a.v_sb + j * a.v_st + kvh * a.v_sh
@@ -86,6 +91,205 @@ __device__ inline void unpack8(uint4 u, float* f) {
 
 __device__ inline int64_t ws_index(const decode_params& p, int b, int h, int r) {
   return (static_cast<int64_t>(b) * p.hq + h) * p.smax + r;
+}
+
+// Speculative split r >= 1: every position is assumed saturated (p = P-1), so
+// the bias is the per-head constant QE[P-1] and the split is one streaming pass
+// of plain attention.  Each 16-lane group owns one key at a time (lane x holds
+// dims 8x..8x+7 of its K and V rows) and keeps an online-softmax state per
+// head over the keys it has seen; the 4 lane groups and 4 waves are merged at
+// the end.  The split's gate total is recorded for the fixup pass.
+constexpr int kSpecUnroll = 4;
+
+template <int GT>
+__global__ void __launch_bounds__(kThreads) decode_spec_kernel(decode_params p) {
+  constexpr int kMaxGroup = GT;  // registers sized for this group, not the maximum
+  __shared__ float wave_m[kWaves][kMaxGroup];
+  __shared__ float wave_l[kWaves][kMaxGroup];
+  __shared__ double wave_tot[kWaves][kMaxGroup];
+  __shared__ float wave_o[kWaves][kMaxGroup][kD];
+
+  const int r = blockIdx.x + 1, kvh = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int a4 = lane >> 4, x = lane & 15;
+  constexpr int G = GT;
+  const int nk = p.nk[b];
+  int splits = (nk + p.split - 1) / p.split;
+  if (splits > p.smax) splits = p.smax;
+  if (r >= splits) return;
+  const int64_t hi = static_cast<int64_t>(nk) - static_cast<int64_t>(r) * p.split;
+  const int64_t lo = hi - p.split > 0 ? hi - p.split : 0;
+  const int h0 = kvh * G;
+  const float kLog2e = 1.4426950408889634f;
+  const float c_scale = 0.08838834764831845f * kLog2e;  // log2(e) / sqrt(128)
+
+  // q slice of every head in registers; QE[P-1] by a 16-lane reduction
+  float qr[kMaxGroup][8];
+  float bias2[kMaxGroup];  // QE[P-1] * log2(e)
+#pragma unroll
+  for (int gg = 0; gg < kMaxGroup; ++gg) {
+    if (gg < G) {
+      uint4 u = *reinterpret_cast<const uint4*>(p.q + b * p.q_sb + (h0 + gg) * p.q_sh + 8 * x);
+      unpack8(u, qr[gg]);
+      float part = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) part += qr[gg][i] * p.e[(8 * x + i) * p.npos + (p.npos - 1)];
+      part += __shfl_xor(part, 8, 64);
+      part += __shfl_xor(part, 4, 64);
+      part += __shfl_xor(part, 2, 64);
+      part += __shfl_xor(part, 1, 64);
+      bias2[gg] = part * kLog2e;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) qr[gg][i] = 0.f;
+      bias2[gg] = 0.f;
+    }
+  }
+
+  float m[kMaxGroup], l[kMaxGroup], o[kMaxGroup][8];
+  double tsum[kMaxGroup];
+#pragma unroll
+  for (int gg = 0; gg < kMaxGroup; ++gg) {
+    m[gg] = -INFINITY;
+    l[gg] = 0.f;
+    tsum[gg] = 0.0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[gg][i] = 0.f;
+  }
+
+  const int kw = p.split / kWaves;
+  int64_t wlo = lo + static_cast<int64_t>(wave) * kw;
+  int64_t whi = wlo + kw;
+  if (wlo > hi) wlo = hi;
+  if (whi > hi) whi = hi;
+  bool bad = false;
+  for (int64_t base = wlo; base < whi; base += 4 * kSpecUnroll) {
+    uint4 kb[kSpecUnroll], vb[kSpecUnroll];
+#pragma unroll
+    for (int u = 0; u < kSpecUnroll; ++u) {
+      const int64_t j = base + 4 * u + a4;
+      kb[u] = make_uint4(0, 0, 0, 0);
+      vb[u] = make_uint4(0, 0, 0, 0);
+      if (j < whi) {
+        const uint16_t* kr = kv_row(p.kv, b, kvh, j, false, &bad);
+        if (kr) {
+          kb[u] = *reinterpret_cast<const uint4*>(kr + 8 * x);
+          vb[u] = *reinterpret_cast<const uint4*>(kr + kD + 8 * x);
+        }
+      }
+    }
+    float s[kSpecUnroll][kMaxGroup];
+#pragma unroll
+    for (int u = 0; u < kSpecUnroll; ++u) {
+      float kf[8];
+      unpack8(kb[u], kf);
+#pragma unroll
+      for (int gg = 0; gg < kMaxGroup; ++gg) {
+        float d = 0.f;
+        if (gg < G) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) d += qr[gg][i] * kf[i];
+          d += __shfl_xor(d, 8, 64);
+          d += __shfl_xor(d, 4, 64);
+          d += __shfl_xor(d, 2, 64);
+          d += __shfl_xor(d, 1, 64);
+        }
+        s[u][gg] = d;
+      }
+    }
+#pragma unroll
+    for (int gg = 0; gg < kMaxGroup; ++gg) {
+      if (gg >= G) continue;
+      float xs[kSpecUnroll];
+      float mx = m[gg];
+#pragma unroll
+      for (int u = 0; u < kSpecUnroll; ++u) {
+        const bool in = base + 4 * u + a4 < whi;
+        // natural-log logit for the gate mass, log2-domain score for softmax
+        const float logit = s[u][gg] * 0.08838834764831845f;
+        if (in && x == 0) tsum[gg] += static_cast<double>(1.f / (1.f + __expf(-logit)));
+        xs[u] = in ? s[u][gg] * c_scale + bias2[gg] : -INFINITY;
+        mx = fmaxf(mx, xs[u]);
+      }
+      if (mx == -INFINITY) continue;
+      const float corr = __builtin_amdgcn_exp2f(m[gg] - mx);
+      l[gg] *= corr;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[gg][i] *= corr;
+#pragma unroll
+      for (int u = 0; u < kSpecUnroll; ++u) {
+        const float pw = __builtin_amdgcn_exp2f(xs[u] - mx);
+        l[gg] += pw;
+        float vf[8];
+        unpack8(vb[u], vf);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[gg][i] += pw * vf[i];
+      }
+      m[gg] = mx;
+    }
+  }
+
+  // merge the 4 lane groups of the wave (xor 16, then xor 32)
+#pragma unroll
+  for (int off = 16; off <= 32; off <<= 1) {
+#pragma unroll
+    for (int gg = 0; gg < kMaxGroup; ++gg) {
+      if (gg >= G) continue;
+      const float m2 = __shfl_xor(m[gg], off, 64);
+      const float l2 = __shfl_xor(l[gg], off, 64);
+      const float M = fmaxf(m[gg], m2);
+      const float f1 = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[gg] - M);
+      const float f2 = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m2 - M);
+      l[gg] = l[gg] * f1 + l2 * f2;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float o2 = __shfl_xor(o[gg][i], off, 64);
+        o[gg][i] = o[gg][i] * f1 + o2 * f2;
+      }
+      m[gg] = M;
+      tsum[gg] += __shfl_xor(tsum[gg], off, 64);
+    }
+  }
+  if (a4 == 0) {
+#pragma unroll
+    for (int gg = 0; gg < kMaxGroup; ++gg)
+      if (gg < G)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) wave_o[wave][gg][8 * x + i] = o[gg][i];
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int gg = 0; gg < kMaxGroup; ++gg)
+      if (gg < G) {
+        wave_m[wave][gg] = m[gg];
+        wave_l[wave][gg] = l[gg];
+        wave_tot[wave][gg] = tsum[gg];
+      }
+  }
+  __syncthreads();
+  for (int i = tid; i < G * kD; i += kThreads) {
+    const int gg = i / kD, d = i % kD;
+    float M = -INFINITY;
+    for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, wave_m[ww][gg]);
+    float L = 0.f, O = 0.f;
+    for (int ww = 0; ww < kWaves; ++ww) {
+      const float wm = wave_m[ww][gg];
+      if (wm == -INFINITY) continue;
+      const float f = __builtin_amdgcn_exp2f(wm - M);
+      L += wave_l[ww][gg] * f;
+      O += wave_o[ww][gg][d] * f;
+    }
+    const int64_t wi = ws_index(p, b, h0 + gg, r);
+    p.acc[wi * kD + d] = O;
+    if (d == 0) {
+      p.mx[wi] = M;
+      p.sm[wi] = L;
+      double T = 0.0;
+      for (int ww = 0; ww < kWaves; ++ww) T += wave_tot[ww][gg];
+      p.tot[wi] = T;
+    }
+  }
+  if (bad) atomicOr(p.flags, CS_FLAG_BLOCK_INVALID);
 }
 
 __global__ void __launch_bounds__(kThreads) decode_split_kernel(decode_params p, int fixup) {
@@ -436,6 +640,11 @@ extern "C" int cs_ccpe_decode_bf16(const void* q, int64_t q_s_batch, int64_t q_s
     p.kv.num_blocks = kv->num_blocks;
     p.kv.block_table = kv->block_table;
     p.kv.bt_stride = kv->bt_stride;
+    p.kv.bt_cols = kv->bt_cols;
+    p.kv.bs_shift = -1;
+    for (int s = 0; s < 31; ++s)
+      if ((1 << s) == kv->block_size) p.kv.bs_shift = s;
+    CS_REQUIRE(p.kv.bt_cols > 0, "block table needs at least one column");
   } else {
     CS_REQUIRE(kv->k && kv->v && kv->k_s_tok % 8 == 0 && kv->v_s_tok % 8 == 0 &&
                    kv->k_s_head % 8 == 0 && kv->v_s_head % 8 == 0,
@@ -463,9 +672,23 @@ extern "C" int cs_ccpe_decode_bf16(const void* q, int64_t q_s_batch, int64_t q_s
   p.flags = flags;
   if (batch == 0) return CS_OK;
   hipStream_t s = as_stream(stream);
-  dim3 grid(p.smax, hkv, batch);
-  hipLaunchKernelGGL(decode_split_kernel, grid, dim3(kThreads), 0, s, p, 0);
-  if (p.smax > 1) hipLaunchKernelGGL(decode_split_kernel, grid, dim3(kThreads), 0, s, p, 1);
+  // split 0 exactly; splits >= 1 speculatively; then exact fixups where the
+  // speculation does not hold; then the merge.
+  hipLaunchKernelGGL(decode_split_kernel, dim3(1, hkv, batch), dim3(kThreads), 0, s, p, 0);
+  if (p.smax > 1) {
+    dim3 g(p.smax - 1, hkv, batch);
+    switch (p.group) {
+      case 1: hipLaunchKernelGGL(decode_spec_kernel<1>, g, dim3(kThreads), 0, s, p); break;
+      case 2: hipLaunchKernelGGL(decode_spec_kernel<2>, g, dim3(kThreads), 0, s, p); break;
+      case 3: hipLaunchKernelGGL(decode_spec_kernel<3>, g, dim3(kThreads), 0, s, p); break;
+      case 4: hipLaunchKernelGGL(decode_spec_kernel<4>, g, dim3(kThreads), 0, s, p); break;
+      case 5: hipLaunchKernelGGL(decode_spec_kernel<5>, g, dim3(kThreads), 0, s, p); break;
+      case 6: hipLaunchKernelGGL(decode_spec_kernel<6>, g, dim3(kThreads), 0, s, p); break;
+      case 7: hipLaunchKernelGGL(decode_spec_kernel<7>, g, dim3(kThreads), 0, s, p); break;
+      default: hipLaunchKernelGGL(decode_spec_kernel<8>, g, dim3(kThreads), 0, s, p); break;
+    }
+    hipLaunchKernelGGL(decode_split_kernel, dim3(p.smax, hkv, batch), dim3(kThreads), 0, s, p, 1);
+  }
   hipLaunchKernelGGL(decode_combine_kernel, dim3(batch * hq), dim3(kD), 0, s, p);
   CS_LAUNCH_CHECK("ccpe_decode");
   return CS_OK;

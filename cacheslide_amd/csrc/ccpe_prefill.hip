@@ -1,4 +1,4 @@
-// CCPE prefill attention on bf16 MFMA (gfx950 v_mfma_f32_32x32x16_bf16).
+// CCPE prefill attention on bf16 MFMA (gfx950 v_mfma_f32_16x16x32_bf16).
 //
 // Computes, for every query row r (position qpos[r]) and query head h,
 //   logit_j   = (q . k_j) / sqrt(128)                       position.py:157-164
@@ -10,25 +10,24 @@
 //                                                           position.py:518-550
 // for keys 0..nk-1 (the cope_attention default key_positions = arange).
 //
-// Work decomposition.  A workgroup (4 wavefronts) owns 32 query rows x 4 query
-// heads of one GQA group (or 64/128 rows for group sizes 2/1), so every wave
-// shares the K/V tile staged in LDS.  Key tiles of 64 are walked from the
-// right-most causal key leftwards; each row carries the gate mass of the keys
-// already visited, and once every row of a wave carries >= P-1 the remaining
-// tiles are saturated (p = P-1, bias = QE[P-1]) and the sigmoid / scan / lerp
-// work is skipped.
+// Work decomposition.  A workgroup of 8 wavefronts owns 32 query rows x 4
+// query heads of one GQA group (64 x 2 or 128 x 1 for group sizes 2 and 1);
+// each wave owns 16 (row, head) pairs and all 8 waves share the K / V^T tile
+// staged in LDS.  Key tiles of 64 are walked from the right-most causal key
+// leftwards; each row carries the gate mass of the keys already visited, and
+// once every row of a wave carries >= P-1 its remaining tiles are saturated
+// (p = P-1, bias = QE[P-1]) and the sigmoid / scan / lerp work is skipped.
 //
-// MFMA data layout (32x32x16 bf16, lane l, g = l / 32):
-//   A[m][k]: lane holds row m = l % 32, k = 8g .. 8g+7
-//   B[k][n]: lane holds col n = l % 32, k = 8g .. 8g+7
-//   C[m][n]: lane holds col n = l % 32, value v -> row 8(v/4) + 4g + (v%4)
-// S^T = K Q^T puts the query row on the lane (n) and keys on the registers, so
-// the online-softmax statistics are per-lane scalars.  K rows are fed to the A
-// operand through the permutation pi(m) that swaps bits 2 and 3 of m; then C
-// register v of lane group g holds physical key 16(v/8) + 8g + (v%8), i.e. every
-// lane holds runs of 8 consecutive keys, which is exactly the B-operand layout
-// P^T needs for O^T = V^T P^T (keys 8g..8g+7 of each 16-key k-step).  V^T is
-// staged transposed in LDS so its A operand is one 16-byte read per lane.
+// MFMA data layout (16x16x32 bf16, lane l, g = l / 16, n = l % 16):
+//   A[m][k]: lane holds row m = n, k = 8g .. 8g+7
+//   B[k][n]: lane holds col n,     k = 8g .. 8g+7
+//   C[m][n]: lane holds col n,     rows 4g .. 4g+3
+// S^T = K Q^T puts the query row on the lane (n) and keys on the registers:
+// lane group g of M-tile mt holds keys 16 mt + 4g .. +3, so the online-softmax
+// statistics are per-lane scalars shared by the 4 lanes n, n+16, n+32, n+48.
+// For O^T = V^T P^T the 32 keys of a k-step are ordered so that lane group g
+// supplies the 8 S^T values it already holds (keys 32t + 4g + 0..3 and
+// 32t + 16 + 4g + 0..3); V^T, staged transposed in LDS, is read in that order.
 
 #include "common.h"
 
@@ -36,28 +35,29 @@ namespace cs {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float floatx16 __attribute__((ext_vector_type(16)));
-typedef unsigned short ushort8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kD = 128;          // head dim (K and V)
 constexpr int kTileN = 64;       // keys per tile
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
+constexpr int kRows = 16;              // (row, head) pairs per wave
 constexpr int kKStride = kD + 8;       // bf16 per K row in LDS (272 B)
 constexpr int kVStride = kTileN + 8;   // bf16 per V^T row in LDS (144 B)
 // The per-wave QE tables live in LDS next to the K / V^T tiles; P <= 128 keeps
-// the workgroup at <= 101 KB, under the 160 KB a gfx950 workgroup may use.
+// the workgroup at <= 102 KB, under the 160 KB a gfx950 workgroup may use.
 constexpr int kMaxPos = 128;
-constexpr size_t kStaticLds = sizeof(uint16_t) * (kTileN * kKStride + kD * kVStride) + 16;
+constexpr size_t kStaticLds = sizeof(uint16_t) * (kTileN * kKStride + kD * kVStride) + 32;
 constexpr size_t kLdsLimit = 160 * 1024;
 
 struct kv_addr {
   const uint16_t* cache;
   int64_t s_block, s_head, s_offset;
-  int32_t block_size;
+  int32_t block_size, bs_shift;  // bs_shift >= 0 when block_size is a power of two
   int64_t num_blocks;
   const int32_t* block_table;
-  int64_t bt_stride;
+  int64_t bt_stride, bt_cols;
   const uint16_t* k;
   const uint16_t* v;
   int64_t k_sb, k_st, k_sh, v_sb, v_st, v_sh;
@@ -68,7 +68,7 @@ struct prefill_params {
   int64_t q_sb, q_st, q_sh;
   const int64_t* qpos;
   int64_t qpos_sb;
-  int32_t batch, nq, hq, hkv, group, heads_per_wg, rows_per_wave_group, row_blocks;
+  int32_t batch, nq, hq, hkv, group, heads_per_wg, row_blocks;
   const int32_t* nk;
   kv_addr kv;
   const float* e;
@@ -78,45 +78,21 @@ struct prefill_params {
   int32_t total_wg;
 };
 
-// Row pointer of K (or V when is_v) for key j of batch b, kv head kvh, or null.
-__device__ inline const uint16_t* kv_row(const kv_addr& a, int b, int kvh, int64_t j, bool is_v,
-                                         bool* bad) {
-  if (a.block_table) {
-    int64_t bi = j / a.block_size;
-    int32_t blk = a.block_table[b * a.bt_stride + bi];
-    if (blk < 0 || blk >= a.num_blocks) {
-      *bad = true;
-      return nullptr;
-    }
-    int64_t off = j % a.block_size;
-    return a.cache + blk * a.s_block + kvh * a.s_head + off * a.s_offset + (is_v ? kD : 0);
-  }
-  return is_v ? a.v + b * a.v_sb + j * a.v_st + kvh * a.v_sh
-              : a.k + b * a.k_sb + j * a.k_st + kvh * a.k_sh;
-}
-
 __device__ inline bf16x8 as_bf16x8(uint4 u) {
   bf16x8 r;
   __builtin_memcpy(&r, &u, 16);
   return r;
 }
 
-__device__ inline uint32_t pack_bf16x2(float lo, float hi) {
-  return static_cast<uint32_t>(float_to_bf16(lo)) | (static_cast<uint32_t>(float_to_bf16(hi)) << 16);
-}
-
-// Map a flat workgroup id to (batch, kv head, head group, row block), spreading
-// contiguous logical ranges over the 8 XCDs (dispatch is round-robin by id) so
-// that one (batch, kv head)'s K/V stays in one XCD's L2, and visiting the
-// heaviest (right-most) row blocks first.
+// Flat workgroup id -> (batch, kv head, head group, row block).  Dispatch is
+// round-robin over the 8 XCDs by id, so contiguous logical ranges are spread as
+// one per XCD: a (batch, kv head)'s K/V stays in one XCD's L2.  The heaviest
+// (right-most) row blocks go first.
 __device__ inline void decode_wg(const prefill_params& p, int& b, int& kvh, int& hg, int& rb) {
-  int id = blockIdx.x;
+  const int id = blockIdx.x;
   int logical = id;
-  if (p.total_wg % 8 == 0) {
-    int per = p.total_wg / 8;
-    logical = (id % 8) * per + id / 8;
-  }
-  int hgroups = p.group / p.heads_per_wg;
+  if (p.total_wg % 8 == 0) logical = (id % 8) * (p.total_wg / 8) + id / 8;
+  const int hgroups = p.group / p.heads_per_wg;
   rb = p.row_blocks - 1 - (logical % p.row_blocks);
   int rest = logical / p.row_blocks;
   hg = rest % hgroups;
@@ -128,139 +104,156 @@ __device__ inline void decode_wg(const prefill_params& p, int& b, int& kvh, int&
 __global__ void __launch_bounds__(kThreads, 2) ccpe_prefill_kernel(prefill_params p) {
   __shared__ __align__(16) uint16_t k_lds[kTileN * kKStride];
   __shared__ __align__(16) uint16_t v_lds[kD * kVStride];
-  extern __shared__ __align__(16) float tab_lds[];  // [kWaves][32][tab_stride]
+  __shared__ int64_t wg_max_pos;
+  extern __shared__ __align__(16) float tab_lds[];  // [kWaves][16][tab_stride]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int g = lane >> 5;   // lane group
-  const int ln = lane & 31;  // row within the wave
+  const int g = lane >> 4;   // lane group: keys 4g..4g+3 of each 16-key M-tile
+  const int ln = lane & 15;  // this lane's (row, head) pair within the wave
 
   int b, kvh, hg, rb;
   decode_wg(p, b, kvh, hg, rb);
   const int head_slot = wave % p.heads_per_wg;
   const int row_sub = wave / p.heads_per_wg;
   const int h = kvh * p.group + hg * p.heads_per_wg + head_slot;
-  const int wg_rows = 32 * (kWaves / p.heads_per_wg);
-  const int row0 = rb * wg_rows;
-  const int r = row0 + row_sub * 32 + ln;  // this lane's query row
+  const int wg_rows = kRows * (kWaves / p.heads_per_wg);
+  const int r = rb * wg_rows + row_sub * kRows + ln;
   const bool row_ok = r < p.nq;
   const int nk = p.nk[b];
   const int64_t qp = row_ok ? p.qpos[b * p.qpos_sb + r] : -1;
 
-  // Right-most key of the workgroup: max causal key over its rows.
-  __shared__ int64_t wg_max_pos;
   if (tid == 0) wg_max_pos = 0;
   __syncthreads();
-  {
-    int64_t m = qp;
-    for (int off = 32; off > 0; off >>= 1) {
-      int64_t o = __shfl_xor(m, off, 64);
-      m = o > m ? o : m;
-    }
-    if (lane == 0) atomicMax(reinterpret_cast<unsigned long long*>(&wg_max_pos),
-                             static_cast<unsigned long long>(m < 0 ? 0 : m));
+  // wave extremes of the query positions (for the key range and masking)
+  int64_t wmax = qp, wmin = row_ok ? qp : INT64_MAX;
+  for (int off = 32; off > 0; off >>= 1) {
+    const int64_t a = __shfl_xor(wmax, off, 64);
+    const int64_t c = __shfl_xor(wmin, off, 64);
+    wmax = a > wmax ? a : wmax;
+    wmin = c < wmin ? c : wmin;
   }
+  if (lane == 0)
+    atomicMax(reinterpret_cast<unsigned long long*>(&wg_max_pos),
+              static_cast<unsigned long long>(wmax < 0 ? 0 : wmax));
   __syncthreads();
   const int64_t kend = (wg_max_pos + 1) < nk ? (wg_max_pos + 1) : nk;  // keys [0, kend)
 
-  // ---- Q as the B operand of S^T (8 k-steps x 8 bf16) -----------------
-  bf16x8 qreg[8];
+  // ---- Q as the B operand of S^T: 4 k-steps x 8 bf16 ------------------------
+  bf16x8 qreg[4];
   {
     const uint16_t* qrow = p.q + b * p.q_sb + static_cast<int64_t>(row_ok ? r : 0) * p.q_st + h * p.q_sh;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      uint4 u = row_ok ? *reinterpret_cast<const uint4*>(qrow + 16 * s + 8 * g) : make_uint4(0, 0, 0, 0);
+    for (int s = 0; s < 4; ++s) {
+      const uint4 u = row_ok ? *reinterpret_cast<const uint4*>(qrow + 32 * s + 8 * g)
+                             : make_uint4(0, 0, 0, 0);
       qreg[s] = as_bf16x8(u);
     }
   }
 
-  // ---- QE table: QE^T = E^T Q^T with E split into bf16 hi + lo ---------
-  float* tab = tab_lds + wave * 32 * p.tab_stride;
+  // ---- QE table: QE^T = E^T Q^T, E split into bf16 hi + lo (~fp32 product) ----
+  float* tab = tab_lds + wave * kRows * p.tab_stride;
   for (int pt = 0; pt < p.pos_tiles; ++pt) {
-    floatx16 acc = {};
-    const int pos = pt * 32 + ln;
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+    const int pos = pt * 16 + ln;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      ushort8 hi8, lo8;
+    for (int s = 0; s < 4; ++s) {
+      bf16x8 ahi, alo;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        float ev = pos < p.npos ? p.e[(16 * s + 8 * g + i) * p.npos + pos] : 0.f;
-        uint16_t hb = float_to_bf16(ev);
-        float rem = ev - bf16_to_float(hb);
-        hi8[i] = hb;
-        lo8[i] = float_to_bf16(rem);
+        const float ev = pos < p.npos ? p.e[(32 * s + 8 * g + i) * p.npos + pos] : 0.f;
+        const __bf16 hb = static_cast<__bf16>(ev);
+        ahi[i] = hb;
+        alo[i] = static_cast<__bf16>(ev - static_cast<float>(hb));
       }
-      bf16x8 ahi, alo;
-      __builtin_memcpy(&ahi, &hi8, 16);
-      __builtin_memcpy(&alo, &lo8, 16);
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ahi, qreg[s], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(alo, qreg[s], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ahi, qreg[s], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(alo, qreg[s], acc, 0, 0, 0);
     }
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      int posv = pt * 32 + 8 * (v / 4) + 4 * g + (v % 4);
+    for (int v = 0; v < 4; ++v) {
+      const int posv = pt * 16 + 4 * g + v;
       if (posv < p.npos) tab[ln * p.tab_stride + posv] = acc[v];
     }
   }
   __syncthreads();
-  const float qe_last = tab[ln * p.tab_stride + (p.npos - 1)];
+  const float* trow = tab + ln * p.tab_stride;
   const float top = static_cast<float>(p.npos - 1);
-
-  // ---- main loop --------------------------------------------------------
   const float kLog2e = 1.4426950408889634f;
   const float logit_scale = 0.08838834764831845f;  // 1/sqrt(128)
+  const float sat_bias2 = trow[p.npos - 1] * kLog2e;
+
+  // ---- main loop --------------------------------------------------------------
   float carry = row_ok ? 0.f : 3.0e38f;  // padded rows count as saturated
-  float m_run = -INFINITY;                // running max (log2 domain)
+  float m_run = -INFINITY;                // running max (log2 domain), per row
   float l_run = 0.f;                      // this lane's share of the row sum
-  floatx16 o[4];
+  floatx4 o[8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) o[i] = floatx16{};
+  for (int i = 0; i < 8; ++i) o[i] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  // K rows for the A operand: lane loads key pi(ln) of each 32-key M-tile.
-  const int pim = ((ln >> 4) << 4) | (((ln >> 2) & 1) << 3) | (((ln >> 3) & 1) << 2) | (ln & 3);
-
-  // Global->register staging (prefetch of the next tile).
-  uint4 kst[4], vst[4];
+  // Global -> register staging: threads [0, 256) stage K (4 x 16 B), threads
+  // [256, 512) stage V as 4 keys x 8 dims for the transposed store.
+  uint4 st[4];
   bool bad_block = false;
+  const bool k_stager = tid < 256;
+  const int sid = tid & 255;
+  // key (within a tile) and 16-byte chunk of this thread's staging slot rr
+  auto slot_key = [&](int rr) { return k_stager ? ((sid + 256 * rr) >> 4) : 4 * (sid >> 4) + rr; };
+  const int slot_dc = k_stager ? (sid & 15) : (sid & 15);
+  // Block ids of the next tile to load are fetched one tile earlier, so each
+  // iteration issues only the K/V loads (one global round trip, overlapped
+  // with the current tile's compute).
+  int32_t bid[4] = {0, 0, 0, 0};
+  auto fetch_blocks = [&](int64_t base) {
+    if (!p.kv.block_table) return;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int64_t j = base + slot_key(rr);
+      bid[rr] = -1;
+      if (j < kend) {
+        const int64_t bi = p.kv.bs_shift >= 0 ? (j >> p.kv.bs_shift) : j / p.kv.block_size;
+        if (bi < p.kv.bt_cols) bid[rr] = p.kv.block_table[b * p.kv.bt_stride + bi];
+      }
+    }
+  };
   auto load_tile = [&](int64_t base) {
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
-      int c = tid + kThreads * rr;
-      int key = c >> 4, dc = c & 15;
-      int64_t j = base + key;
-      kst[rr] = make_uint4(0, 0, 0, 0);
+      const int64_t j = base + slot_key(rr);
+      st[rr] = make_uint4(0, 0, 0, 0);
       if (j < kend) {
-        const uint16_t* kr = kv_row(p.kv, b, kvh, j, false, &bad_block);
-        if (kr) kst[rr] = *reinterpret_cast<const uint4*>(kr + 8 * dc);
-      }
-    }
-    {
-      int dc = tid & 15, kg = tid >> 4;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        int64_t j = base + 4 * kg + i;
-        vst[i] = make_uint4(0, 0, 0, 0);
-        if (j < kend) {
-          const uint16_t* vr = kv_row(p.kv, b, kvh, j, true, &bad_block);
-          if (vr) vst[i] = *reinterpret_cast<const uint4*>(vr + 8 * dc);
+        const uint16_t* row = nullptr;
+        if (p.kv.block_table) {
+          const int32_t blk = bid[rr];
+          if (blk < 0 || blk >= p.kv.num_blocks) {
+            bad_block = true;
+          } else {
+            const int64_t off = p.kv.bs_shift >= 0 ? (j & ((int64_t(1) << p.kv.bs_shift) - 1))
+                                                   : j % p.kv.block_size;
+            row = p.kv.cache + blk * p.kv.s_block + kvh * p.kv.s_head + off * p.kv.s_offset +
+                  (k_stager ? 0 : kD);
+          }
+        } else {
+          row = k_stager ? p.kv.k + b * p.kv.k_sb + j * p.kv.k_st + kvh * p.kv.k_sh
+                         : p.kv.v + b * p.kv.v_sb + j * p.kv.v_st + kvh * p.kv.v_sh;
         }
+        if (row) st[rr] = *reinterpret_cast<const uint4*>(row + 8 * slot_dc);
       }
     }
   };
   auto store_tile = [&]() {
+    if (k_stager) {
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      int c = tid + kThreads * rr;
-      int key = c >> 4, dc = c & 15;
-      *reinterpret_cast<uint4*>(&k_lds[key * kKStride + 8 * dc]) = kst[rr];
-    }
-    {
-      int dc = tid & 15, kg = tid >> 4;
-      const uint16_t* e0 = reinterpret_cast<const uint16_t*>(&vst[0]);
-      const uint16_t* e1 = reinterpret_cast<const uint16_t*>(&vst[1]);
-      const uint16_t* e2 = reinterpret_cast<const uint16_t*>(&vst[2]);
-      const uint16_t* e3 = reinterpret_cast<const uint16_t*>(&vst[3]);
+      for (int rr = 0; rr < 4; ++rr) {
+        const int c = sid + 256 * rr;
+        *reinterpret_cast<uint4*>(&k_lds[(c >> 4) * kKStride + 8 * (c & 15)]) = st[rr];
+      }
+    } else {
+      const int dc = sid & 15, kg = sid >> 4;
+      const uint16_t* e0 = reinterpret_cast<const uint16_t*>(&st[0]);
+      const uint16_t* e1 = reinterpret_cast<const uint16_t*>(&st[1]);
+      const uint16_t* e2 = reinterpret_cast<const uint16_t*>(&st[2]);
+      const uint16_t* e3 = reinterpret_cast<const uint16_t*>(&st[3]);
 #pragma unroll
       for (int d = 0; d < 8; ++d) {
         uint2 w;
@@ -272,165 +265,163 @@ __global__ void __launch_bounds__(kThreads, 2) ccpe_prefill_kernel(prefill_param
   };
 
   const int64_t ntiles = (kend + kTileN - 1) / kTileN;
-  if (ntiles > 0) load_tile((ntiles - 1) * kTileN);
+  if (ntiles > 0) {
+    fetch_blocks((ntiles - 1) * kTileN);
+    load_tile((ntiles - 1) * kTileN);
+    if (ntiles > 1) fetch_blocks((ntiles - 2) * kTileN);
+  }
   for (int64_t t = ntiles - 1; t >= 0; --t) {
     const int64_t base = t * kTileN;
     __syncthreads();
     store_tile();
     __syncthreads();
     if (t > 0) load_tile((t - 1) * kTileN);
+    if (t > 1) fetch_blocks((t - 2) * kTileN);
 
-    // S^T for the two 32-key halves of the tile.
-    floatx16 sacc[2];
+    // Waves whose rows all precede the tile contribute nothing to it.
+    if (base > wmax) continue;
+
+    // S^T for the four 16-key M-tiles: sacc[mt][v] = key 16 mt + 4g + v.
+    floatx4 sacc[4];
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      sacc[mt] = floatx16{};
-      const uint16_t* krow = &k_lds[(32 * mt + pim) * kKStride + 8 * g];
+    for (int mt = 0; mt < 4; ++mt) {
+      sacc[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+      const uint16_t* krow = &k_lds[(16 * mt + ln) * kKStride + 8 * g];
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4*>(krow + 16 * s));
-        sacc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[s], sacc[mt], 0, 0, 0);
+      for (int s = 0; s < 4; ++s) {
+        const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4*>(krow + 32 * s));
+        sacc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qreg[s], sacc[mt], 0, 0, 0);
       }
     }
 
-    // Causal masking is needed unless every key of the tile is <= every row.
-    const bool wave_sat = __all(carry >= top);
-    const int64_t tile_last = base + kTileN - 1;
-    // Logits (log2 domain) with masked keys at -inf; keys of run (mt, v/8).
-    float x[2][16];
-    bool any_masked = false;
+    // Masking is needed only when some key of the tile is past some row's
+    // position (or past kend).
+    const bool need_mask = (base + kTileN - 1 > wmin) || (base + kTileN > kend);
+    if (need_mask) {
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+      for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        int64_t j = base + 32 * mt + 16 * (v / 8) + 8 * g + (v % 8);
-        bool ok = row_ok && j <= qp && j < kend;
-        any_masked |= !ok;
-        x[mt][v] = ok ? sacc[mt][v] * logit_scale : -INFINITY;
-      }
-    (void)tile_last;
-
-    if (wave_sat) {
-      const float bl = qe_last;
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) x[mt][v] = (x[mt][v] + bl) * kLog2e;
-    } else {
-      // gates and in-run suffix sums (runs of 8 keys, right to left)
-      float gsuf[2][16];
-      float run_tot[4];
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int rb2 = 0; rb2 < 2; ++rb2) {
-          float acc = 0.f;
-#pragma unroll
-          for (int i = 7; i >= 0; --i) {
-            int v = 8 * rb2 + i;
-            float xv = x[mt][v];
-            float gate = xv == -INFINITY ? 0.f : 1.f / (1.f + __expf(-xv));
-            acc += gate;
-            gsuf[mt][v] = acc;
-          }
-          run_tot[2 * mt + rb2] = acc;
+        for (int v = 0; v < 4; ++v) {
+          const int64_t j = base + 16 * mt + 4 * g + v;
+          if (!(j <= qp && j < kend)) sacc[mt][v] = -INFINITY;
         }
-      // Run R = 4mt + 2rb2 + g in physical key order; the partner lane (g^1)
-      // holds the other parity.  Exclusive suffix over runs.
-      float other[4];
+    }
+
+    if (__all(carry >= top)) {
+      // saturated: bias = QE[P-1]; score (log2 domain) = logit*scale*log2e + const
 #pragma unroll
-      for (int i = 0; i < 4; ++i) other[i] = __shfl_xor(run_tot[i], 32, 64);
-      float tot[8];
+      for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        tot[2 * i + g] = run_tot[i];
-        tot[2 * i + (1 - g)] = other[i];
+        for (int v = 0; v < 4; ++v) sacc[mt][v] = sacc[mt][v] * (logit_scale * kLog2e) + sat_bias2;
+    } else {
+      // gates, in-run suffix sums (runs of 4 keys), cross-lane suffix over runs
+      float suf[4][4];
+      float run[4];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        float acc = 0.f;
+#pragma unroll
+        for (int v = 3; v >= 0; --v) {
+          const float xv = sacc[mt][v] * logit_scale;
+          const float gate = sacc[mt][v] == -INFINITY ? 0.f : 1.f / (1.f + __expf(-xv));
+          acc += gate;
+          suf[mt][v] = acc;
+        }
+        run[mt] = acc;
       }
-      float excl[8];
-      float accr = 0.f;
+      // inclusive suffix over the 4 lane groups (g ascending = keys ascending)
+      float incl[4], mt_total[4];
 #pragma unroll
-      for (int R = 7; R >= 0; --R) {
-        excl[R] = accr;
-        accr += tot[R];
+      for (int mt = 0; mt < 4; ++mt) {
+        float s1 = run[mt];
+        float n1 = __shfl_down(s1, 16, 64);
+        if (g < 3) s1 += n1;
+        float n2 = __shfl_down(s1, 32, 64);
+        if (g < 2) s1 += n2;
+        incl[mt] = s1;
+        mt_total[mt] = __shfl(s1, ln, 64);  // lane group 0 holds the M-tile total
       }
-      const float* trow = tab + ln * p.tab_stride;
+      float right = 0.f;  // gate mass of the M-tiles to the right of mt
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+      for (int mt = 3; mt >= 0; --mt) {
+        const float before = carry + right + (incl[mt] - run[mt]);
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          int R = 4 * mt + 2 * (v / 8) + g;
-          float pos = carry + excl[R] + gsuf[mt][v];
+        for (int v = 0; v < 4; ++v) {
+          float pos = before + suf[mt][v];
           pos = pos < top ? pos : top;
           pos = pos > 0.f ? pos : 0.f;  // also maps NaN to 0: table reads stay in range
-          float fl = floorf(pos);
-          int lo = static_cast<int>(fl);
-          int hi = lo + 1 < p.npos - 1 ? lo + 1 : p.npos - 1;
-          float lo_b = trow[lo];
-          float hi_b = trow[hi];
-          float bias = lo_b + (pos - fl) * (hi_b - lo_b);
-          x[mt][v] = (x[mt][v] + bias) * kLog2e;
+          const float fl = floorf(pos);
+          const int lo = static_cast<int>(fl);
+          const int hi = lo + 1 < p.npos - 1 ? lo + 1 : p.npos - 1;
+          const float lo_b = trow[lo];
+          const float bias = lo_b + (pos - fl) * (trow[hi] - lo_b);
+          sacc[mt][v] = (sacc[mt][v] * logit_scale + bias) * kLog2e;
         }
-      carry += accr;
+        right += mt_total[mt];
+      }
+      carry += right;
     }
-    (void)any_masked;
 
-    // Online softmax (per lane = per query row, partner lane shares the row).
+    // Online softmax: row max over the 16 values and the 4 lanes of the row.
     float tmax = -INFINITY;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+    for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) tmax = fmaxf(tmax, x[mt][v]);
+      for (int v = 0; v < 4; ++v) tmax = fmaxf(tmax, sacc[mt][v]);
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
     const float m_new = fmaxf(m_run, tmax);
-    const float corr = (m_new == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
-    float psum = 0.f;
-    bf16x8 pb[4];
+    const bool live = m_new != -INFINITY;
+    if (__any(m_new != m_run)) {
+      const float corr = (live && m_run != -INFINITY) ? __builtin_amdgcn_exp2f(m_run - m_new) : (live ? 0.f : 1.f);
+      l_run *= corr;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+      for (int dt = 0; dt < 8; ++dt) o[dt] *= corr;
+    }
+    m_run = m_new;
+    float psum = 0.f;
+    bf16x8 pb[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
-        ushort8 packed;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          float xv = x[mt][8 * half + i];
-          float pv = (m_new == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(xv - m_new);
+        for (int v = 0; v < 4; ++v) {
+          const float pv = live ? __builtin_amdgcn_exp2f(sacc[2 * kt + half][v] - m_new) : 0.f;
           psum += pv;
-          packed[i] = float_to_bf16(pv);
+          pb[kt][4 * half + v] = static_cast<__bf16>(pv);
         }
-        __builtin_memcpy(&pb[2 * mt + half], &packed, 16);
       }
-    l_run = l_run * corr + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) o[dt] *= corr;
+    }
+    l_run += psum;
 
-    // O^T += V^T P^T
+    // O^T += V^T P^T: A = V^T rows (dims), keys in the k-step order above.
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-      const uint16_t* vrow = &v_lds[(32 * dt + ln) * kVStride + 8 * g];
+    for (int dt = 0; dt < 8; ++dt) {
+      const uint16_t* vrow = &v_lds[(16 * dt + ln) * kVStride + 4 * g];
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4*>(vrow + 16 * ks));
-        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[ks], o[dt], 0, 0, 0);
+      for (int kt = 0; kt < 2; ++kt) {
+        const uint2 lo4 = *reinterpret_cast<const uint2*>(vrow + 32 * kt);
+        const uint2 hi4 = *reinterpret_cast<const uint2*>(vrow + 32 * kt + 16);
+        const uint4 u = make_uint4(lo4.x, lo4.y, hi4.x, hi4.y);
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(u), pb[kt], o[dt], 0, 0, 0);
       }
     }
   }
 
-  // ---- epilogue ---------------------------------------------------------
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  // ---- epilogue: O^T lane holds row ln, dims 16 dt + 4g + v ------------------
+  float l_tot = l_run + __shfl_xor(l_run, 16, 64);
+  l_tot += __shfl_xor(l_tot, 32, 64);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   if (row_ok) {
     uint16_t* orow = p.out + ((static_cast<int64_t>(b) * p.nq + r) * p.hq + h) * kD;
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+    for (int dt = 0; dt < 8; ++dt) {
+      bf16x4 w;
 #pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        int dim = 32 * dt + 8 * q4 + 4 * g;
-        uint2 w;
-        w.x = pack_bf16x2(o[dt][4 * q4 + 0] * inv, o[dt][4 * q4 + 1] * inv);
-        w.y = pack_bf16x2(o[dt][4 * q4 + 2] * inv, o[dt][4 * q4 + 3] * inv);
-        *reinterpret_cast<uint2*>(orow + dim) = w;
-      }
+      for (int v = 0; v < 4; ++v) w[v] = static_cast<__bf16>(o[dt][v] * inv);
+      *reinterpret_cast<bf16x4*>(orow + 16 * dt + 4 * g) = w;
+    }
   }
   if (bad_block) atomicOr(p.flags, CS_FLAG_BLOCK_INVALID);
 }
@@ -454,9 +445,14 @@ int fill_kv(const cs_kv_source* kv, cs::kv_addr* a) {
     r.s_head = kv->s_head;
     r.s_offset = kv->s_offset;
     r.block_size = kv->block_size;
+    r.bs_shift = -1;
+    for (int s = 0; s < 31; ++s)
+      if ((1 << s) == kv->block_size) r.bs_shift = s;
     r.num_blocks = kv->num_blocks;
     r.block_table = kv->block_table;
     r.bt_stride = kv->bt_stride;
+    r.bt_cols = kv->bt_cols;
+    CS_REQUIRE(r.bt_cols > 0, "block table needs at least one column");
   } else {
     CS_REQUIRE(kv->k && kv->v, "dense kv needs k and v");
     CS_REQUIRE(kv->k_s_tok % 8 == 0 && kv->k_s_head % 8 == 0 && kv->v_s_tok % 8 == 0 &&
@@ -516,19 +512,19 @@ extern "C" int cs_ccpe_prefill_bf16(const void* q, int64_t q_s_batch, int64_t q_
   p.hkv = hkv;
   p.group = group;
   p.heads_per_wg = heads_per_wg;
-  const int wg_rows = 32 * (kWaves / heads_per_wg);
+  const int wg_rows = kRows * (kWaves / heads_per_wg);
   p.row_blocks = static_cast<int32_t>(ceil_div(nq, wg_rows));
   p.nk = nk;
   p.e = e;
   p.npos = max_positions;
-  p.pos_tiles = (max_positions + 31) / 32;
-  p.tab_stride = p.pos_tiles * 32 + 1;
+  p.pos_tiles = (max_positions + 15) / 16;
+  p.tab_stride = p.pos_tiles * 16 + 1;
   p.out = static_cast<uint16_t*>(out);
   p.flags = flags;
   int64_t total = static_cast<int64_t>(batch) * hkv * (group / heads_per_wg) * p.row_blocks;
   CS_REQUIRE(total < (1ll << 31), "grid too large");
   p.total_wg = static_cast<int32_t>(total);
-  size_t smem = sizeof(float) * kWaves * 32 * p.tab_stride;
+  size_t smem = sizeof(float) * kWaves * kRows * p.tab_stride;
   if (smem + kStaticLds > kLdsLimit) {
     set_error("prefill LDS %zu bytes exceeds the workgroup limit", smem + kStaticLds);
     return CS_EUNSUPPORTED;

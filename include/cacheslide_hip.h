@@ -194,6 +194,7 @@ typedef struct cs_kv_source {
   int64_t num_blocks;
   const int32_t* block_table; /* [B, max_blocks] */
   int64_t bt_stride;          /* elements between rows of block_table */
+  int64_t bt_cols;            /* max_blocks: keys beyond it flag CS_FLAG_BLOCK_INVALID */
   /* dense form (block_table == NULL): k,v [B][nk, Hkv, 128] */
   const void* k;
   const void* v;
