@@ -228,8 +228,23 @@ def decode_measure(device, steps: int, warmup: int):
     }
 
 
+def copy_calibration(device, nbytes: int, steps: int) -> dict:
+    """A plain device copy of a known size, for scaling HBM counters
+    (FETCH_SIZE / WRITE_SIZE) read under rocprofv3 --pmc."""
+    import torch
+
+    n = nbytes // 2
+    src = torch.ones(n, dtype=torch.bfloat16, device=device)
+    dst = torch.empty_like(src)
+    ms = time_steps(lambda: dst.copy_(src), steps, 2)
+    return {"copy_bytes_read": n * 2, "copy_bytes_written": n * 2, "ms_per_copy": round(ms, 4),
+            "GBs": round(2 * n * 2 / (ms * 1e-3) / 1e9, 1)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="only time a plain device copy of BYTES (counter calibration)")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
@@ -244,6 +259,9 @@ def main() -> int:
     import torch
 
     device = torch.device("cuda", 0)
+    if args.copy_calibration:
+        print(json.dumps(copy_calibration(device, args.copy_calibration, args.steps)), flush=True)
+        return 0
     inputs, shape, host = build_prefill(device)
     step = prefill_launcher(inputs, shape, device)
     ms = time_steps(step, args.steps, args.warmup)
