@@ -7,22 +7,35 @@
 // right-most split always holds S keys.  Split 0 is computed exactly (carry 0).
 // Every other split assumes that the gate mass of the keys to its right is
 // already >= P-1, which makes every position in it P-1 and the bias the row
-// constant QE[P-1]; it records its own gate total.  A fixup launch then forms
-// each split's true carry (sum of the totals to its right) and recomputes
-// exactly only the splits whose carry is below P-1.  A combine launch merges
-// the per-split (max, sum, accumulator) triples.
+// constant QE[P-1]; it records its own gate total.  A plan launch forms each
+// split's true carry (sum of the totals to its right) and queues the splits
+// whose carry is below P-1; a fixup launch recomputes exactly the queued
+// splits; a combine launch merges the per-split (max, sum, accumulator)
+// triples.  Split 0 and the speculative splits share one launch, split 0's
+// workgroups first.
 //
-// Inside a split, each of the 4 wavefronts owns a contiguous quarter of the
-// keys.  Speculative splits stream K and V once with an online softmax
-// (decode_spec_kernel).  Exact splits (decode_split_kernel): pass 1 streams K
-// (16 lanes x 16 B per key row) and leaves the logits of the whole GQA group in
-// LDS; pass 2 turns them into scores with an exact right-to-left wave scan from
-// the carry; pass 3 streams V and accumulates P.V.
+// Inside a split each of the 4 wavefronts owns a contiguous quarter of the
+// keys and walks it in tiles of 16 keys from the right.  Per tile:
+//   S^T = K Q^T on v_mfma_f32_16x16x32_bf16 (keys on M, the GQA heads on N):
+//     A: lane (g, n) holds key n, dims 32t + 8g .. +7 (t = 0..3)
+//     B: lane (g, n) holds head n, the same dims (heads >= group are zero)
+//     C: lane (g, n) holds head n, keys 4g .. 4g+3 of the tile
+//   so lane (g, n) keeps an online softmax for head n over the keys of row g.
+//   P.V runs on the VALU with packed v_dot2c_f32_bf16: lane (g, x) holds V of
+//   keys 4g .. 4g+3, dims 8x .. 8x+7, and the probabilities of head h reach it
+//   from lane (g, h) through a DPP row broadcast.
+// The next tile's K/V loads are issued before the current tile is consumed.
+// Record offsets of the split's keys are resolved through the block table
+// once, into LDS.
 
 #include "common.h"
 
 namespace cs {
 namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kD = 128;
 constexpr int kWaves = 4;
@@ -30,6 +43,10 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kMaxGroup = 8;
 constexpr int kMaxPos = 256;
 constexpr int kMaxSplit = 1024;
+constexpr int kTile = 16;
+constexpr int kFixupGrid = 1024;
+constexpr float kInvSqrtD = 0.08838834764831845f;  // 1/sqrt(128)
+constexpr float kLog2e = 1.4426950408889634f;
 
 struct kv_addr {
   const uint16_t* cache;
@@ -52,520 +69,607 @@ struct decode_params {
   const float* e;
   int32_t npos;
   int32_t split, smax;
-  double* tot;   // [B, hq, smax] gate totals
-  float* mx;     // [B, hq, smax] running max (log2 domain)
-  float* sm;     // [B, hq, smax] sum of exp2
-  float* acc;    // [B, hq, smax, 128]
+  double* tot;         // [B, hq, smax] gate totals
+  double* carry;       // [B, hq, smax] gate mass to the right of each split
+  float* mx;           // [B, hq, smax] running max (log2 domain)
+  float* sm;           // [B, hq, smax] sum of exp2
+  float* acc;          // [B, hq, smax, 128]
+  int32_t* work;       // fixup queue: (b * hkv + kvh) * smax + r
+  int32_t* work_count;
   uint16_t* out;
   int32_t* flags;
 };
-
-__device__ inline const uint16_t* kv_row(const kv_addr& a, int b, int kvh, int64_t j, bool is_v,
-                                         bool* bad) {
-  if (a.block_table) {
-    const int64_t bi = a.bs_shift >= 0 ? (j >> a.bs_shift) : j / a.block_size;
-    if (bi >= a.bt_cols) {
-      *bad = true;
-      return nullptr;
-    }
-    const int32_t blk = a.block_table[b * a.bt_stride + bi];
-    if (blk < 0 || blk >= a.num_blocks) {
-      *bad = true;
-      return nullptr;
-    }
-    const int64_t off = a.bs_shift >= 0 ? (j & ((int64_t(1) << a.bs_shift) - 1)) : j % a.block_size;
-    return a.cache + blk * a.s_block + kvh * a.s_head + off * a.s_offset + (is_v ? kD : 0);
-  }
-  return is_v ? a.v + b * a.v_sb + j * a.v_st + kvh * a.v_sh
-              : a.k + b * a.k_sb + j * a.k_st + kvh * a.k_sh;
-}
-
-__device__ inline void unpack8(uint4 u, float* f) {
-  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    f[2 * i] = __uint_as_float(w[i] << 16);
-    f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-  }
-}
 
 __device__ inline int64_t ws_index(const decode_params& p, int b, int h, int r) {
   return (static_cast<int64_t>(b) * p.hq + h) * p.smax + r;
 }
 
-// Speculative split r >= 1: every position is assumed saturated (p = P-1), so
-// the bias is the per-head constant QE[P-1] and the split is one streaming pass
-// of plain attention.  Each 16-lane group owns one key at a time (lane x holds
-// dims 8x..8x+7 of its K and V rows) and keeps an online-softmax state per
-// head over the keys it has seen; the 4 lane groups and 4 waves are merged at
-// the end.  The split's gate total is recorded for the fixup pass.
-constexpr int kSpecUnroll = 4;
+template <int G>
+struct smem_t {
+  int64_t koff[kMaxSplit];  // record offset of each key of the split (paged), -1 if invalid
+  union {
+    float sc[G][kMaxSplit];       // exact splits: logits
+    float wave_o[kWaves][G][kD];  // end of a split: per-wave accumulators
+  } u;
+  float qe[G][kMaxPos];  // exact splits: QE = q . E
+  float q[G][kD];
+  double wave_tot[kWaves][G];
+  double carry[G];
+  float wave_m[kWaves][G];
+  float wave_l[kWaves][G];
+};
 
-template <int GT>
-__global__ void __launch_bounds__(kThreads) decode_spec_kernel(decode_params p) {
-  constexpr int kMaxGroup = GT;  // registers sized for this group, not the maximum
-  __shared__ float wave_m[kWaves][kMaxGroup];
-  __shared__ float wave_l[kWaves][kMaxGroup];
-  __shared__ double wave_tot[kWaves][kMaxGroup];
-  __shared__ float wave_o[kWaves][kMaxGroup][kD];
+struct split_ctx {
+  int b, kvh, h0, r;
+  int64_t lo, hi;
+};
 
-  const int r = blockIdx.x + 1, kvh = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int a4 = lane >> 4, x = lane & 15;
-  constexpr int G = GT;
+__device__ inline bool make_ctx(const decode_params& p, int b, int kvh, int r, split_ctx& c) {
   const int nk = p.nk[b];
   int splits = (nk + p.split - 1) / p.split;
-  if (splits > p.smax) splits = p.smax;
-  if (r >= splits) return;
-  const int64_t hi = static_cast<int64_t>(nk) - static_cast<int64_t>(r) * p.split;
-  const int64_t lo = hi - p.split > 0 ? hi - p.split : 0;
-  const int h0 = kvh * G;
-  const float kLog2e = 1.4426950408889634f;
-  const float c_scale = 0.08838834764831845f * kLog2e;  // log2(e) / sqrt(128)
+  if (splits > p.smax) splits = p.smax;  // the workspace holds smax splits
+  if (r >= splits) return false;
+  c.b = b;
+  c.kvh = kvh;
+  c.h0 = kvh * p.group;
+  c.r = r;
+  c.hi = static_cast<int64_t>(nk) - static_cast<int64_t>(r) * p.split;
+  c.lo = c.hi - p.split > 0 ? c.hi - p.split : 0;
+  return true;
+}
 
-  // q slice of every head in registers; QE[P-1] by a 16-lane reduction
-  float qr[kMaxGroup][8];
-  float bias2[kMaxGroup];  // QE[P-1] * log2(e)
+// gate of a logit: sigmoid (position.py:305)
+__device__ inline float gate_of(float logit) { return 1.f / (1.f + __expf(-logit)); }
+
+template <int H>
+__device__ inline uint32_t dpp_row_bcast(uint32_t x) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x150 + H, 0xF, 0xF, false));
+}
+
+// value of lane h of this lane's row of 16
+__device__ inline uint32_t row_bcast(uint32_t x, int h) {
+  switch (h) {
+    case 0: return dpp_row_bcast<0>(x);
+    case 1: return dpp_row_bcast<1>(x);
+    case 2: return dpp_row_bcast<2>(x);
+    case 3: return dpp_row_bcast<3>(x);
+    case 4: return dpp_row_bcast<4>(x);
+    case 5: return dpp_row_bcast<5>(x);
+    case 6: return dpp_row_bcast<6>(x);
+    default: return dpp_row_bcast<7>(x);
+  }
+}
+
+__device__ inline float row_bcast_f(float x, int h) {
+  return __uint_as_float(row_bcast(__float_as_uint(x), h));
+}
+
+__device__ inline uint32_t pack_bf16x2(float lo, float hi) {
+  bf16x2 v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ inline float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b),
+                                         c, false);
+}
+
+__device__ inline uint4 ld16(const uint16_t* ptr) {
+  return ptr ? *reinterpret_cast<const uint4*>(ptr) : make_uint4(0, 0, 0, 0);
+}
+
+// Resolve the record offsets of keys [lo, hi) through the block table.
+template <int G>
+__device__ void load_offsets(const decode_params& p, smem_t<G>& s, const split_ctx& c, bool& bad) {
+  if (!p.kv.block_table) return;
+  const int n = static_cast<int>(c.hi - c.lo);
+  for (int i = threadIdx.x; i < n; i += kThreads) {
+    const int64_t j = c.lo + i;
+    const int64_t bi = p.kv.bs_shift >= 0 ? (j >> p.kv.bs_shift) : j / p.kv.block_size;
+    int64_t off = -1;
+    if (bi < p.kv.bt_cols) {
+      const int64_t blk = p.kv.block_table[c.b * p.kv.bt_stride + bi];
+      if (blk >= 0 && blk < p.kv.num_blocks) {
+        const int64_t o =
+            p.kv.bs_shift >= 0 ? (j & ((int64_t(1) << p.kv.bs_shift) - 1)) : j % p.kv.block_size;
+        off = blk * p.kv.s_block + c.kvh * p.kv.s_head + o * p.kv.s_offset;
+      }
+    }
+    if (off < 0) bad = true;
+    s.koff[i] = off;
+  }
+}
+
+// K / V row of key j (lo <= j < hi), or null for an invalid block.
+template <int G>
+__device__ inline const uint16_t* k_row(const decode_params& p, const smem_t<G>& s,
+                                        const split_ctx& c, int64_t j) {
+  if (p.kv.block_table) {
+    const int64_t o = s.koff[j - c.lo];
+    return o < 0 ? nullptr : p.kv.cache + o;
+  }
+  return p.kv.k + c.b * p.kv.k_sb + j * p.kv.k_st + c.kvh * p.kv.k_sh;
+}
+
+template <int G>
+__device__ inline const uint16_t* v_row(const decode_params& p, const smem_t<G>& s,
+                                        const split_ctx& c, int64_t j) {
+  if (p.kv.block_table) {
+    const int64_t o = s.koff[j - c.lo];
+    return o < 0 ? nullptr : p.kv.cache + o + kD;
+  }
+  return p.kv.v + c.b * p.kv.v_sb + j * p.kv.v_st + c.kvh * p.kv.v_sh;
+}
+
+struct ktile {
+  bf16x8 a[4];
+};
+struct vtile {
+  uint4 v[4];
+};
+
+// K operand of tile t0: lane (g, n) loads key t0 + n, dims 32t + 8g .. +7.
+template <int G>
+__device__ inline void load_k(ktile& kt, const decode_params& p, const smem_t<G>& s,
+                              const split_ctx& c, int64_t t0, int64_t wlo, int lane) {
+  const int g = lane >> 4, n = lane & 15;
+  const int64_t j = t0 + n;
+  const uint16_t* row = j >= wlo ? k_row(p, s, c, j) : nullptr;
 #pragma unroll
-  for (int gg = 0; gg < kMaxGroup; ++gg) {
-    if (gg < G) {
-      uint4 u = *reinterpret_cast<const uint4*>(p.q + b * p.q_sb + (h0 + gg) * p.q_sh + 8 * x);
-      unpack8(u, qr[gg]);
-      float part = 0.f;
+  for (int t = 0; t < 4; ++t)
+    kt.a[t] = __builtin_bit_cast(bf16x8, ld16(row ? row + 32 * t + 8 * g : nullptr));
+}
+
+// V of tile t0: lane (g, x) loads keys t0 + 4g + v (v = 0..3), dims 8x .. +7.
+template <int G>
+__device__ inline void load_v(vtile& vt, const decode_params& p, const smem_t<G>& s,
+                              const split_ctx& c, int64_t t0, int64_t wlo, int lane) {
+  const int g = lane >> 4, x = lane & 15;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) part += qr[gg][i] * p.e[(8 * x + i) * p.npos + (p.npos - 1)];
-      part += __shfl_xor(part, 8, 64);
-      part += __shfl_xor(part, 4, 64);
-      part += __shfl_xor(part, 2, 64);
-      part += __shfl_xor(part, 1, 64);
-      bias2[gg] = part * kLog2e;
-    } else {
+  for (int v = 0; v < 4; ++v) {
+    const int64_t j = t0 + 4 * g + v;
+    const uint16_t* row = j >= wlo ? v_row(p, s, c, j) : nullptr;
+    vt.v[v] = ld16(row ? row + 8 * x : nullptr);
+  }
+}
+
+__device__ inline floatx4 qk_tile(const ktile& kt, const bf16x8* qb) {
+  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int i = 0; i < 8; ++i) qr[gg][i] = 0.f;
-      bias2[gg] = 0.f;
+  for (int t = 0; t < 4; ++t) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kt.a[t], qb[t], acc, 0, 0, 0);
+  return acc;
+}
+
+template <int G>
+struct wstate {
+  float m, l;      // lane (g, n): head n over the keys of row g (log2 domain)
+  float o[G][8];   // lane (g, x): head h, dims 8x..8x+7 over the keys of row g
+  double tsum;     // lane (g, n): gate mass of head n over the keys of row g
+};
+
+template <int G>
+__device__ inline void init_state(wstate<G>& st) {
+  st.m = -INFINITY;
+  st.l = 0.f;
+  st.tsum = 0.0;
+#pragma unroll
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) st.o[h][i] = 0.f;
+}
+
+// Online-softmax update with the 4 scores x[v] (log2 domain, -inf when masked)
+// of this lane's head, then P.V for the 4 keys of the row.
+template <int G>
+__device__ inline void accumulate(wstate<G>& st, const float* x, const vtile& vt) {
+  float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+  mx = fmaxf(mx, st.m);
+  float corr = 1.f, pv[4] = {0.f, 0.f, 0.f, 0.f};
+  if (mx != -INFINITY) {
+    corr = __builtin_amdgcn_exp2f(st.m - mx);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) pv[v] = __builtin_amdgcn_exp2f(x[v] - mx);
+  }
+  st.l = st.l * corr + ((pv[0] + pv[1]) + (pv[2] + pv[3]));
+  st.m = mx;
+  const uint32_t p01 = pack_bf16x2(pv[0], pv[1]);
+  const uint32_t p23 = pack_bf16x2(pv[2], pv[3]);
+  // (key 4g, key 4g+1) and (key 4g+2, key 4g+3) pairs of each dim
+  uint32_t lo01[4], hi01[4], lo23[4], hi23[4];
+  const uint32_t w0[4] = {vt.v[0].x, vt.v[0].y, vt.v[0].z, vt.v[0].w};
+  const uint32_t w1[4] = {vt.v[1].x, vt.v[1].y, vt.v[1].z, vt.v[1].w};
+  const uint32_t w2[4] = {vt.v[2].x, vt.v[2].y, vt.v[2].z, vt.v[2].w};
+  const uint32_t w3[4] = {vt.v[3].x, vt.v[3].y, vt.v[3].z, vt.v[3].w};
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    lo01[w] = __builtin_amdgcn_perm(w1[w], w0[w], 0x05040100u);
+    hi01[w] = __builtin_amdgcn_perm(w1[w], w0[w], 0x07060302u);
+    lo23[w] = __builtin_amdgcn_perm(w3[w], w2[w], 0x05040100u);
+    hi23[w] = __builtin_amdgcn_perm(w3[w], w2[w], 0x07060302u);
+  }
+  if (__any(corr != 1.f)) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float ch = row_bcast_f(corr, h);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) st.o[h][i] *= ch;
     }
   }
-
-  float m[kMaxGroup], l[kMaxGroup], o[kMaxGroup][8];
-  double tsum[kMaxGroup];
 #pragma unroll
-  for (int gg = 0; gg < kMaxGroup; ++gg) {
-    m[gg] = -INFINITY;
-    l[gg] = 0.f;
-    tsum[gg] = 0.0;
+  for (int h = 0; h < G; ++h) {
+    const uint32_t a = row_bcast(p01, h);
+    const uint32_t b = row_bcast(p23, h);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) o[gg][i] = 0.f;
-  }
-
-  const int kw = p.split / kWaves;
-  int64_t wlo = lo + static_cast<int64_t>(wave) * kw;
-  int64_t whi = wlo + kw;
-  if (wlo > hi) wlo = hi;
-  if (whi > hi) whi = hi;
-  bool bad = false;
-  for (int64_t base = wlo; base < whi; base += 4 * kSpecUnroll) {
-    uint4 kb[kSpecUnroll], vb[kSpecUnroll];
-#pragma unroll
-    for (int u = 0; u < kSpecUnroll; ++u) {
-      const int64_t j = base + 4 * u + a4;
-      kb[u] = make_uint4(0, 0, 0, 0);
-      vb[u] = make_uint4(0, 0, 0, 0);
-      if (j < whi) {
-        const uint16_t* kr = kv_row(p.kv, b, kvh, j, false, &bad);
-        if (kr) {
-          kb[u] = *reinterpret_cast<const uint4*>(kr + 8 * x);
-          vb[u] = *reinterpret_cast<const uint4*>(kr + kD + 8 * x);
-        }
-      }
-    }
-    float s[kSpecUnroll][kMaxGroup];
-#pragma unroll
-    for (int u = 0; u < kSpecUnroll; ++u) {
-      float kf[8];
-      unpack8(kb[u], kf);
-#pragma unroll
-      for (int gg = 0; gg < kMaxGroup; ++gg) {
-        float d = 0.f;
-        if (gg < G) {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) d += qr[gg][i] * kf[i];
-          d += __shfl_xor(d, 8, 64);
-          d += __shfl_xor(d, 4, 64);
-          d += __shfl_xor(d, 2, 64);
-          d += __shfl_xor(d, 1, 64);
-        }
-        s[u][gg] = d;
-      }
-    }
-#pragma unroll
-    for (int gg = 0; gg < kMaxGroup; ++gg) {
-      if (gg >= G) continue;
-      float xs[kSpecUnroll];
-      float mx = m[gg];
-#pragma unroll
-      for (int u = 0; u < kSpecUnroll; ++u) {
-        const bool in = base + 4 * u + a4 < whi;
-        // natural-log logit for the gate mass, log2-domain score for softmax
-        const float logit = s[u][gg] * 0.08838834764831845f;
-        if (in && x == 0) tsum[gg] += static_cast<double>(1.f / (1.f + __expf(-logit)));
-        xs[u] = in ? s[u][gg] * c_scale + bias2[gg] : -INFINITY;
-        mx = fmaxf(mx, xs[u]);
-      }
-      if (mx == -INFINITY) continue;
-      const float corr = __builtin_amdgcn_exp2f(m[gg] - mx);
-      l[gg] *= corr;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) o[gg][i] *= corr;
-#pragma unroll
-      for (int u = 0; u < kSpecUnroll; ++u) {
-        const float pw = __builtin_amdgcn_exp2f(xs[u] - mx);
-        l[gg] += pw;
-        float vf[8];
-        unpack8(vb[u], vf);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) o[gg][i] += pw * vf[i];
-      }
-      m[gg] = mx;
+    for (int w = 0; w < 4; ++w) {
+      st.o[h][2 * w] = dot2(a, lo01[w], st.o[h][2 * w]);
+      st.o[h][2 * w + 1] = dot2(a, hi01[w], st.o[h][2 * w + 1]);
+      st.o[h][2 * w] = dot2(b, lo23[w], st.o[h][2 * w]);
+      st.o[h][2 * w + 1] = dot2(b, hi23[w], st.o[h][2 * w + 1]);
     }
   }
+}
 
-  // merge the 4 lane groups of the wave (xor 16, then xor 32)
+// Merge the 4 rows of the wave and leave the wave's (m, l, o, gate total) in LDS.
+template <int G>
+__device__ inline void wave_finish(wstate<G>& st, smem_t<G>& s, int wave, int lane) {
+  const int g = lane >> 4, x = lane & 15;
 #pragma unroll
-  for (int off = 16; off <= 32; off <<= 1) {
+  for (int h = 0; h < G; ++h) {
+    float mh = row_bcast_f(st.m, h);
+    float lh = row_bcast_f(st.l, h);
 #pragma unroll
-    for (int gg = 0; gg < kMaxGroup; ++gg) {
-      if (gg >= G) continue;
-      const float m2 = __shfl_xor(m[gg], off, 64);
-      const float l2 = __shfl_xor(l[gg], off, 64);
-      const float M = fmaxf(m[gg], m2);
-      const float f1 = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[gg] - M);
+    for (int off = 16; off <= 32; off <<= 1) {
+      const float m2 = __shfl_xor(mh, off, 64);
+      const float l2 = __shfl_xor(lh, off, 64);
+      const float M = fmaxf(mh, m2);
+      const float f1 = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mh - M);
       const float f2 = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m2 - M);
-      l[gg] = l[gg] * f1 + l2 * f2;
+      lh = lh * f1 + l2 * f2;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float o2 = __shfl_xor(o[gg][i], off, 64);
-        o[gg][i] = o[gg][i] * f1 + o2 * f2;
+        const float o2 = __shfl_xor(st.o[h][i], off, 64);
+        st.o[h][i] = st.o[h][i] * f1 + o2 * f2;
       }
-      m[gg] = M;
-      tsum[gg] += __shfl_xor(tsum[gg], off, 64);
+      mh = M;
+    }
+    if (g == 0) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s.u.wave_o[wave][h][8 * x + i] = st.o[h][i];
+    }
+    if (lane == h) {
+      s.wave_m[wave][h] = mh;
+      s.wave_l[wave][h] = lh;
     }
   }
-  if (a4 == 0) {
-#pragma unroll
-    for (int gg = 0; gg < kMaxGroup; ++gg)
-      if (gg < G)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) wave_o[wave][gg][8 * x + i] = o[gg][i];
-  }
-  if (lane == 0) {
-#pragma unroll
-    for (int gg = 0; gg < kMaxGroup; ++gg)
-      if (gg < G) {
-        wave_m[wave][gg] = m[gg];
-        wave_l[wave][gg] = l[gg];
-        wave_tot[wave][gg] = tsum[gg];
-      }
-  }
+  double t = st.tsum;
+  t += __shfl_xor(t, 16, 64);
+  t += __shfl_xor(t, 32, 64);
+  if (lane < G) s.wave_tot[wave][lane] = t;
+}
+
+// Merge the 4 waves and write the split's partial.
+template <int G>
+__device__ inline void split_finish(const decode_params& p, smem_t<G>& s, const split_ctx& c,
+                                    bool write_tot) {
   __syncthreads();
-  for (int i = tid; i < G * kD; i += kThreads) {
-    const int gg = i / kD, d = i % kD;
+  for (int i = threadIdx.x; i < G * kD; i += kThreads) {
+    const int h = i / kD, d = i % kD;
     float M = -INFINITY;
-    for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, wave_m[ww][gg]);
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s.wave_m[w][h]);
     float L = 0.f, O = 0.f;
-    for (int ww = 0; ww < kWaves; ++ww) {
-      const float wm = wave_m[ww][gg];
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float wm = s.wave_m[w][h];
       if (wm == -INFINITY) continue;
       const float f = __builtin_amdgcn_exp2f(wm - M);
-      L += wave_l[ww][gg] * f;
-      O += wave_o[ww][gg][d] * f;
+      L += s.wave_l[w][h] * f;
+      O += s.u.wave_o[w][h][d] * f;
     }
-    const int64_t wi = ws_index(p, b, h0 + gg, r);
+    const int64_t wi = ws_index(p, c.b, c.h0 + h, c.r);
     p.acc[wi * kD + d] = O;
     if (d == 0) {
       p.mx[wi] = M;
       p.sm[wi] = L;
-      double T = 0.0;
-      for (int ww = 0; ww < kWaves; ++ww) T += wave_tot[ww][gg];
-      p.tot[wi] = T;
+      if (write_tot) {
+        double T = 0.0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) T += s.wave_tot[w][h];
+        p.tot[wi] = T;
+      }
     }
+  }
+}
+
+// Q operand (lane (g, n): head n, dims 32t + 8g .. +7; zero for n >= G).
+template <int G>
+__device__ inline void load_q(bf16x8* qb, const decode_params& p, const split_ctx& c, int lane) {
+  const int g = lane >> 4, n = lane & 15;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    uint4 u = make_uint4(0, 0, 0, 0);
+    if (n < G) u = *reinterpret_cast<const uint4*>(p.q + c.b * p.q_sb + (c.h0 + n) * p.q_sh + 32 * t + 8 * g);
+    qb[t] = __builtin_bit_cast(bf16x8, u);
+  }
+}
+
+// Speculative split: every position is P-1, the bias the constant QE[P-1].
+template <int G>
+__device__ void run_spec(const decode_params& p, smem_t<G>& s, const split_ctx& c, bool& bad) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane >> 4, n = lane & 15;
+  load_offsets(p, s, c, bad);
+  bf16x8 qb[4];
+  load_q<G>(qb, p, c, lane);
+  // QE[P-1] of head n: lane (g, n) sums its 32 dims, then the 4 rows are added
+  float part = 0.f;
+  if (n < G) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint4 u = __builtin_bit_cast(uint4, qb[t]);
+      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int d = 32 * t + 8 * g + 2 * i;
+        part += __uint_as_float(w[i] << 16) * p.e[d * p.npos + (p.npos - 1)];
+        part += __uint_as_float(w[i] & 0xffff0000u) * p.e[(d + 1) * p.npos + (p.npos - 1)];
+      }
+    }
+  }
+  part += __shfl_xor(part, 16, 64);
+  part += __shfl_xor(part, 32, 64);
+  const float bias2 = part * kLog2e;
+  const float c_scale = kInvSqrtD * kLog2e;
+  __syncthreads();
+
+  const int kw = p.split / kWaves;
+  int64_t wlo = c.lo + static_cast<int64_t>(wave) * kw;
+  int64_t whi = wlo + kw;
+  if (wlo > c.hi) wlo = c.hi;
+  if (whi > c.hi) whi = c.hi;
+  const int ntiles = static_cast<int>((whi - wlo + kTile - 1) / kTile);
+
+  wstate<G> st;
+  init_state(st);
+  auto tile = [&](const ktile& kt, const vtile& vt, int64_t t0) {
+    const floatx4 sT = qk_tile(kt, qb);
+    float x[4], tg = 0.f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const bool valid = n < G && t0 + 4 * g + v >= wlo;
+      const float logit = sT[v] * kInvSqrtD;
+      tg += valid ? __builtin_amdgcn_rcpf(1.f + __expf(-logit)) : 0.f;
+      x[v] = valid ? sT[v] * c_scale + bias2 : -INFINITY;
+    }
+    st.tsum += static_cast<double>(tg);
+    accumulate(st, x, vt);
+  };
+  ktile ka, kb;
+  vtile va, vb;
+  if (ntiles > 0) {
+    load_k(ka, p, s, c, whi - kTile, wlo, lane);
+    load_v(va, p, s, c, whi - kTile, wlo, lane);
+  }
+  for (int i = 0; i < ntiles; i += 2) {
+    const int64_t t0 = whi - static_cast<int64_t>(i + 1) * kTile;
+    if (i + 1 < ntiles) {
+      load_k(kb, p, s, c, t0 - kTile, wlo, lane);
+      load_v(vb, p, s, c, t0 - kTile, wlo, lane);
+    }
+    tile(ka, va, t0);
+    if (i + 1 < ntiles) {
+      if (i + 2 < ntiles) {
+        load_k(ka, p, s, c, t0 - 2 * kTile, wlo, lane);
+        load_v(va, p, s, c, t0 - 2 * kTile, wlo, lane);
+      }
+      tile(kb, vb, t0 - kTile);
+    }
+  }
+  __syncthreads();
+  wave_finish(st, s, wave, lane);
+  split_finish(p, s, c, true);
+}
+
+// Exact split with the given carry per head (s.carry): positions from the
+// gate suffix sums (fp64), bias by interpolation in the QE table.
+template <int G>
+__device__ void run_exact(const decode_params& p, smem_t<G>& s, const split_ctx& c, bool write_tot,
+                          bool& bad) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, n = lane & 15;
+  load_offsets(p, s, c, bad);
+  bf16x8 qb[4];
+  load_q<G>(qb, p, c, lane);
+  for (int i = tid; i < G * kD; i += kThreads) {
+    const int h = i / kD, d = i % kD;
+    s.q[h][d] = bf16_to_float(p.q[c.b * p.q_sb + (c.h0 + h) * p.q_sh + d]);
+  }
+  __syncthreads();
+  for (int i = tid; i < G * p.npos; i += kThreads) {
+    const int h = i / p.npos, pp = i % p.npos;
+    float a = 0.f;
+    for (int d = 0; d < kD; ++d) a += s.q[h][d] * p.e[d * p.npos + pp];
+    s.qe[h][pp] = a;
+  }
+
+  const int kw = p.split / kWaves;
+  int64_t wlo = c.lo + static_cast<int64_t>(wave) * kw;
+  int64_t whi = wlo + kw;
+  if (wlo > c.hi) wlo = c.hi;
+  if (whi > c.hi) whi = c.hi;
+  const int ntiles = static_cast<int>((whi - wlo + kTile - 1) / kTile);
+
+  // ---- pass 1: logits into LDS, gate totals per wave -----------------------
+  double gsum = 0.0;
+  auto ktile_pass = [&](const ktile& kt, int64_t t0) {
+    const floatx4 sT = qk_tile(kt, qb);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int64_t j = t0 + 4 * g + v;
+      if (n < G && j >= wlo) {
+        const float logit = sT[v] * kInvSqrtD;
+        s.u.sc[n][j - c.lo] = logit;
+        gsum += static_cast<double>(gate_of(logit));
+      }
+    }
+  };
+  {
+    ktile ka, kb;
+    if (ntiles > 0) load_k(ka, p, s, c, whi - kTile, wlo, lane);
+    for (int i = 0; i < ntiles; i += 2) {
+      const int64_t t0 = whi - static_cast<int64_t>(i + 1) * kTile;
+      if (i + 1 < ntiles) load_k(kb, p, s, c, t0 - kTile, wlo, lane);
+      ktile_pass(ka, t0);
+      if (i + 1 < ntiles) {
+        if (i + 2 < ntiles) load_k(ka, p, s, c, t0 - 2 * kTile, wlo, lane);
+        ktile_pass(kb, t0 - kTile);
+      }
+    }
+  }
+  {
+    double t = gsum;
+    t += __shfl_xor(t, 16, 64);
+    t += __shfl_xor(t, 32, 64);
+    if (lane < G) s.wave_tot[wave][lane] = t;
+  }
+  __syncthreads();
+
+  // ---- pass 2: positions, scores, P.V ---------------------------------------
+  const float top = static_cast<float>(p.npos - 1);
+  double carry = 0.0;
+  if (n < G) {
+    carry = s.carry[n];
+    for (int w = kWaves - 1; w > wave; --w) carry += s.wave_tot[w][n];
+  }
+  wstate<G> st;
+  init_state(st);
+  auto vtile_pass = [&](const vtile& vt, int64_t t0) {
+    float lg[4];
+    double gt[4];
+    bool valid[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int64_t j = t0 + 4 * g + v;
+      valid[v] = n < G && j >= wlo;
+      lg[v] = valid[v] ? s.u.sc[n][j - c.lo] : 0.f;
+      gt[v] = valid[v] ? static_cast<double>(gate_of(lg[v])) : 0.0;
+    }
+    // suffix sums in descending key order: within the row, then over rows
+    double sfx[4];
+    sfx[3] = gt[3];
+    sfx[2] = sfx[3] + gt[2];
+    sfx[1] = sfx[2] + gt[1];
+    sfx[0] = sfx[1] + gt[0];
+    const double r1 = __shfl(sfx[0], lane + 16, 64);
+    const double r2 = __shfl(sfx[0], lane + 32, 64);
+    const double r3 = __shfl(sfx[0], lane + 48, 64);
+    double above = 0.0;
+    if (g < 3) above += r1;
+    if (g < 2) above += r2;
+    if (g < 1) above += r3;
+    const double total = __shfl(above + sfx[0], n, 64);  // lane (0, n): whole tile
+    float x[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      float pos = static_cast<float>(carry + above + sfx[v]);
+      pos = pos < top ? pos : top;
+      pos = pos > 0.f ? pos : 0.f;  // also maps NaN to 0: table reads stay in range
+      const float fl = floorf(pos);
+      const int lo_i = static_cast<int>(fl);
+      const int hi_i = lo_i + 1 < p.npos - 1 ? lo_i + 1 : p.npos - 1;
+      const int hh = n < G ? n : 0;
+      const float bias = s.qe[hh][lo_i] + (pos - fl) * (s.qe[hh][hi_i] - s.qe[hh][lo_i]);
+      x[v] = valid[v] ? (lg[v] + bias) * kLog2e : -INFINITY;
+    }
+    carry += total;
+    accumulate(st, x, vt);
+  };
+  {
+    vtile va, vb;
+    if (ntiles > 0) load_v(va, p, s, c, whi - kTile, wlo, lane);
+    for (int i = 0; i < ntiles; i += 2) {
+      const int64_t t0 = whi - static_cast<int64_t>(i + 1) * kTile;
+      if (i + 1 < ntiles) load_v(vb, p, s, c, t0 - kTile, wlo, lane);
+      vtile_pass(va, t0);
+      if (i + 1 < ntiles) {
+        if (i + 2 < ntiles) load_v(va, p, s, c, t0 - 2 * kTile, wlo, lane);
+        vtile_pass(vb, t0 - kTile);
+      }
+    }
+  }
+  __syncthreads();  // the per-wave accumulators overwrite the logits
+  st.tsum = gsum;    // wave_finish publishes the pass-1 gate totals again
+  wave_finish(st, s, wave, lane);
+  split_finish(p, s, c, write_tot);
+}
+
+// Split 0 of every (request, KV head) exactly, then the speculative splits;
+// the grid is ordered split-major so the exact workgroups start first.
+template <int G>
+__global__ void __launch_bounds__(kThreads) decode_main_kernel(decode_params p) {
+  __shared__ smem_t<G> s;
+  const int per_r = p.hkv * p.batch;
+  const int id = blockIdx.x;
+  const int r = id / per_r, rem = id % per_r;
+  const int b = rem / p.hkv, kvh = rem % p.hkv;
+  if (id == 0 && threadIdx.x == 0) *p.work_count = 0;
+  split_ctx c;
+  if (!make_ctx(p, b, kvh, r, c)) return;
+  bool bad = false;
+  if (r == 0) {
+    if (threadIdx.x < G) s.carry[threadIdx.x] = 0.0;
+    run_exact<G>(p, s, c, true, bad);
+  } else {
+    run_spec<G>(p, s, c, bad);
   }
   if (bad) atomicOr(p.flags, CS_FLAG_BLOCK_INVALID);
 }
 
-__global__ void __launch_bounds__(kThreads) decode_split_kernel(decode_params p, int fixup) {
-  __shared__ float q_lds[kMaxGroup][kD];
-  __shared__ float qe_lds[kMaxGroup][kMaxPos];
-  __shared__ float sc_lds[kMaxGroup][kMaxSplit];
-  __shared__ double wave_tot[kWaves][kMaxGroup];
-  __shared__ double carry_lds[kMaxGroup];
-  __shared__ float wave_m[kWaves][kMaxGroup];
-  __shared__ float wave_l[kWaves][kMaxGroup];
-  __shared__ float wave_o[kWaves][kMaxGroup][kD];
-  __shared__ int skip_lds;
-
-  const int r = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int G = p.group;
+// Carry of every split (fp64 sum of the totals to its right, in split order)
+// and the queue of splits whose carry is below P-1 for some head.
+__global__ void decode_plan_kernel(decode_params p) {
+  const int b = blockIdx.x / p.hkv, kvh = blockIdx.x % p.hkv;
   const int nk = p.nk[b];
   int splits = (nk + p.split - 1) / p.split;
-  if (splits > p.smax) splits = p.smax;  // the workspace holds smax splits
-  if (r >= splits) return;
-  const int64_t hi = static_cast<int64_t>(nk) - static_cast<int64_t>(r) * p.split;
-  const int64_t lo = hi - p.split > 0 ? hi - p.split : 0;
-  const int h0 = kvh * G;
-  const float top = static_cast<float>(p.npos - 1);
-
-  if (fixup) {
-    if (r == 0) return;
-    if (tid < G) {
-      double c = 0.0;
-      for (int rr = 0; rr < r; ++rr) c += p.tot[ws_index(p, b, h0 + tid, rr)];
-      carry_lds[tid] = c;
+  if (splits > p.smax) splits = p.smax;
+  const int G = p.group, h0 = kvh * G;
+  const double top = static_cast<double>(p.npos - 1);
+  if (static_cast<int>(threadIdx.x) < G) {
+    const int h = h0 + threadIdx.x;
+    double carry = 0.0;
+    for (int r = 0; r < splits; ++r) {
+      const int64_t wi = ws_index(p, b, h, r);
+      p.carry[wi] = carry;
+      carry += p.tot[wi];
     }
-    if (tid == 0) skip_lds = 1;
-    __syncthreads();
-    if (tid < G && carry_lds[tid] < static_cast<double>(top)) skip_lds = 0;
-    __syncthreads();
-    if (skip_lds) return;
-  } else {
-    if (tid < G) carry_lds[tid] = 0.0;
-  }
-  const bool exact = fixup || r == 0;
-
-  // q rows of the group (float) and the QE table (full when exact).
-  for (int i = tid; i < G * kD; i += kThreads) {
-    int gg = i / kD, d = i % kD;
-    q_lds[gg][d] = bf16_to_float(p.q[b * p.q_sb + (h0 + gg) * p.q_sh + d]);
   }
   __syncthreads();
-  for (int i = tid; i < G * p.npos; i += kThreads) {
-    int gg = i / p.npos, pp = i % p.npos;
-    if (!exact && pp != p.npos - 1) continue;
-    float a = 0.f;
-    for (int d = 0; d < kD; ++d) a += q_lds[gg][d] * p.e[d * p.npos + pp];
-    qe_lds[gg][pp] = a;
+  for (int r = 1 + threadIdx.x; r < splits; r += blockDim.x) {
+    bool need = false;
+    for (int h = 0; h < G; ++h) need |= p.carry[ws_index(p, b, h0 + h, r)] < top;
+    if (need) {
+      const int slot = atomicAdd(p.work_count, 1);
+      p.work[slot] = (b * p.hkv + kvh) * p.smax + r;
+    }
   }
+}
 
-  // ---- pass 1: logits for this wave's quarter of the split -------------
-  const int kw = p.split / kWaves;
-  const int64_t wlo = lo + static_cast<int64_t>(wave) * kw > hi ? hi : lo + static_cast<int64_t>(wave) * kw;
-  int64_t whi_ = lo + static_cast<int64_t>(wave + 1) * kw;
-  const int64_t whi = whi_ > hi ? hi : whi_;
-  const int a4 = lane >> 4, x = lane & 15;
-  float qr[kMaxGroup][8];
-#pragma unroll
-  for (int gg = 0; gg < kMaxGroup; ++gg)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) qr[gg][i] = gg < G ? q_lds[gg][8 * x + i] : 0.f;
-  const float logit_scale = 0.08838834764831845f;  // 1/sqrt(128)
-  double gsum[kMaxGroup];
-#pragma unroll
-  for (int gg = 0; gg < kMaxGroup; ++gg) gsum[gg] = 0.0;
+template <int G>
+__global__ void __launch_bounds__(kThreads) decode_fixup_kernel(decode_params p) {
+  __shared__ smem_t<G> s;
+  const int count = *p.work_count;
   bool bad = false;
-  constexpr int kUnroll = 4;
-  for (int64_t base = wlo; base < whi; base += 4 * kUnroll) {
-    uint4 kb[kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      int64_t j = base + 4 * u + a4;
-      kb[u] = make_uint4(0, 0, 0, 0);
-      if (j < whi) {
-        const uint16_t* kr = kv_row(p.kv, b, kvh, j, false, &bad);
-        if (kr) kb[u] = *reinterpret_cast<const uint4*>(kr + 8 * x);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      int64_t j = base + 4 * u + a4;
-      float kf[8];
-      unpack8(kb[u], kf);
-      float dot[kMaxGroup];
-#pragma unroll
-      for (int gg = 0; gg < kMaxGroup; ++gg) {
-        float s = 0.f;
-        if (gg < G) {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) s += qr[gg][i] * kf[i];
-        }
-        dot[gg] = s;
-      }
-#pragma unroll
-      for (int gg = 0; gg < kMaxGroup; ++gg) {
-        if (gg < G) {
-          float s = dot[gg];
-          s += __shfl_xor(s, 8, 64);
-          s += __shfl_xor(s, 4, 64);
-          s += __shfl_xor(s, 2, 64);
-          s += __shfl_xor(s, 1, 64);
-          dot[gg] = s * logit_scale;
-        }
-      }
-      if (x == 0 && j < whi) {
-#pragma unroll
-        for (int gg = 0; gg < kMaxGroup; ++gg)
-          if (gg < G) {
-            sc_lds[gg][j - lo] = dot[gg];
-            gsum[gg] += static_cast<double>(1.f / (1.f + __expf(-dot[gg])));
-          }
-      }
-    }
-  }
-  // wave gate totals
-#pragma unroll
-  for (int gg = 0; gg < kMaxGroup; ++gg) {
-    if (gg < G) {
-      double s = gsum[gg];
-      s += __shfl_xor(s, 16, 64);
-      s += __shfl_xor(s, 32, 64);
-      if (lane == 0) wave_tot[wave][gg] = s;
-    }
-  }
-  __syncthreads();
-
-  // ---- pass 2: scores, wave max, probabilities --------------------------
-  const float kLog2e = 1.4426950408889634f;
-  float m_w[kMaxGroup], l_w[kMaxGroup];
-#pragma unroll
-  for (int gg = 0; gg < kMaxGroup; ++gg) {
-    m_w[gg] = -INFINITY;
-    l_w[gg] = 0.f;
-  }
-  for (int gg = 0; gg < G; ++gg) {
-    float* sc = sc_lds[gg];
-    const float* qe = qe_lds[gg];
-    if (exact) {
-      double carry = carry_lds[gg];
-      for (int ww = kWaves - 1; ww > wave; --ww) carry += wave_tot[ww][gg];
-      const int64_t n = whi - wlo;
-      for (int64_t c0 = ((n + 63) / 64 - 1) * 64; c0 >= 0; c0 -= 64) {
-        int64_t j = wlo + c0 + lane;
-        bool in = j < whi;
-        float lg = in ? sc[j - lo] : 0.f;
-        double gate = in ? static_cast<double>(1.f / (1.f + __expf(-lg))) : 0.0;
-        double s = gate;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-          double nb = __shfl_down(s, off, 64);
-          if (lane + off < 64) s += nb;
-        }
-        double tile_total = __shfl(s, 0, 64);
-        float pos = static_cast<float>(carry + s);
-        pos = pos < top ? pos : top;
-        pos = pos > 0.f ? pos : 0.f;  // also maps NaN to 0: table reads stay in range
-        float fl = floorf(pos);
-        int lo_i = static_cast<int>(fl);
-        int hi_i = lo_i + 1 < p.npos - 1 ? lo_i + 1 : p.npos - 1;
-        float bias = qe[lo_i] + (pos - fl) * (qe[hi_i] - qe[lo_i]);
-        if (in) sc[j - lo] = (lg + bias) * kLog2e;
-        carry += tile_total;
-      }
-    } else {
-      const float bl = qe[p.npos - 1];
-      for (int64_t j = wlo + lane; j < whi; j += 64) sc[j - lo] = (sc[j - lo] + bl) * kLog2e;
-    }
-    float mx = -INFINITY;
-    for (int64_t j = wlo + lane; j < whi; j += 64) mx = fmaxf(mx, sc[j - lo]);
-    mx = wave_max(mx);
-    float sum = 0.f;
-    for (int64_t j = wlo + lane; j < whi; j += 64) {
-      float pv = __builtin_amdgcn_exp2f(sc[j - lo] - mx);
-      sc[j - lo] = pv;
-      sum += pv;
-    }
-    sum = wave_sum(sum);
-    m_w[gg] = mx;
-    l_w[gg] = sum;
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-
-  // ---- pass 3: P.V -------------------------------------------------------
-  float o[kMaxGroup][8];
-#pragma unroll
-  for (int gg = 0; gg < kMaxGroup; ++gg)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) o[gg][i] = 0.f;
-  for (int64_t base = wlo; base < whi; base += 4 * kUnroll) {
-    uint4 vb[kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      int64_t j = base + 4 * u + a4;
-      vb[u] = make_uint4(0, 0, 0, 0);
-      if (j < whi) {
-        const uint16_t* vr = kv_row(p.kv, b, kvh, j, true, &bad);
-        if (vr) vb[u] = *reinterpret_cast<const uint4*>(vr + 8 * x);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      int64_t j = base + 4 * u + a4;
-      if (j < whi) {
-        float vf[8];
-        unpack8(vb[u], vf);
-#pragma unroll
-        for (int gg = 0; gg < kMaxGroup; ++gg) {
-          if (gg < G) {
-            float pw = sc_lds[gg][j - lo];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) o[gg][i] += pw * vf[i];
-          }
-        }
-      }
-    }
-  }
-#pragma unroll
-  for (int gg = 0; gg < kMaxGroup; ++gg)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      if (gg < G) {
-        float s = o[gg][i];
-        s += __shfl_xor(s, 16, 64);
-        s += __shfl_xor(s, 32, 64);
-        o[gg][i] = s;
-      }
-    }
-  if (a4 == 0) {
-#pragma unroll
-    for (int gg = 0; gg < kMaxGroup; ++gg)
-      if (gg < G)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) wave_o[wave][gg][8 * x + i] = o[gg][i];
-  }
-  if (lane == 0) {
-#pragma unroll
-    for (int gg = 0; gg < kMaxGroup; ++gg)
-      if (gg < G) {
-        wave_m[wave][gg] = m_w[gg];
-        wave_l[wave][gg] = l_w[gg];
-      }
-  }
-  __syncthreads();
-
-  // ---- merge the 4 waves and write the split's partial ------------------
-  for (int i = tid; i < G * kD; i += kThreads) {
-    int gg = i / kD, d = i % kD;
-    float M = -INFINITY;
-    for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, wave_m[ww][gg]);
-    float L = 0.f, O = 0.f;
-    for (int ww = 0; ww < kWaves; ++ww) {
-      float wm = wave_m[ww][gg];
-      if (wm == -INFINITY) continue;
-      float f = __builtin_amdgcn_exp2f(wm - M);
-      L += wave_l[ww][gg] * f;
-      O += wave_o[ww][gg][d] * f;
-    }
-    int64_t wi = ws_index(p, b, h0 + gg, r);
-    p.acc[wi * kD + d] = O;
-    if (d == 0) {
-      p.mx[wi] = M;
-      p.sm[wi] = L;
-      if (!fixup) {
-        double T = 0.0;
-        for (int ww = 0; ww < kWaves; ++ww) T += wave_tot[ww][gg];
-        p.tot[wi] = T;
-      }
-    }
+  for (int i = blockIdx.x; i < count; i += gridDim.x) {
+    const int item = p.work[i];
+    const int r = item % p.smax, bk = item / p.smax;
+    const int b = bk / p.hkv, kvh = bk % p.hkv;
+    split_ctx c;
+    if (!make_ctx(p, b, kvh, r, c)) continue;
+    if (threadIdx.x < G) s.carry[threadIdx.x] = p.carry[ws_index(p, b, c.h0 + threadIdx.x, r)];
+    __syncthreads();
+    run_exact<G>(p, s, c, false, bad);
+    __syncthreads();
   }
   if (bad) atomicOr(p.flags, CS_FLAG_BLOCK_INVALID);
 }
@@ -581,15 +685,29 @@ __global__ void decode_combine_kernel(decode_params p) {
   for (int r = 0; r < splits; ++r) M = fmaxf(M, p.mx[ws_index(p, b, h, r)]);
   float L = 0.f, O = 0.f;
   for (int r = 0; r < splits; ++r) {
-    int64_t wi = ws_index(p, b, h, r);
-    float m = p.mx[wi];
+    const int64_t wi = ws_index(p, b, h, r);
+    const float m = p.mx[wi];
     if (m == -INFINITY) continue;
-    float f = __builtin_amdgcn_exp2f(m - M);
+    const float f = __builtin_amdgcn_exp2f(m - M);
     L += p.sm[wi] * f;
     O += p.acc[wi * kD + d] * f;
   }
-  float val = L > 0.f ? O / L : 0.f;
+  const float val = L > 0.f ? O / L : 0.f;
   p.out[static_cast<int64_t>(b) * p.hq * kD + h * kD + d] = float_to_bf16(val);
+}
+
+template <int G>
+void launch_split_kernels(const decode_params& p, hipStream_t s) {
+  const int64_t main_grid = static_cast<int64_t>(p.smax) * p.hkv * p.batch;
+  hipLaunchKernelGGL(decode_main_kernel<G>, dim3(static_cast<uint32_t>(main_grid)), dim3(kThreads), 0,
+                     s, p);
+  if (p.smax > 1) {
+    hipLaunchKernelGGL(decode_plan_kernel, dim3(p.hkv * p.batch), dim3(64), 0, s, p);
+    int64_t fix = static_cast<int64_t>(p.smax - 1) * p.hkv * p.batch;
+    if (fix > kFixupGrid) fix = kFixupGrid;
+    hipLaunchKernelGGL(decode_fixup_kernel<G>, dim3(static_cast<uint32_t>(fix)), dim3(kThreads), 0, s,
+                       p);
+  }
 }
 
 }  // namespace
@@ -600,9 +718,10 @@ using namespace cs;
 extern "C" int64_t cs_ccpe_decode_workspace_bytes(int32_t batch, int32_t hq, int32_t max_nk,
                                                   int32_t split) {
   if (batch <= 0 || hq <= 0 || max_nk <= 0 || split <= 0) return 0;
-  int64_t smax = (static_cast<int64_t>(max_nk) + split - 1) / split;
-  int64_t n = static_cast<int64_t>(batch) * hq * smax;
-  return n * (8 + 4 + 4 + 4 * kD);
+  const int64_t smax = (static_cast<int64_t>(max_nk) + split - 1) / split;
+  const int64_t n = static_cast<int64_t>(batch) * hq * smax;
+  // tot, carry (f64) | acc (f32 x 128) | mx, sm (f32) | fixup queue (i32) | count
+  return n * (8 + 8 + 4 * kD + 4 + 4 + 4) + 16;
 }
 
 extern "C" int cs_ccpe_decode_bf16(const void* q, int64_t q_s_batch, int64_t q_s_head,
@@ -618,7 +737,12 @@ extern "C" int cs_ccpe_decode_bf16(const void* q, int64_t q_s_batch, int64_t q_s
   CS_REQUIRE(split >= 64 && split <= kMaxSplit && split % 64 == 0,
              "split must be a multiple of 64 in [64, %d]", kMaxSplit);
   CS_REQUIRE(max_nk >= 1, "max_nk must be positive");
+  CS_REQUIRE(batch >= 0, "batch must be non-negative");
   CS_REQUIRE((reinterpret_cast<uintptr_t>(workspace) % 16) == 0, "workspace must be aligned");
+  CS_REQUIRE((reinterpret_cast<uintptr_t>(q) % 16) == 0 && q_s_batch % 8 == 0 && q_s_head % 8 == 0,
+             "query rows must be 16-byte aligned");
+  const int64_t smax = (static_cast<int64_t>(max_nk) + split - 1) / split;
+  CS_REQUIRE(smax * hkv * batch < (int64_t(1) << 31), "too many splits for one launch");
   decode_params p{};
   p.q = static_cast<const uint16_t*>(q);
   p.q_sb = q_s_batch;
@@ -642,12 +766,14 @@ extern "C" int cs_ccpe_decode_bf16(const void* q, int64_t q_s_batch, int64_t q_s
     p.kv.bt_stride = kv->bt_stride;
     p.kv.bt_cols = kv->bt_cols;
     p.kv.bs_shift = -1;
-    for (int s = 0; s < 31; ++s)
-      if ((1 << s) == kv->block_size) p.kv.bs_shift = s;
+    for (int sh = 0; sh < 31; ++sh)
+      if ((1 << sh) == kv->block_size) p.kv.bs_shift = sh;
     CS_REQUIRE(p.kv.bt_cols > 0, "block table needs at least one column");
   } else {
-    CS_REQUIRE(kv->k && kv->v && kv->k_s_tok % 8 == 0 && kv->v_s_tok % 8 == 0 &&
-                   kv->k_s_head % 8 == 0 && kv->v_s_head % 8 == 0,
+    CS_REQUIRE(kv->k && kv->v && (reinterpret_cast<uintptr_t>(kv->k) % 16) == 0 &&
+                   (reinterpret_cast<uintptr_t>(kv->v) % 16) == 0 && kv->k_s_tok % 8 == 0 &&
+                   kv->v_s_tok % 8 == 0 && kv->k_s_head % 8 == 0 && kv->v_s_head % 8 == 0 &&
+                   kv->k_s_batch % 8 == 0 && kv->v_s_batch % 8 == 0,
                "dense K/V rows must be 16-byte aligned");
     p.kv.k = static_cast<const uint16_t*>(kv->k);
     p.kv.v = static_cast<const uint16_t*>(kv->v);
@@ -661,33 +787,29 @@ extern "C" int cs_ccpe_decode_bf16(const void* q, int64_t q_s_batch, int64_t q_s
   p.e = e;
   p.npos = max_positions;
   p.split = split;
-  p.smax = static_cast<int32_t>((static_cast<int64_t>(max_nk) + split - 1) / split);
-  int64_t n = static_cast<int64_t>(batch) * hq * p.smax;
+  p.smax = static_cast<int32_t>(smax);
+  const int64_t n = static_cast<int64_t>(batch) * hq * p.smax;
   char* ws = static_cast<char*>(workspace);
   p.tot = reinterpret_cast<double*>(ws);
-  p.acc = reinterpret_cast<float*>(ws + n * 8);
+  p.carry = p.tot + n;
+  p.acc = reinterpret_cast<float*>(ws + n * 16);
   p.mx = p.acc + n * kD;
   p.sm = p.mx + n;
+  p.work = reinterpret_cast<int32_t*>(p.sm + n);
+  p.work_count = p.work + n;
   p.out = static_cast<uint16_t*>(out);
   p.flags = flags;
   if (batch == 0) return CS_OK;
   hipStream_t s = as_stream(stream);
-  // split 0 exactly; splits >= 1 speculatively; then exact fixups where the
-  // speculation does not hold; then the merge.
-  hipLaunchKernelGGL(decode_split_kernel, dim3(1, hkv, batch), dim3(kThreads), 0, s, p, 0);
-  if (p.smax > 1) {
-    dim3 g(p.smax - 1, hkv, batch);
-    switch (p.group) {
-      case 1: hipLaunchKernelGGL(decode_spec_kernel<1>, g, dim3(kThreads), 0, s, p); break;
-      case 2: hipLaunchKernelGGL(decode_spec_kernel<2>, g, dim3(kThreads), 0, s, p); break;
-      case 3: hipLaunchKernelGGL(decode_spec_kernel<3>, g, dim3(kThreads), 0, s, p); break;
-      case 4: hipLaunchKernelGGL(decode_spec_kernel<4>, g, dim3(kThreads), 0, s, p); break;
-      case 5: hipLaunchKernelGGL(decode_spec_kernel<5>, g, dim3(kThreads), 0, s, p); break;
-      case 6: hipLaunchKernelGGL(decode_spec_kernel<6>, g, dim3(kThreads), 0, s, p); break;
-      case 7: hipLaunchKernelGGL(decode_spec_kernel<7>, g, dim3(kThreads), 0, s, p); break;
-      default: hipLaunchKernelGGL(decode_spec_kernel<8>, g, dim3(kThreads), 0, s, p); break;
-    }
-    hipLaunchKernelGGL(decode_split_kernel, dim3(p.smax, hkv, batch), dim3(kThreads), 0, s, p, 1);
+  switch (p.group) {
+    case 1: launch_split_kernels<1>(p, s); break;
+    case 2: launch_split_kernels<2>(p, s); break;
+    case 3: launch_split_kernels<3>(p, s); break;
+    case 4: launch_split_kernels<4>(p, s); break;
+    case 5: launch_split_kernels<5>(p, s); break;
+    case 6: launch_split_kernels<6>(p, s); break;
+    case 7: launch_split_kernels<7>(p, s); break;
+    default: launch_split_kernels<8>(p, s); break;
   }
   hipLaunchKernelGGL(decode_combine_kernel, dim3(batch * hq), dim3(kD), 0, s, p);
   CS_LAUNCH_CHECK("ccpe_decode");

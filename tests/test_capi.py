@@ -48,4 +48,6 @@ def test_argument_errors_need_no_device():
     status = lib.cs_ccpe_attention(None, None)
     assert status == _hip.CS_EINVAL
     assert b"null" in lib.cs_last_error()
-    assert lib.cs_ccpe_decode_workspace_bytes(2, 4, 1000, 256) == 2 * 4 * 4 * (8 + 4 + 4 + 4 * 128)
+    # per split: gate total and carry (f64), accumulator (128 f32), max, sum,
+    # fixup-queue entry; plus the queue counter
+    assert lib.cs_ccpe_decode_workspace_bytes(2, 4, 1000, 256) == 2 * 4 * 4 * (8 + 8 + 4 * 128 + 4 + 4 + 4) + 16
