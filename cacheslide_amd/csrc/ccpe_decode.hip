@@ -48,6 +48,11 @@ constexpr int kFixupGrid = 1024;
 constexpr float kInvSqrtD = 0.08838834764831845f;  // 1/sqrt(128)
 constexpr float kLog2e = 1.4426950408889634f;
 
+// Masked keys and keys of invalid blocks read this zero record, so every load
+// is issued unconditionally and the compiler can count outstanding loads
+// exactly (a load under a branch makes it wait for all of them).
+__device__ __attribute__((aligned(16))) uint32_t g_zero_record[kD] = {};
+
 struct kv_addr {
   const uint16_t* cache;
   int64_t s_block, s_head, s_offset;
@@ -155,9 +160,11 @@ __device__ inline float dot2(uint32_t a, uint32_t b, float c) {
                                          c, false);
 }
 
-__device__ inline uint4 ld16(const uint16_t* ptr) {
-  return ptr ? *reinterpret_cast<const uint4*>(ptr) : make_uint4(0, 0, 0, 0);
+__device__ inline const uint16_t* zero_record() {
+  return reinterpret_cast<const uint16_t*>(g_zero_record);
 }
+
+__device__ inline uint4 ld16(const uint16_t* ptr) { return *reinterpret_cast<const uint4*>(ptr); }
 
 // Resolve the record offsets of keys [lo, hi) through the block table.
 template <int G>
@@ -181,25 +188,28 @@ __device__ void load_offsets(const decode_params& p, smem_t<G>& s, const split_c
   }
 }
 
-// K / V row of key j (lo <= j < hi), or null for an invalid block.
-template <int G>
+// K / V row of key j, or the zero record when the key is masked (valid is
+// false) or its block is invalid.  Valid keys satisfy lo <= j < hi.
+template <int G, bool PAGED>
 __device__ inline const uint16_t* k_row(const decode_params& p, const smem_t<G>& s,
-                                        const split_ctx& c, int64_t j) {
-  if (p.kv.block_table) {
-    const int64_t o = s.koff[j - c.lo];
-    return o < 0 ? nullptr : p.kv.cache + o;
+                                        const split_ctx& c, int64_t j, bool valid) {
+  if constexpr (PAGED) {
+    const int64_t o = s.koff[valid ? j - c.lo : 0];
+    return valid && o >= 0 ? p.kv.cache + o : zero_record();
+  } else {
+    return valid ? p.kv.k + c.b * p.kv.k_sb + j * p.kv.k_st + c.kvh * p.kv.k_sh : zero_record();
   }
-  return p.kv.k + c.b * p.kv.k_sb + j * p.kv.k_st + c.kvh * p.kv.k_sh;
 }
 
-template <int G>
+template <int G, bool PAGED>
 __device__ inline const uint16_t* v_row(const decode_params& p, const smem_t<G>& s,
-                                        const split_ctx& c, int64_t j) {
-  if (p.kv.block_table) {
-    const int64_t o = s.koff[j - c.lo];
-    return o < 0 ? nullptr : p.kv.cache + o + kD;
+                                        const split_ctx& c, int64_t j, bool valid) {
+  if constexpr (PAGED) {
+    const int64_t o = s.koff[valid ? j - c.lo : 0];
+    return valid && o >= 0 ? p.kv.cache + o + kD : zero_record() + kD;
+  } else {
+    return valid ? p.kv.v + c.b * p.kv.v_sb + j * p.kv.v_st + c.kvh * p.kv.v_sh : zero_record() + kD;
   }
-  return p.kv.v + c.b * p.kv.v_sb + j * p.kv.v_st + c.kvh * p.kv.v_sh;
 }
 
 struct ktile {
@@ -210,27 +220,26 @@ struct vtile {
 };
 
 // K operand of tile t0: lane (g, n) loads key t0 + n, dims 32t + 8g .. +7.
-template <int G>
+// Keys below wlo (tiles past the wave's range included) read zeros.
+template <int G, bool PAGED>
 __device__ inline void load_k(ktile& kt, const decode_params& p, const smem_t<G>& s,
                               const split_ctx& c, int64_t t0, int64_t wlo, int lane) {
   const int g = lane >> 4, n = lane & 15;
   const int64_t j = t0 + n;
-  const uint16_t* row = j >= wlo ? k_row(p, s, c, j) : nullptr;
+  const uint16_t* row = k_row<G, PAGED>(p, s, c, j, j >= wlo);
 #pragma unroll
-  for (int t = 0; t < 4; ++t)
-    kt.a[t] = __builtin_bit_cast(bf16x8, ld16(row ? row + 32 * t + 8 * g : nullptr));
+  for (int t = 0; t < 4; ++t) kt.a[t] = __builtin_bit_cast(bf16x8, ld16(row + 32 * t + 8 * g));
 }
 
 // V of tile t0: lane (g, x) loads keys t0 + 4g + v (v = 0..3), dims 8x .. +7.
-template <int G>
+template <int G, bool PAGED>
 __device__ inline void load_v(vtile& vt, const decode_params& p, const smem_t<G>& s,
                               const split_ctx& c, int64_t t0, int64_t wlo, int lane) {
   const int g = lane >> 4, x = lane & 15;
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const int64_t j = t0 + 4 * g + v;
-    const uint16_t* row = j >= wlo ? v_row(p, s, c, j) : nullptr;
-    vt.v[v] = ld16(row ? row + 8 * x : nullptr);
+    vt.v[v] = ld16(v_row<G, PAGED>(p, s, c, j, j >= wlo) + 8 * x);
   }
 }
 
@@ -395,11 +404,11 @@ __device__ inline void load_q(bf16x8* qb, const decode_params& p, const split_ct
 }
 
 // Speculative split: every position is P-1, the bias the constant QE[P-1].
-template <int G>
+template <int G, bool PAGED>
 __device__ void run_spec(const decode_params& p, smem_t<G>& s, const split_ctx& c, bool& bad) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, n = lane & 15;
-  load_offsets(p, s, c, bad);
+  if constexpr (PAGED) load_offsets(p, s, c, bad);
   bf16x8 qb[4];
   load_q<G>(qb, p, c, lane);
   // QE[P-1] of head n: lane (g, n) sums its 32 dims, then the 4 rows are added
@@ -445,26 +454,20 @@ __device__ void run_spec(const decode_params& p, smem_t<G>& s, const split_ctx& 
     st.tsum += static_cast<double>(tg);
     accumulate(st, x, vt);
   };
+  // tiles in pairs (a masked tile pads an odd count); the loads of the next
+  // tile are always in flight while the current one is consumed
   ktile ka, kb;
   vtile va, vb;
-  if (ntiles > 0) {
-    load_k(ka, p, s, c, whi - kTile, wlo, lane);
-    load_v(va, p, s, c, whi - kTile, wlo, lane);
-  }
+  load_k<G, PAGED>(ka, p, s, c, whi - kTile, wlo, lane);
+  load_v<G, PAGED>(va, p, s, c, whi - kTile, wlo, lane);
   for (int i = 0; i < ntiles; i += 2) {
     const int64_t t0 = whi - static_cast<int64_t>(i + 1) * kTile;
-    if (i + 1 < ntiles) {
-      load_k(kb, p, s, c, t0 - kTile, wlo, lane);
-      load_v(vb, p, s, c, t0 - kTile, wlo, lane);
-    }
+    load_k<G, PAGED>(kb, p, s, c, t0 - kTile, wlo, lane);
+    load_v<G, PAGED>(vb, p, s, c, t0 - kTile, wlo, lane);
     tile(ka, va, t0);
-    if (i + 1 < ntiles) {
-      if (i + 2 < ntiles) {
-        load_k(ka, p, s, c, t0 - 2 * kTile, wlo, lane);
-        load_v(va, p, s, c, t0 - 2 * kTile, wlo, lane);
-      }
-      tile(kb, vb, t0 - kTile);
-    }
+    load_k<G, PAGED>(ka, p, s, c, t0 - 2 * kTile, wlo, lane);
+    load_v<G, PAGED>(va, p, s, c, t0 - 2 * kTile, wlo, lane);
+    tile(kb, vb, t0 - kTile);
   }
   __syncthreads();
   wave_finish(st, s, wave, lane);
@@ -473,12 +476,12 @@ __device__ void run_spec(const decode_params& p, smem_t<G>& s, const split_ctx& 
 
 // Exact split with the given carry per head (s.carry): positions from the
 // gate suffix sums (fp64), bias by interpolation in the QE table.
-template <int G>
+template <int G, bool PAGED>
 __device__ void run_exact(const decode_params& p, smem_t<G>& s, const split_ctx& c, bool write_tot,
                           bool& bad) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, n = lane & 15;
-  load_offsets(p, s, c, bad);
+  if constexpr (PAGED) load_offsets(p, s, c, bad);
   bf16x8 qb[4];
   load_q<G>(qb, p, c, lane);
   for (int i = tid; i < G * kD; i += kThreads) {
@@ -516,15 +519,13 @@ __device__ void run_exact(const decode_params& p, smem_t<G>& s, const split_ctx&
   };
   {
     ktile ka, kb;
-    if (ntiles > 0) load_k(ka, p, s, c, whi - kTile, wlo, lane);
+    load_k<G, PAGED>(ka, p, s, c, whi - kTile, wlo, lane);
     for (int i = 0; i < ntiles; i += 2) {
       const int64_t t0 = whi - static_cast<int64_t>(i + 1) * kTile;
-      if (i + 1 < ntiles) load_k(kb, p, s, c, t0 - kTile, wlo, lane);
+      load_k<G, PAGED>(kb, p, s, c, t0 - kTile, wlo, lane);
       ktile_pass(ka, t0);
-      if (i + 1 < ntiles) {
-        if (i + 2 < ntiles) load_k(ka, p, s, c, t0 - 2 * kTile, wlo, lane);
-        ktile_pass(kb, t0 - kTile);
-      }
+      load_k<G, PAGED>(ka, p, s, c, t0 - 2 * kTile, wlo, lane);
+      ktile_pass(kb, t0 - kTile);
     }
   }
   {
@@ -587,15 +588,13 @@ __device__ void run_exact(const decode_params& p, smem_t<G>& s, const split_ctx&
   };
   {
     vtile va, vb;
-    if (ntiles > 0) load_v(va, p, s, c, whi - kTile, wlo, lane);
+    load_v<G, PAGED>(va, p, s, c, whi - kTile, wlo, lane);
     for (int i = 0; i < ntiles; i += 2) {
       const int64_t t0 = whi - static_cast<int64_t>(i + 1) * kTile;
-      if (i + 1 < ntiles) load_v(vb, p, s, c, t0 - kTile, wlo, lane);
+      load_v<G, PAGED>(vb, p, s, c, t0 - kTile, wlo, lane);
       vtile_pass(va, t0);
-      if (i + 1 < ntiles) {
-        if (i + 2 < ntiles) load_v(va, p, s, c, t0 - 2 * kTile, wlo, lane);
-        vtile_pass(vb, t0 - kTile);
-      }
+      load_v<G, PAGED>(va, p, s, c, t0 - 2 * kTile, wlo, lane);
+      vtile_pass(vb, t0 - kTile);
     }
   }
   __syncthreads();  // the per-wave accumulators overwrite the logits
@@ -606,7 +605,7 @@ __device__ void run_exact(const decode_params& p, smem_t<G>& s, const split_ctx&
 
 // Split 0 of every (request, KV head) exactly, then the speculative splits;
 // the grid is ordered split-major so the exact workgroups start first.
-template <int G>
+template <int G, bool PAGED>
 __global__ void __launch_bounds__(kThreads) decode_main_kernel(decode_params p) {
   __shared__ smem_t<G> s;
   const int per_r = p.hkv * p.batch;
@@ -619,9 +618,9 @@ __global__ void __launch_bounds__(kThreads) decode_main_kernel(decode_params p) 
   bool bad = false;
   if (r == 0) {
     if (threadIdx.x < G) s.carry[threadIdx.x] = 0.0;
-    run_exact<G>(p, s, c, true, bad);
+    run_exact<G, PAGED>(p, s, c, true, bad);
   } else {
-    run_spec<G>(p, s, c, bad);
+    run_spec<G, PAGED>(p, s, c, bad);
   }
   if (bad) atomicOr(p.flags, CS_FLAG_BLOCK_INVALID);
 }
@@ -655,7 +654,7 @@ __global__ void decode_plan_kernel(decode_params p) {
   }
 }
 
-template <int G>
+template <int G, bool PAGED>
 __global__ void __launch_bounds__(kThreads) decode_fixup_kernel(decode_params p) {
   __shared__ smem_t<G> s;
   const int count = *p.work_count;
@@ -668,7 +667,7 @@ __global__ void __launch_bounds__(kThreads) decode_fixup_kernel(decode_params p)
     if (!make_ctx(p, b, kvh, r, c)) continue;
     if (threadIdx.x < G) s.carry[threadIdx.x] = p.carry[ws_index(p, b, c.h0 + threadIdx.x, r)];
     __syncthreads();
-    run_exact<G>(p, s, c, false, bad);
+    run_exact<G, PAGED>(p, s, c, false, bad);
     __syncthreads();
   }
   if (bad) atomicOr(p.flags, CS_FLAG_BLOCK_INVALID);
@@ -696,18 +695,26 @@ __global__ void decode_combine_kernel(decode_params p) {
   p.out[static_cast<int64_t>(b) * p.hq * kD + h * kD + d] = float_to_bf16(val);
 }
 
-template <int G>
+template <int G, bool PAGED>
 void launch_split_kernels(const decode_params& p, hipStream_t s) {
   const int64_t main_grid = static_cast<int64_t>(p.smax) * p.hkv * p.batch;
-  hipLaunchKernelGGL(decode_main_kernel<G>, dim3(static_cast<uint32_t>(main_grid)), dim3(kThreads), 0,
-                     s, p);
+  hipLaunchKernelGGL((decode_main_kernel<G, PAGED>), dim3(static_cast<uint32_t>(main_grid)),
+                     dim3(kThreads), 0, s, p);
   if (p.smax > 1) {
     hipLaunchKernelGGL(decode_plan_kernel, dim3(p.hkv * p.batch), dim3(64), 0, s, p);
     int64_t fix = static_cast<int64_t>(p.smax - 1) * p.hkv * p.batch;
     if (fix > kFixupGrid) fix = kFixupGrid;
-    hipLaunchKernelGGL(decode_fixup_kernel<G>, dim3(static_cast<uint32_t>(fix)), dim3(kThreads), 0, s,
-                       p);
+    hipLaunchKernelGGL((decode_fixup_kernel<G, PAGED>), dim3(static_cast<uint32_t>(fix)),
+                       dim3(kThreads), 0, s, p);
   }
+}
+
+template <int G>
+void launch_group(const decode_params& p, hipStream_t s) {
+  if (p.kv.block_table)
+    launch_split_kernels<G, true>(p, s);
+  else
+    launch_split_kernels<G, false>(p, s);
 }
 
 }  // namespace
@@ -802,14 +809,14 @@ extern "C" int cs_ccpe_decode_bf16(const void* q, int64_t q_s_batch, int64_t q_s
   if (batch == 0) return CS_OK;
   hipStream_t s = as_stream(stream);
   switch (p.group) {
-    case 1: launch_split_kernels<1>(p, s); break;
-    case 2: launch_split_kernels<2>(p, s); break;
-    case 3: launch_split_kernels<3>(p, s); break;
-    case 4: launch_split_kernels<4>(p, s); break;
-    case 5: launch_split_kernels<5>(p, s); break;
-    case 6: launch_split_kernels<6>(p, s); break;
-    case 7: launch_split_kernels<7>(p, s); break;
-    default: launch_split_kernels<8>(p, s); break;
+    case 1: launch_group<1>(p, s); break;
+    case 2: launch_group<2>(p, s); break;
+    case 3: launch_group<3>(p, s); break;
+    case 4: launch_group<4>(p, s); break;
+    case 5: launch_group<5>(p, s); break;
+    case 6: launch_group<6>(p, s); break;
+    case 7: launch_group<7>(p, s); break;
+    default: launch_group<8>(p, s); break;
   }
   hipLaunchKernelGGL(decode_combine_kernel, dim3(batch * hq), dim3(kD), 0, s, p);
   CS_LAUNCH_CHECK("ccpe_decode");
