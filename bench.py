@@ -186,7 +186,7 @@ def decode_measure(device, steps: int, warmup: int):
     from cacheslide_amd import CoPE, _hip
     from cacheslide_amd.ccpe import _paged_source, decode_workspace
 
-    B, CTX, HQ, HKV, D, P, BS, SPLIT = 64, 32769, 32, 8, 128, 64, 16, 512
+    B, CTX, HQ, HKV, D, P, BS, SPLIT = 64, 32769, 32, 8, 128, 64, 16, 1024
     per = (CTX + BS - 1) // BS
     nblocks = B * per
     gen = torch.Generator(device=device).manual_seed(5005)
@@ -219,7 +219,7 @@ def decode_measure(device, steps: int, warmup: int):
     torch.cuda.empty_cache()
     return {
         "workload": "ccpe_decode_paged: 64 requests x 32769 keys, 32q/8kv heads, head_dim 128, "
-                    "P=64, block 16, split 512, one layer of distinct KV",
+                    "P=64, block 16, split 1024, one layer of distinct KV",
         "ms_per_call": round(ms, 4),
         "kv_bytes_per_call": kv_bytes,
         "achieved_GBs": round(gbs, 1),

@@ -131,7 +131,7 @@ def ccpe_decode_paged(
     cope,
     *,
     max_context: int | None = None,
-    split: int = 512,
+    split: int = 1024,
     workspace: Tensor | None = None,
     check: bool = True,
 ) -> Tensor:

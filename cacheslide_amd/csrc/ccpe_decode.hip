@@ -625,28 +625,53 @@ __global__ void __launch_bounds__(kThreads) decode_main_kernel(decode_params p) 
   if (bad) atomicOr(p.flags, CS_FLAG_BLOCK_INVALID);
 }
 
-// Carry of every split (fp64 sum of the totals to its right, in split order)
-// and the queue of splits whose carry is below P-1 for some head.
-__global__ void decode_plan_kernel(decode_params p) {
+// Carry of every split (fp64 exclusive scan of the split totals, from the
+// right-most split) and the queue of splits whose carry is below P-1 for some
+// head.  One workgroup per (request, KV head); splits in chunks of 256.
+constexpr int kPlanThreads = 256;
+
+__global__ void __launch_bounds__(kPlanThreads) decode_plan_kernel(decode_params p) {
+  __shared__ double chunk_sum[kPlanThreads / 64];
   const int b = blockIdx.x / p.hkv, kvh = blockIdx.x % p.hkv;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nk = p.nk[b];
   int splits = (nk + p.split - 1) / p.split;
   if (splits > p.smax) splits = p.smax;
   const int G = p.group, h0 = kvh * G;
   const double top = static_cast<double>(p.npos - 1);
-  if (static_cast<int>(threadIdx.x) < G) {
-    const int h = h0 + threadIdx.x;
-    double carry = 0.0;
-    for (int r = 0; r < splits; ++r) {
-      const int64_t wi = ws_index(p, b, h, r);
-      p.carry[wi] = carry;
-      carry += p.tot[wi];
-    }
-  }
-  __syncthreads();
-  for (int r = 1 + threadIdx.x; r < splits; r += blockDim.x) {
+  double carry_in[kMaxGroup];
+#pragma unroll
+  for (int h = 0; h < kMaxGroup; ++h) carry_in[h] = 0.0;
+  for (int base = 0; base < splits; base += kPlanThreads) {
+    const int r = base + tid;
     bool need = false;
-    for (int h = 0; h < G; ++h) need |= p.carry[ws_index(p, b, h0 + h, r)] < top;
+#pragma unroll
+    for (int h = 0; h < kMaxGroup; ++h) {
+      if (h >= G) continue;
+      const int64_t wi = ws_index(p, b, h0 + h, r < splits ? r : 0);
+      const double v = r < splits ? p.tot[wi] : 0.0;
+      double x = v;  // inclusive scan within the wave
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const double y = __shfl_up(x, off, 64);
+        if (lane >= off) x += y;
+      }
+      double excl = __shfl_up(x, 1, 64);
+      if (lane == 0) excl = 0.0;
+      if (lane == 63) chunk_sum[wave] = x;
+      __syncthreads();
+      double before = carry_in[h];
+      for (int w = 0; w < wave; ++w) before += chunk_sum[w];
+      excl += before;
+      double total = 0.0;
+      for (int w = 0; w < kPlanThreads / 64; ++w) total += chunk_sum[w];
+      __syncthreads();
+      carry_in[h] += total;
+      if (r < splits) {
+        p.carry[wi] = excl;
+        need |= r >= 1 && excl < top;
+      }
+    }
     if (need) {
       const int slot = atomicAdd(p.work_count, 1);
       p.work[slot] = (b * p.hkv + kvh) * p.smax + r;
@@ -673,24 +698,51 @@ __global__ void __launch_bounds__(kThreads) decode_fixup_kernel(decode_params p)
   if (bad) atomicOr(p.flags, CS_FLAG_BLOCK_INVALID);
 }
 
-__global__ void decode_combine_kernel(decode_params p) {
+// Merge of the split partials of one (request, query head): 128 threads,
+// thread d owns output dim d; split weights are formed 128 at a time in LDS.
+__global__ void __launch_bounds__(kD) decode_combine_kernel(decode_params p) {
+  __shared__ float wgt[kD];
+  __shared__ float red[kD / 64];
   const int bh = blockIdx.x;
   const int b = bh / p.hq, h = bh % p.hq;
-  const int d = threadIdx.x;  // 128 threads
+  const int d = threadIdx.x, lane = d & 63, wave = d >> 6;
   const int nk = p.nk[b];
   int splits = (nk + p.split - 1) / p.split;
   if (splits > p.smax) splits = p.smax;
+  const int64_t w0 = ws_index(p, b, h, 0);
   float M = -INFINITY;
-  for (int r = 0; r < splits; ++r) M = fmaxf(M, p.mx[ws_index(p, b, h, r)]);
+  for (int r = d; r < splits; r += kD) M = fmaxf(M, p.mx[w0 + r]);
+  M = wave_max(M);
+  if (lane == 0) red[wave] = M;
+  __syncthreads();
+  M = fmaxf(red[0], red[1]);
+  __syncthreads();
   float L = 0.f, O = 0.f;
-  for (int r = 0; r < splits; ++r) {
-    const int64_t wi = ws_index(p, b, h, r);
-    const float m = p.mx[wi];
-    if (m == -INFINITY) continue;
-    const float f = __builtin_amdgcn_exp2f(m - M);
-    L += p.sm[wi] * f;
-    O += p.acc[wi * kD + d] * f;
+  for (int base = 0; base < splits; base += kD) {
+    const int r = base + d;
+    float f = 0.f;
+    if (r < splits) {
+      const float m = p.mx[w0 + r];
+      f = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
+      L += p.sm[w0 + r] * f;
+    }
+    wgt[d] = f;
+    __syncthreads();
+    const int n = splits - base < kD ? splits - base : kD;
+    const float* acc = p.acc + (w0 + base) * kD + d;
+    int i = 0;
+    for (; i + 4 <= n; i += 4) {
+      const float a0 = acc[(i + 0) * kD], a1 = acc[(i + 1) * kD];
+      const float a2 = acc[(i + 2) * kD], a3 = acc[(i + 3) * kD];
+      O += wgt[i] * a0 + wgt[i + 1] * a1 + wgt[i + 2] * a2 + wgt[i + 3] * a3;
+    }
+    for (; i < n; ++i) O += wgt[i] * acc[i * kD];
+    __syncthreads();
   }
+  L = wave_sum(L);
+  if (lane == 0) red[wave] = L;
+  __syncthreads();
+  L = red[0] + red[1];
   const float val = L > 0.f ? O / L : 0.f;
   p.out[static_cast<int64_t>(b) * p.hq * kD + h * kD + d] = float_to_bf16(val);
 }
@@ -701,7 +753,7 @@ void launch_split_kernels(const decode_params& p, hipStream_t s) {
   hipLaunchKernelGGL((decode_main_kernel<G, PAGED>), dim3(static_cast<uint32_t>(main_grid)),
                      dim3(kThreads), 0, s, p);
   if (p.smax > 1) {
-    hipLaunchKernelGGL(decode_plan_kernel, dim3(p.hkv * p.batch), dim3(64), 0, s, p);
+    hipLaunchKernelGGL(decode_plan_kernel, dim3(p.hkv * p.batch), dim3(kPlanThreads), 0, s, p);
     int64_t fix = static_cast<int64_t>(p.smax - 1) * p.hkv * p.batch;
     if (fix > kFixupGrid) fix = kFixupGrid;
     hipLaunchKernelGGL((decode_fixup_kernel<G, PAGED>), dim3(static_cast<uint32_t>(fix)),
