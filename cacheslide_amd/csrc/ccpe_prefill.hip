@@ -1,4 +1,4 @@
-// CCPE prefill attention on bf16 MFMA (gfx950 v_mfma_f32_16x16x32_bf16).
+// CCPE prefill attention on bf16 MFMA (gfx950 v_mfma_f32_32x32x16_bf16).
 //
 // Computes, for every query row r (position qpos[r]) and query head h,
 //   logit_j   = (q . k_j) / sqrt(128)                       position.py:157-164
@@ -10,24 +10,34 @@
 //                                                           position.py:518-550
 // for keys 0..nk-1 (the cope_attention default key_positions = arange).
 //
-// Work decomposition.  A workgroup of 8 wavefronts owns 32 query rows x 4
-// query heads of one GQA group (64 x 2 or 128 x 1 for group sizes 2 and 1);
-// each wave owns 16 (row, head) pairs and all 8 waves share the K / V^T tile
-// staged in LDS.  Key tiles of 64 are walked from the right-most causal key
-// leftwards; each row carries the gate mass of the keys already visited, and
-// once every row of a wave carries >= P-1 its remaining tiles are saturated
-// (p = P-1, bias = QE[P-1]) and the sigmoid / scan / lerp work is skipped.
+// Softmax is invariant to a per-row constant, so the kernel adds
+// bias_j - QE[P-1] instead of bias_j: keys whose position saturates at P-1
+// add nothing, and a tile whose columns all carry gate mass >= P-1 is plain
+// attention.
 //
-// MFMA data layout (16x16x32 bf16, lane l, g = l / 16, n = l % 16):
-//   A[m][k]: lane holds row m = n, k = 8g .. 8g+7
-//   B[k][n]: lane holds col n,     k = 8g .. 8g+7
-//   C[m][n]: lane holds col n,     rows 4g .. 4g+3
-// S^T = K Q^T puts the query row on the lane (n) and keys on the registers:
-// lane group g of M-tile mt holds keys 16 mt + 4g .. +3, so the online-softmax
-// statistics are per-lane scalars shared by the 4 lanes n, n+16, n+32, n+48.
-// For O^T = V^T P^T the 32 keys of a k-step are ordered so that lane group g
-// supplies the 8 S^T values it already holds (keys 32t + 4g + 0..3 and
-// 32t + 16 + 4g + 0..3); V^T, staged transposed in LDS, is read in that order.
+// Work decomposition.  A workgroup of 4 wavefronts owns 128 (row, head)
+// columns of one GQA group: 128/G rows x the G query heads of one KV head
+// (column c = row_local * G + head_local); each wave owns 32 columns.  Key
+// tiles of 32 are walked from the right-most causal key leftwards through two
+// LDS stages filled by direct global->LDS loads (global_load_lds_dwordx4),
+// one tile ahead.
+//
+// MFMA layout (32x32x16 bf16, lane l, n = l % 32, h = l / 32):
+//   A[m][k]: lane holds row m = n, k = 8h .. 8h+7
+//   B[k][n]: lane holds col n,     k = 8h .. 8h+7
+//   C[m][n]: lane holds col n,     rows 8(v/4) + 4h + v%4, v = 0..15
+// S^T = K Q^T puts the column on the lane and the 32 keys of the tile on the
+// 16 accumulator registers (runs of 4 keys alternating between h = 0 and 1),
+// so the online-softmax statistics are per-lane scalars shared by lanes n and
+// n + 32.  O^T = V^T P^T takes P^T straight from those registers: k-step ks
+// uses keys 16ks + 4h + 0..3 and 16ks + 8 + 4h + 0..3 as k = 8h .. 8h+7, and
+// the V^T operand is read in the same order from the row-major V tile with
+// ds_read_b64_tr_b16 (lane i of a 16-lane group receives element i of the
+// four 4-element rows addressed by lanes 4e .. 4e+3).
+//
+// LDS tiles are XOR-swizzled by 16-byte chunk: K chunk c of key k sits at
+// c ^ (k % 16) (conflict-free MFMA A reads of 16 keys x one chunk), V chunk c
+// at c ^ 2(k % 4) (conflict-free transposed reads of 4 keys x 2 chunks).
 
 #include "common.h"
 
@@ -36,20 +46,33 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4_tr;
+#define CS_LDS __attribute__((address_space(3)))
 
-constexpr int kD = 128;          // head dim (K and V)
-constexpr int kTileN = 64;       // keys per tile
-constexpr int kWaves = 8;
+constexpr int kD = 128;
+constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kRows = 16;              // (row, head) pairs per wave
-constexpr int kKStride = kD + 8;       // bf16 per K row in LDS (272 B)
-constexpr int kVStride = kTileN + 8;   // bf16 per V^T row in LDS (144 B)
-// The per-wave QE tables live in LDS next to the K / V^T tiles; P <= 128 keeps
-// the workgroup at <= 102 KB, under the 160 KB a gfx950 workgroup may use.
+constexpr int kCols = 32;                // (row, head) columns per wave
+constexpr int kWgCols = kCols * kWaves;  // per workgroup
+constexpr int kTileN = 32;               // keys per tile
+constexpr int kChunks = 16;              // 16-byte chunks of a 256-byte K or V row
+constexpr int kStageSlots = kTileN * kChunks;  // uint4 slots of one K (or V) stage
 constexpr int kMaxPos = 128;
-constexpr size_t kStaticLds = sizeof(uint16_t) * (kTileN * kKStride + kD * kVStride) + 32;
+constexpr int kPosChunk = 64;  // E^T positions staged per pass (bf16 hi and lo, 16 KB each)
+constexpr int kBtWindow = 1024;  // block-table entries held in LDS at a time
+constexpr size_t kStaticLds = 4 * kStageSlots * 16 + 4 * kBtWindow + 16;
 constexpr size_t kLdsLimit = 160 * 1024;
+constexpr float kInvSqrtD = 0.08838834764831845f;  // 1/sqrt(128)
+constexpr float kLog2e = 1.4426950408889634f;
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
+// vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt[5:4] in [15:14]).
+constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// Keys past the causal range and keys of invalid blocks are loaded from this
+// zero record (256 bf16), so every tile load is issued unconditionally.
+__device__ __attribute__((aligned(16))) uint32_t g_zero_record[kD] = {};
 
 struct kv_addr {
   const uint16_t* cache;
@@ -68,360 +91,381 @@ struct prefill_params {
   int64_t q_sb, q_st, q_sh;
   const int64_t* qpos;
   int64_t qpos_sb;
-  int32_t batch, nq, hq, hkv, group, heads_per_wg, row_blocks;
+  int32_t batch, nq, hq, hkv, group, rows_per_wg, row_blocks, total_wg;
   const int32_t* nk;
   kv_addr kv;
   const float* e;
-  int32_t npos, pos_tiles, tab_stride;
+  int32_t npos, tab_stride;
   uint16_t* out;
   int32_t* flags;
-  int32_t total_wg;
 };
 
-__device__ inline bf16x8 as_bf16x8(uint4 u) {
-  bf16x8 r;
-  __builtin_memcpy(&r, &u, 16);
-  return r;
+__device__ inline bf16x8 as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
+
+// Direct global -> LDS load of 16 bytes per lane: lane i's bytes land at
+// lds_base + 16 i (lds_base wave-uniform).  Issued through inline assembly so
+// the compiler does not tie later LDS reads to it; completion is made visible
+// only by the explicit vmcnt wait and barrier of the tile loop.
+__device__ inline void lds_dma16(const void* gptr, const void* lds_base) {
+  const uint32_t base = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((CS_LDS const void*)lds_base)));
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" : : "s"(base), "v"(gptr)
+               : "memory", "m0");
 }
 
-// Flat workgroup id -> (batch, kv head, head group, row block).  Dispatch is
-// round-robin over the 8 XCDs by id, so contiguous logical ranges are spread as
-// one per XCD: a (batch, kv head)'s K/V stays in one XCD's L2.  The heaviest
+// Flat workgroup id -> (batch, kv head, row block).  Dispatch is round-robin
+// over the 8 XCDs by id, so contiguous logical ranges are spread as one per
+// XCD: a (batch, kv head)'s K/V stays in one XCD's L2.  The heaviest
 // (right-most) row blocks go first.
-__device__ inline void decode_wg(const prefill_params& p, int& b, int& kvh, int& hg, int& rb) {
+__device__ inline void decode_wg(const prefill_params& p, int& b, int& kvh, int& rb) {
   const int id = blockIdx.x;
   int logical = id;
   if (p.total_wg % 8 == 0) logical = (id % 8) * (p.total_wg / 8) + id / 8;
-  const int hgroups = p.group / p.heads_per_wg;
   rb = p.row_blocks - 1 - (logical % p.row_blocks);
-  int rest = logical / p.row_blocks;
-  hg = rest % hgroups;
-  rest /= hgroups;
+  const int rest = logical / p.row_blocks;
   kvh = rest % p.hkv;
   b = rest / p.hkv;
 }
 
+// First element of key j's K (kpart) or V row, or null if its block is invalid.
+template <bool PAGED>
+__device__ inline const uint16_t* key_row(const prefill_params& p, int b, int kvh, int64_t j,
+                                          int32_t blk, bool kpart) {
+  if constexpr (PAGED) {
+    if (blk < 0 || blk >= p.kv.num_blocks) return nullptr;
+    const int64_t off = j & ((int64_t(1) << p.kv.bs_shift) - 1);
+    return p.kv.cache + blk * p.kv.s_block + kvh * p.kv.s_head + off * p.kv.s_offset +
+           (kpart ? 0 : kD);
+  } else {
+    return kpart ? p.kv.k + b * p.kv.k_sb + j * p.kv.k_st + kvh * p.kv.k_sh
+                 : p.kv.v + b * p.kv.v_sb + j * p.kv.v_st + kvh * p.kv.v_sh;
+  }
+}
+
+
+struct stage_t {
+  uint4 k[kStageSlots];
+  uint4 v[kStageSlots];
+};
+
+template <bool PAGED>
 __global__ void __launch_bounds__(kThreads, 2) ccpe_prefill_kernel(prefill_params p) {
-  __shared__ __align__(16) uint16_t k_lds[kTileN * kKStride];
-  __shared__ __align__(16) uint16_t v_lds[kD * kVStride];
+  __shared__ __align__(16) stage_t st0;
+  __shared__ __align__(16) stage_t st1;
+  __shared__ int32_t bt_lds[kBtWindow];  // block ids of blocks [bt_lo, bt_lo + kBtWindow)
   __shared__ int64_t wg_max_pos;
-  extern __shared__ __align__(16) float tab_lds[];  // [kWaves][16][tab_stride]
+  extern __shared__ __align__(16) float tab[];  // [kWgCols][tab_stride]: (QE - QE[P-1]) log2e
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int g = lane >> 4;   // lane group: keys 4g..4g+3 of each 16-key M-tile
-  const int ln = lane & 15;  // this lane's (row, head) pair within the wave
+  const int n = lane & 31;  // column within the wave
+  const int h = lane >> 5;  // k half of the MFMA operands
 
-  int b, kvh, hg, rb;
-  decode_wg(p, b, kvh, hg, rb);
-  const int head_slot = wave % p.heads_per_wg;
-  const int row_sub = wave / p.heads_per_wg;
-  const int h = kvh * p.group + hg * p.heads_per_wg + head_slot;
-  const int wg_rows = kRows * (kWaves / p.heads_per_wg);
-  const int r = rb * wg_rows + row_sub * kRows + ln;
-  const bool row_ok = r < p.nq;
+  int b, kvh, rb;
+  decode_wg(p, b, kvh, rb);
+  const int c = wave * kCols + n;  // column within the workgroup
+  const int row = rb * p.rows_per_wg + c / p.group;
+  const int head = kvh * p.group + c % p.group;
+  const bool row_ok = row < p.nq;
   const int nk = p.nk[b];
-  const int64_t qp = row_ok ? p.qpos[b * p.qpos_sb + r] : -1;
+  const int64_t qp = row_ok ? p.qpos[b * p.qpos_sb + row] : -1;
 
   if (tid == 0) wg_max_pos = 0;
   __syncthreads();
-  // wave extremes of the query positions (for the key range and masking)
   int64_t wmax = qp, wmin = row_ok ? qp : INT64_MAX;
   for (int off = 32; off > 0; off >>= 1) {
     const int64_t a = __shfl_xor(wmax, off, 64);
-    const int64_t c = __shfl_xor(wmin, off, 64);
+    const int64_t d = __shfl_xor(wmin, off, 64);
     wmax = a > wmax ? a : wmax;
-    wmin = c < wmin ? c : wmin;
+    wmin = d < wmin ? d : wmin;
   }
-  if (lane == 0)
-    atomicMax(reinterpret_cast<unsigned long long*>(&wg_max_pos),
-              static_cast<unsigned long long>(wmax < 0 ? 0 : wmax));
-  __syncthreads();
-  const int64_t kend = (wg_max_pos + 1) < nk ? (wg_max_pos + 1) : nk;  // keys [0, kend)
+  if (lane == 0 && wmax >= 0)
+    atomicMax(reinterpret_cast<unsigned long long*>(&wg_max_pos), static_cast<unsigned long long>(wmax));
 
-  // ---- Q as the B operand of S^T: 4 k-steps x 8 bf16 ------------------------
-  bf16x8 qreg[4];
+  // ---- Q^T as the B operand of S^T: 8 k-steps of 16 dims ---------------------
+  bf16x8 qb[8];
   {
-    const uint16_t* qrow = p.q + b * p.q_sb + static_cast<int64_t>(row_ok ? r : 0) * p.q_st + h * p.q_sh;
+    const uint16_t* qrow = p.q + b * p.q_sb + static_cast<int64_t>(row_ok ? row : 0) * p.q_st + head * p.q_sh;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const uint4 u = row_ok ? *reinterpret_cast<const uint4*>(qrow + 32 * s + 8 * g)
-                             : make_uint4(0, 0, 0, 0);
-      qreg[s] = as_bf16x8(u);
+    for (int ks = 0; ks < 8; ++ks) {
+      const uint4 u = row_ok ? *reinterpret_cast<const uint4*>(qrow + 16 * ks + 8 * h) : make_uint4(0, 0, 0, 0);
+      qb[ks] = as_bf16x8(u);
     }
   }
 
-  // ---- QE table: QE^T = E^T Q^T, E split into bf16 hi + lo (~fp32 product) ----
-  float* tab = tab_lds + wave * kRows * p.tab_stride;
-  for (int pt = 0; pt < p.pos_tiles; ++pt) {
-    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-    const int pos = pt * 16 + ln;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      bf16x8 ahi, alo;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float ev = pos < p.npos ? p.e[(32 * s + 8 * g + i) * p.npos + pos] : 0.f;
-        const __bf16 hb = static_cast<__bf16>(ev);
-        ahi[i] = hb;
-        alo[i] = static_cast<__bf16>(ev - static_cast<float>(hb));
-      }
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ahi, qreg[s], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(alo, qreg[s], acc, 0, 0, 0);
+  // ---- QE table: QE^T = E^T Q^T on MFMA, E split into bf16 hi + lo ------------
+  // E^T hi / lo for kPosChunk positions are staged in the (still unused) K / V
+  // stages, swizzled like K: chunk c of position pos at c ^ (pos % 16).
+  uint16_t* ehi = reinterpret_cast<uint16_t*>(&st0);  // [64 pos][128 dims], 16 KB
+  uint16_t* elo = reinterpret_cast<uint16_t*>(&st1);
+  float* tcol = tab + c * p.tab_stride;
+  for (int pc = 0; pc < p.npos; pc += kPosChunk) {
+    __syncthreads();
+    for (int i = tid; i < kPosChunk * kD; i += kThreads) {
+      const int pos = i % kPosChunk, d = i / kPosChunk;  // consecutive threads: consecutive positions
+      const float ev = pc + pos < p.npos ? p.e[d * p.npos + pc + pos] : 0.f;
+      const __bf16 hb = static_cast<__bf16>(ev);
+      const __bf16 lb = static_cast<__bf16>(ev - static_cast<float>(hb));
+      const int slot = pos * kChunks + ((d >> 3) ^ (pos & 15));
+      ehi[slot * 8 + (d & 7)] = __builtin_bit_cast(uint16_t, hb);
+      elo[slot * 8 + (d & 7)] = __builtin_bit_cast(uint16_t, lb);
     }
+    __syncthreads();
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int posv = pt * 16 + 4 * g + v;
-      if (posv < p.npos) tab[ln * p.tab_stride + posv] = acc[v];
+    for (int pb = 0; pb < kPosChunk / 32; ++pb) {
+      if (pc + 32 * pb >= p.npos) break;
+      floatx16 acc = {};
+      const int pos = 32 * pb + n;
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        const int slot = pos * kChunks + ((2 * ks + h) ^ (pos & 15));
+        const bf16x8 ah = as_bf16x8(*reinterpret_cast<const uint4*>(ehi + slot * 8));
+        const bf16x8 al = as_bf16x8(*reinterpret_cast<const uint4*>(elo + slot * 8));
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, qb[ks], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, qb[ks], acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int pv = pc + 32 * pb + 8 * (v >> 2) + 4 * h + (v & 3);
+        if (pv < p.npos) tcol[pv] = acc[v];
+      }
     }
   }
   __syncthreads();
-  const float* trow = tab + ln * p.tab_stride;
-  const float top = static_cast<float>(p.npos - 1);
-  const float kLog2e = 1.4426950408889634f;
-  const float logit_scale = 0.08838834764831845f;  // 1/sqrt(128)
-  const float sat_bias2 = trow[p.npos - 1] * kLog2e;
-
-  // ---- main loop --------------------------------------------------------------
-  float carry = row_ok ? 0.f : 3.0e38f;  // padded rows count as saturated
-  float m_run = -INFINITY;                // running max (log2 domain), per row
-  float l_run = 0.f;                      // this lane's share of the row sum
-  floatx4 o[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) o[i] = floatx4{0.f, 0.f, 0.f, 0.f};
-
-  // Global -> register staging: threads [0, 256) stage K (4 x 16 B), threads
-  // [256, 512) stage V as 4 keys x 8 dims for the transposed store.
-  uint4 st[4];
-  bool bad_block = false;
-  const bool k_stager = tid < 256;
-  const int sid = tid & 255;
-  // key (within a tile) and 16-byte chunk of this thread's staging slot rr
-  auto slot_key = [&](int rr) { return k_stager ? ((sid + 256 * rr) >> 4) : 4 * (sid >> 4) + rr; };
-  const int slot_dc = k_stager ? (sid & 15) : (sid & 15);
-  // Block ids of the next tile to load are fetched one tile earlier, so each
-  // iteration issues only the K/V loads (one global round trip, overlapped
-  // with the current tile's compute).
-  int32_t bid[4] = {0, 0, 0, 0};
-  auto fetch_blocks = [&](int64_t base) {
-    if (!p.kv.block_table) return;
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int64_t j = base + slot_key(rr);
-      bid[rr] = -1;
-      if (j < kend) {
-        const int64_t bi = p.kv.bs_shift >= 0 ? (j >> p.kv.bs_shift) : j / p.kv.block_size;
-        if (bi < p.kv.bt_cols) bid[rr] = p.kv.block_table[b * p.kv.bt_stride + bi];
-      }
-    }
-  };
-  auto load_tile = [&](int64_t base) {
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int64_t j = base + slot_key(rr);
-      st[rr] = make_uint4(0, 0, 0, 0);
-      if (j < kend) {
-        const uint16_t* row = nullptr;
-        if (p.kv.block_table) {
-          const int32_t blk = bid[rr];
-          if (blk < 0 || blk >= p.kv.num_blocks) {
-            bad_block = true;
-          } else {
-            const int64_t off = p.kv.bs_shift >= 0 ? (j & ((int64_t(1) << p.kv.bs_shift) - 1))
-                                                   : j % p.kv.block_size;
-            row = p.kv.cache + blk * p.kv.s_block + kvh * p.kv.s_head + off * p.kv.s_offset +
-                  (k_stager ? 0 : kD);
-          }
-        } else {
-          row = k_stager ? p.kv.k + b * p.kv.k_sb + j * p.kv.k_st + kvh * p.kv.k_sh
-                         : p.kv.v + b * p.kv.v_sb + j * p.kv.v_st + kvh * p.kv.v_sh;
-        }
-        if (row) st[rr] = *reinterpret_cast<const uint4*>(row + 8 * slot_dc);
-      }
-    }
-  };
-  auto store_tile = [&]() {
-    if (k_stager) {
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int c = sid + 256 * rr;
-        *reinterpret_cast<uint4*>(&k_lds[(c >> 4) * kKStride + 8 * (c & 15)]) = st[rr];
-      }
-    } else {
-      const int dc = sid & 15, kg = sid >> 4;
-      const uint16_t* e0 = reinterpret_cast<const uint16_t*>(&st[0]);
-      const uint16_t* e1 = reinterpret_cast<const uint16_t*>(&st[1]);
-      const uint16_t* e2 = reinterpret_cast<const uint16_t*>(&st[2]);
-      const uint16_t* e3 = reinterpret_cast<const uint16_t*>(&st[3]);
-#pragma unroll
-      for (int d = 0; d < 8; ++d) {
-        uint2 w;
-        w.x = static_cast<uint32_t>(e0[d]) | (static_cast<uint32_t>(e1[d]) << 16);
-        w.y = static_cast<uint32_t>(e2[d]) | (static_cast<uint32_t>(e3[d]) << 16);
-        *reinterpret_cast<uint2*>(&v_lds[(8 * dc + d) * kVStride + 4 * kg]) = w;
-      }
-    }
-  };
-
-  const int64_t ntiles = (kend + kTileN - 1) / kTileN;
-  if (ntiles > 0) {
-    fetch_blocks((ntiles - 1) * kTileN);
-    load_tile((ntiles - 1) * kTileN);
-    if (ntiles > 1) fetch_blocks((ntiles - 2) * kTileN);
+  {
+    const float top_qe = tcol[p.npos - 1];
+    for (int pv = h; pv < p.npos; pv += 2) tcol[pv] = (tcol[pv] - top_qe) * kLog2e;
   }
-  for (int64_t t = ntiles - 1; t >= 0; --t) {
-    const int64_t base = t * kTileN;
-    __syncthreads();
-    store_tile();
-    __syncthreads();
-    if (t > 0) load_tile((t - 1) * kTileN);
-    if (t > 1) fetch_blocks((t - 2) * kTileN);
 
-    // Waves whose rows all precede the tile contribute nothing to it.
-    if (base > wmax) continue;
+  const int64_t wgmax = wg_max_pos;
+  const int64_t kend = wgmax + 1 < nk ? wgmax + 1 : (nk > 0 ? nk : 0);  // keys [0, kend)
+  const int ntiles = static_cast<int>((kend + kTileN - 1) / kTileN);
 
-    // S^T for the four 16-key M-tiles: sacc[mt][v] = key 16 mt + 4g + v.
-    floatx4 sacc[4];
+  // ---- block ids: the table entries of a window of tiles are copied to LDS
+  // before the window's tile loop, so that loop issues no vector-memory
+  // operation other than the tile loads themselves.
+  int64_t bt_lo = 0;
+  auto load_window = [&](int tlo, int thi) {  // blocks of keys [32 tlo, 32 thi)
+    const int64_t blo = (static_cast<int64_t>(tlo) * kTileN) >> p.kv.bs_shift;
+    const int64_t bhi = (static_cast<int64_t>(thi) * kTileN - 1) >> p.kv.bs_shift;
+    for (int64_t i = tid; i <= bhi - blo; i += kThreads)
+      bt_lds[i] = blo + i < p.kv.bt_cols ? p.kv.block_table[b * p.kv.bt_stride + blo + i] : -1;
+    bt_lo = blo;
+  };
+
+  // ---- tile loads: lane owns keys 8 wave + 4i + lane/16 (i = 0, 1), one chunk each
+  const int kl0 = 8 * wave + (lane >> 4);
+  const int pos_l = lane & 15;
+  bool bad_block = false;
+  auto issue = [&](int t, uint4* kst, uint4* vst) {
+    const uint16_t* kg[2];
+    const uint16_t* vg[2];
+    const uint16_t* z = reinterpret_cast<const uint16_t*>(g_zero_record);
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      sacc[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
-      const uint16_t* krow = &k_lds[(16 * mt + ln) * kKStride + 8 * g];
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4*>(krow + 32 * s));
-        sacc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qreg[s], sacc[mt], 0, 0, 0);
+    for (int i = 0; i < 2; ++i) {
+      const int kl = kl0 + 4 * i;
+      const int64_t j = static_cast<int64_t>(t) * kTileN + kl;
+      const uint16_t* kr = nullptr;
+      const uint16_t* vr = nullptr;
+      if (j < kend) {
+        int32_t blk = 0;
+        if constexpr (PAGED) blk = bt_lds[(j >> p.kv.bs_shift) - bt_lo];
+        kr = key_row<PAGED>(p, b, kvh, j, blk, true);
+        vr = key_row<PAGED>(p, b, kvh, j, blk, false);
+        if (!kr) bad_block = true;
       }
+      const int kc = pos_l ^ (kl & 15), vc = pos_l ^ (2 * (kl & 3));
+      kg[i] = (kr ? kr : z) + 8 * kc;
+      vg[i] = (vr ? vr : z + kD) + 8 * vc;
     }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int slot0 = (8 * wave + 4 * i) * kChunks;  // wave-uniform LDS base of this load
+      lds_dma16(kg[i], kst + slot0);
+      lds_dma16(vg[i], vst + slot0);
+    }
+  };
+  // tile loads issued after a tile's own loads: the next tile's 4
+  constexpr int kAfter = 4;
 
-    // Masking is needed only when some key of the tile is past some row's
-    // position (or past kend).
+  // ---- per-tile compute -------------------------------------------------------
+  const float top = static_cast<float>(p.npos - 1);
+  float carry = row_ok ? 0.f : 3.0e38f;  // padded columns count as saturated
+  float m_run = -INFINITY;               // running max (log2 domain) of the column
+  float l_run = 0.f;                     // this lane's share of the column sum
+  floatx16 o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = floatx16{};
+
+  auto compute = [&](int t, const uint4* kst, const uint4* vst) {
+    const int64_t base = static_cast<int64_t>(t) * kTileN;
+    if (base > wmax) return;  // every column of the wave precedes the tile
+    floatx16 s = {};
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      const bf16x8 a = as_bf16x8(kst[n * kChunks + ((2 * ks + h) ^ (n & 15))]);
+      s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qb[ks], s, 0, 0, 0);
+    }
     const bool need_mask = (base + kTileN - 1 > wmin) || (base + kTileN > kend);
-    if (need_mask) {
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int64_t j = base + 16 * mt + 4 * g + v;
-          if (!(j <= qp && j < kend)) sacc[mt][v] = -INFINITY;
-        }
-    }
-
+    float x[16];
     if (__all(carry >= top)) {
-      // saturated: bias = QE[P-1]; score (log2 domain) = logit*scale*log2e + const
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) sacc[mt][v] = sacc[mt][v] * (logit_scale * kLog2e) + sat_bias2;
+      for (int v = 0; v < 16; ++v) {
+        x[v] = s[v] * (kInvSqrtD * kLog2e);
+        if (need_mask) {
+          const int64_t j = base + 8 * (v >> 2) + 4 * h + (v & 3);
+          if (!(j <= qp && j < kend)) x[v] = -INFINITY;
+        }
+      }
     } else {
-      // gates, in-run suffix sums (runs of 4 keys), cross-lane suffix over runs
-      float suf[4][4];
-      float run[4];
+      // gates; runs of 4 keys (8 j4 + 4h + 0..3) and their in-run suffix sums
+      float gsuf[16], run[4];
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
+      for (int j4 = 0; j4 < 4; ++j4) {
         float acc = 0.f;
 #pragma unroll
-        for (int v = 3; v >= 0; --v) {
-          const float xv = sacc[mt][v] * logit_scale;
-          const float gate = sacc[mt][v] == -INFINITY ? 0.f : 1.f / (1.f + __expf(-xv));
-          acc += gate;
-          suf[mt][v] = acc;
+        for (int i = 3; i >= 0; --i) {
+          const int v = 4 * j4 + i;
+          const int64_t j = base + 8 * j4 + 4 * h + i;
+          const bool ok = j <= qp && j < kend;
+          const float lg = s[v] * kInvSqrtD;
+          acc += ok ? __builtin_amdgcn_rcpf(1.f + __expf(-lg)) : 0.f;
+          gsuf[v] = acc;
+          x[v] = ok ? lg : -INFINITY;
         }
-        run[mt] = acc;
+        run[j4] = acc;
       }
-      // inclusive suffix over the 4 lane groups (g ascending = keys ascending)
-      float incl[4], mt_total[4];
+      float other[4];
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        float s1 = run[mt];
-        float n1 = __shfl_down(s1, 16, 64);
-        if (g < 3) s1 += n1;
-        float n2 = __shfl_down(s1, 32, 64);
-        if (g < 2) s1 += n2;
-        incl[mt] = s1;
-        mt_total[mt] = __shfl(s1, ln, 64);  // lane group 0 holds the M-tile total
+      for (int j4 = 0; j4 < 4; ++j4) other[j4] = __shfl_xor(run[j4], 32, 64);
+      // gate mass of the runs with larger keys: (j4, h=1) follows (j4, h=0)
+      float after[4];
+      float acc = 0.f;
+#pragma unroll
+      for (int j4 = 3; j4 >= 0; --j4) {
+        after[j4] = acc + (h == 0 ? other[j4] : 0.f);
+        acc += run[j4] + other[j4];
       }
-      float right = 0.f;  // gate mass of the M-tiles to the right of mt
+      const float total = acc;
 #pragma unroll
-      for (int mt = 3; mt >= 0; --mt) {
-        const float before = carry + right + (incl[mt] - run[mt]);
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          float pos = before + suf[mt][v];
-          pos = pos < top ? pos : top;
-          pos = pos > 0.f ? pos : 0.f;  // also maps NaN to 0: table reads stay in range
-          const float fl = floorf(pos);
-          const int lo = static_cast<int>(fl);
-          const int hi = lo + 1 < p.npos - 1 ? lo + 1 : p.npos - 1;
-          const float lo_b = trow[lo];
-          const float bias = lo_b + (pos - fl) * (trow[hi] - lo_b);
-          sacc[mt][v] = (sacc[mt][v] * logit_scale + bias) * kLog2e;
-        }
-        right += mt_total[mt];
+      for (int v = 0; v < 16; ++v) {
+        float pos = carry + after[v >> 2] + gsuf[v];
+        pos = pos < top ? pos : top;
+        pos = pos > 0.f ? pos : 0.f;  // also maps NaN to 0: table reads stay in range
+        const float fl = floorf(pos);
+        const int lo = static_cast<int>(fl);
+        const int hi = lo + 1 < p.npos - 1 ? lo + 1 : p.npos - 1;
+        const float tlo = tcol[lo];
+        const float bias = tlo + (pos - fl) * (tcol[hi] - tlo);
+        x[v] = x[v] == -INFINITY ? -INFINITY : x[v] * kLog2e + bias;
       }
-      carry += right;
+      carry += total;
     }
-
-    // Online softmax: row max over the 16 values and the 4 lanes of the row.
-    float tmax = -INFINITY;
+    // online softmax over the 32 keys of the column (16 here, 16 in lane n ^ 32)
+    float tmax = x[0];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) tmax = fmaxf(tmax, sacc[mt][v]);
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    for (int v = 1; v < 16; ++v) tmax = fmaxf(tmax, x[v]);
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
     const float m_new = fmaxf(m_run, tmax);
     const bool live = m_new != -INFINITY;
-    if (__any(m_new != m_run)) {
-      const float corr = (live && m_run != -INFINITY) ? __builtin_amdgcn_exp2f(m_run - m_new) : (live ? 0.f : 1.f);
+    const float corr = live ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.f;
+    if (__any(corr != 1.f)) {
       l_run *= corr;
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) o[dt] *= corr;
+      for (int d = 0; d < 4; ++d) o[d] *= corr;
     }
     m_run = m_new;
-    float psum = 0.f;
     bf16x8 pb[2];
+    float psum = 0.f;
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const float pv = live ? __builtin_amdgcn_exp2f(sacc[2 * kt + half][v] - m_new) : 0.f;
-          psum += pv;
-          pb[kt][4 * half + v] = static_cast<__bf16>(pv);
-        }
-      }
+    for (int v = 0; v < 16; ++v) {
+      const float pv = live ? __builtin_amdgcn_exp2f(x[v] - m_new) : 0.f;
+      psum += pv;
+      pb[v >> 3][v & 7] = static_cast<__bf16>(pv);
     }
     l_run += psum;
-
-    // O^T += V^T P^T: A = V^T rows (dims), keys in the k-step order above.
+    // O^T += V^T P^T: V^T operand by transposed reads of the row-major V tile
+    const int q4 = lane >> 4, j16 = lane & 15;
+    const int dsub = 16 * (q4 & 1) + 4 * (j16 & 3);  // dim of this lane's 8-byte read, less 32 db
+    const int krow = j16 >> 2;                      // key within the 4-key run
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const uint16_t* vrow = &v_lds[(16 * dt + ln) * kVStride + 4 * g];
+    for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        const uint2 lo4 = *reinterpret_cast<const uint2*>(vrow + 32 * kt);
-        const uint2 hi4 = *reinterpret_cast<const uint2*>(vrow + 32 * kt + 16);
-        const uint4 u = make_uint4(lo4.x, lo4.y, hi4.x, hi4.y);
-        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(u), pb[kt], o[dt], 0, 0, 0);
+      for (int db = 0; db < 4; ++db) {
+        bf16x8 a;
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const int key = 16 * ks + 8 * r + 4 * h + krow;
+          const int dim = 32 * db + dsub;
+          const int slot = key * kChunks + ((dim >> 3) ^ (2 * (key & 3)));
+          const uint16_t* addr = reinterpret_cast<const uint16_t*>(vst + slot) + (dim & 7);
+          const bf16x4_tr tr = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((CS_LDS bf16x4_tr*)(addr));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) a[4 * r + e] = tr[e];
+        }
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[ks], o[db], 0, 0, 0);
       }
     }
+  };
+
+  // ---- main loop: windows of tiles right to left; inside a window, tiles right
+  // to left through two LDS stages with the loads one tile ahead.  Each wave
+  // waits for its own loads of a tile before the barrier that publishes the
+  // stage; the barrier after the compute frees the stage.
+  // Every prologue load (Q, E, positions) has landed: without this the
+  // compiler keeps a full vector-memory wait inside the tile loop for them.
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+  int tiles_per_window = ntiles;
+  if constexpr (PAGED)
+    tiles_per_window = static_cast<int>(((static_cast<int64_t>(kBtWindow) - 1) << p.kv.bs_shift) / kTileN);
+  if (tiles_per_window < 1) tiles_per_window = 1;
+  for (int thi = ntiles; thi > 0;) {
+    const int tlo = thi - tiles_per_window > 0 ? thi - tiles_per_window : 0;
+    if constexpr (PAGED) {
+      __syncthreads();
+      load_window(tlo, thi);
+      __syncthreads();
+    }
+    issue(thi - 1, st0.k, st0.v);
+    for (int t = thi - 1; t >= tlo; t -= 2) {
+      if (t - 1 >= tlo) {
+        issue(t - 1, st1.k, st1.v);
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(kAfter));
+      } else {
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+      }
+      __syncthreads();
+      compute(t, st0.k, st0.v);
+      __syncthreads();
+      if (t - 1 < tlo) break;
+      if (t - 2 >= tlo) {
+        issue(t - 2, st0.k, st0.v);
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(kAfter));
+      } else {
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+      }
+      __syncthreads();
+      compute(t - 1, st1.k, st1.v);
+      __syncthreads();
+    }
+    thi = tlo;
   }
 
-  // ---- epilogue: O^T lane holds row ln, dims 16 dt + 4g + v ------------------
-  float l_tot = l_run + __shfl_xor(l_run, 16, 64);
-  l_tot += __shfl_xor(l_tot, 32, 64);
+  // ---- epilogue: O^T lane holds column n, dims 32 db + 8 (v/4) + 4h + v%4 ----------
+  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   if (row_ok) {
-    uint16_t* orow = p.out + ((static_cast<int64_t>(b) * p.nq + r) * p.hq + h) * kD;
+    uint16_t* orow = p.out + ((static_cast<int64_t>(b) * p.nq + row) * p.hq + head) * kD;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      bf16x4 w;
+    for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) w[v] = static_cast<__bf16>(o[dt][v] * inv);
-      *reinterpret_cast<bf16x4*>(orow + 16 * dt + 4 * g) = w;
-    }
+      for (int j4 = 0; j4 < 4; ++j4) {
+        bf16x4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = static_cast<__bf16>(o[db][4 * j4 + e] * inv);
+        *reinterpret_cast<bf16x4*>(orow + 32 * db + 8 * j4 + 4 * h) = w;
+      }
   }
   if (bad_block) atomicOr(p.flags, CS_FLAG_BLOCK_INVALID);
 }
@@ -488,17 +532,18 @@ extern "C" int cs_ccpe_prefill_bf16(const void* q, int64_t q_s_batch, int64_t q_
                  (reinterpret_cast<uintptr_t>(q) % 16) == 0,
              "query rows must be 16-byte aligned");
   const int group = hq / hkv;
-  int heads_per_wg;
-  if (group % 4 == 0) heads_per_wg = 4;
-  else if (group == 2) heads_per_wg = 2;
-  else if (group == 1) heads_per_wg = 1;
-  else {
-    set_error("GQA group size %d is not supported by the MFMA prefill kernel", group);
+  if (kCols % group != 0) {
+    set_error("GQA group size %d is not supported by the MFMA prefill kernel (it must divide %d)",
+              group, kCols);
     return CS_EUNSUPPORTED;
   }
   cs::prefill_params p{};
   int st = fill_kv(kv, &p.kv);
   if (st) return st;
+  if (p.kv.block_table && p.kv.bs_shift < 0) {
+    set_error("the MFMA prefill kernel needs a power-of-two block size (got %d)", kv->block_size);
+    return CS_EUNSUPPORTED;
+  }
   if (batch == 0 || nq == 0) return CS_OK;
   p.q = static_cast<const uint16_t*>(q);
   p.q_sb = q_s_batch;
@@ -511,26 +556,28 @@ extern "C" int cs_ccpe_prefill_bf16(const void* q, int64_t q_s_batch, int64_t q_
   p.hq = hq;
   p.hkv = hkv;
   p.group = group;
-  p.heads_per_wg = heads_per_wg;
-  const int wg_rows = kRows * (kWaves / heads_per_wg);
-  p.row_blocks = static_cast<int32_t>(ceil_div(nq, wg_rows));
+  p.rows_per_wg = kWgCols / group;
+  p.row_blocks = static_cast<int32_t>(ceil_div(nq, p.rows_per_wg));
   p.nk = nk;
   p.e = e;
   p.npos = max_positions;
-  p.pos_tiles = (max_positions + 15) / 16;
-  p.tab_stride = p.pos_tiles * 16 + 1;
+  p.tab_stride = max_positions + 1;
   p.out = static_cast<uint16_t*>(out);
   p.flags = flags;
-  int64_t total = static_cast<int64_t>(batch) * hkv * (group / heads_per_wg) * p.row_blocks;
+  const int64_t total = static_cast<int64_t>(batch) * hkv * p.row_blocks;
   CS_REQUIRE(total < (1ll << 31), "grid too large");
   p.total_wg = static_cast<int32_t>(total);
-  size_t smem = sizeof(float) * kWaves * kRows * p.tab_stride;
+  const size_t smem = sizeof(float) * kWgCols * p.tab_stride;
   if (smem + kStaticLds > kLdsLimit) {
     set_error("prefill LDS %zu bytes exceeds the workgroup limit", smem + kStaticLds);
     return CS_EUNSUPPORTED;
   }
-  hipLaunchKernelGGL(ccpe_prefill_kernel, dim3(p.total_wg), dim3(kThreads), smem,
-                     as_stream(stream), p);
+  if (p.kv.block_table)
+    hipLaunchKernelGGL(ccpe_prefill_kernel<true>, dim3(p.total_wg), dim3(kThreads), smem,
+                       as_stream(stream), p);
+  else
+    hipLaunchKernelGGL(ccpe_prefill_kernel<false>, dim3(p.total_wg), dim3(kThreads), smem,
+                       as_stream(stream), p);
   CS_LAUNCH_CHECK("ccpe_prefill");
   return CS_OK;
 }

@@ -660,7 +660,7 @@ def _fast_path_ok(query, key, value, e, cope, amask, visibility_mask, fixed_posi
         if t.stride(2) != 1 or t.data_ptr() % 16 or t.stride(0) % 8 or t.stride(1) % 8:
             return False
     group = query.shape[1] // key.shape[1]
-    return group in (1, 2) or group % 4 == 0
+    return group in (1, 2, 4, 8, 16, 32)
 
 
 def _chunked_attention(query, key, value, cope, query_positions, key_positions, amask,
