@@ -35,9 +35,12 @@
 // ds_read_b64_tr_b16 (lane i of a 16-lane group receives element i of the
 // four 4-element rows addressed by lanes 4e .. 4e+3).
 //
-// LDS tiles are XOR-swizzled by 16-byte chunk: K chunk c of key k sits at
-// c ^ (k % 16) (conflict-free MFMA A reads of 16 keys x one chunk), V chunk c
-// at c ^ 2(k % 4) (conflict-free transposed reads of 4 keys x 2 chunks).
+// LDS tile layouts (16-byte chunk c of key k, in 16-byte slots), chosen so
+// every read is one per-lane base plus an immediate offset and no two lanes
+// of a 16-lane phase share a bank:
+//   K: slot (k / 16) * 256 + c * 16 + k % 16   (A reads: 16 keys x one chunk)
+//   V: slot (k / 4) * 64 + c * 4 + k % 4       (transposed reads: 4 keys x 2 chunks)
+// The direct loads pick, per lane, the (key, chunk) that lands in its slot.
 
 #include "common.h"
 
@@ -65,6 +68,20 @@ constexpr size_t kStaticLds = 4 * kStageSlots * 16 + 4 * kBtWindow + 16;
 constexpr size_t kLdsLimit = 160 * 1024;
 constexpr float kInvSqrtD = 0.08838834764831845f;  // 1/sqrt(128)
 constexpr float kLog2e = 1.4426950408889634f;
+
+// Exchange with lane l ^ 32: v_permlane32_swap of x with itself leaves
+// {x[l], x[l ^ 32]} in the two results, in an order that depends on the half.
+__device__ inline void swap_halves(float x, float& lo, float& hi) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  lo = __uint_as_float(r[0]);
+  hi = __uint_as_float(r[1]);
+}
+
+__device__ inline uint32_t pack_bf16x2(float a, float b) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const bf16x2 v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+  return __builtin_bit_cast(uint32_t, v);
+}
 
 // s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
 // vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt[5:4] in [15:14]).
@@ -254,37 +271,36 @@ __global__ void __launch_bounds__(kThreads, 2) ccpe_prefill_kernel(prefill_param
     bt_lo = blo;
   };
 
-  // ---- tile loads: lane owns keys 8 wave + 4i + lane/16 (i = 0, 1), one chunk each
-  const int kl0 = 8 * wave + (lane >> 4);
-  const int pos_l = lane & 15;
+  // ---- tile loads.  Wave w issues the loads of slots [128 w, 128 w + 128) of
+  // each stage (two 64-slot loads per stage).  K: one key per lane,
+  // 16 (w / 2) + lane % 16, chunks 8 (w % 2) + lane / 16 and 4 more.  V: keys
+  // 8w + 4i + lane % 4 (i = 0, 1), chunk lane / 4.
+  const int k_key = 16 * (wave >> 1) + (lane & 15);
+  const int k_chunk = 8 * (wave & 1) + (lane >> 4);
+  const int v_key = 8 * wave + (lane & 3);
+  const int v_chunk = lane >> 2;
   bool bad_block = false;
+  auto row_of = [&](int t, int key, bool kpart) -> const uint16_t* {
+    const uint16_t* z = reinterpret_cast<const uint16_t*>(g_zero_record) + (kpart ? 0 : kD);
+    const int64_t j = static_cast<int64_t>(t) * kTileN + key;
+    if (j >= kend) return z;
+    int32_t blk = 0;
+    if constexpr (PAGED) blk = bt_lds[(j >> p.kv.bs_shift) - bt_lo];
+    const uint16_t* r = key_row<PAGED>(p, b, kvh, j, blk, kpart);
+    if (!r) {
+      bad_block = true;
+      return z;
+    }
+    return r;
+  };
   auto issue = [&](int t, uint4* kst, uint4* vst) {
-    const uint16_t* kg[2];
-    const uint16_t* vg[2];
-    const uint16_t* z = reinterpret_cast<const uint16_t*>(g_zero_record);
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int kl = kl0 + 4 * i;
-      const int64_t j = static_cast<int64_t>(t) * kTileN + kl;
-      const uint16_t* kr = nullptr;
-      const uint16_t* vr = nullptr;
-      if (j < kend) {
-        int32_t blk = 0;
-        if constexpr (PAGED) blk = bt_lds[(j >> p.kv.bs_shift) - bt_lo];
-        kr = key_row<PAGED>(p, b, kvh, j, blk, true);
-        vr = key_row<PAGED>(p, b, kvh, j, blk, false);
-        if (!kr) bad_block = true;
-      }
-      const int kc = pos_l ^ (kl & 15), vc = pos_l ^ (2 * (kl & 3));
-      kg[i] = (kr ? kr : z) + 8 * kc;
-      vg[i] = (vr ? vr : z + kD) + 8 * vc;
-    }
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int slot0 = (8 * wave + 4 * i) * kChunks;  // wave-uniform LDS base of this load
-      lds_dma16(kg[i], kst + slot0);
-      lds_dma16(vg[i], vst + slot0);
-    }
+    const uint16_t* kr = row_of(t, k_key, true);
+    const uint16_t* vr0 = row_of(t, v_key, false);
+    const uint16_t* vr1 = row_of(t, v_key + 4, false);
+    lds_dma16(kr + 8 * k_chunk, kst + 128 * wave);
+    lds_dma16(kr + 8 * (k_chunk + 4), kst + 128 * wave + 64);
+    lds_dma16(vr0 + 8 * v_chunk, vst + 128 * wave);
+    lds_dma16(vr1 + 8 * v_chunk, vst + 128 * wave + 64);
   };
   // tile loads issued after a tile's own loads: the next tile's 4
   constexpr int kAfter = 4;
@@ -298,27 +314,59 @@ __global__ void __launch_bounds__(kThreads, 2) ccpe_prefill_kernel(prefill_param
 #pragma unroll
   for (int i = 0; i < 4; ++i) o[i] = floatx16{};
 
+  // key coordinates of the tile loop fit in 32 bits (kend <= nk < 2^31)
+  const int qp32 = qp < 0 ? -1 : static_cast<int>(qp);
+  const int kend32 = static_cast<int>(kend);
+  // wave extremes are wave-uniform after the reduction; keep them scalar so the
+  // tile tests below are uniform branches
+  const int wmax32 = __builtin_amdgcn_readfirstlane(wmax < 0 ? -1 : static_cast<int>(wmax));
+  const int wmin32 = __builtin_amdgcn_readfirstlane(wmin > kend ? kend32 : static_cast<int>(wmin));
+  const int j16 = lane & 15;
+  // element offset of this lane's transposed V read within a stage
+  const int vrd_off = 512 * h + 32 * (2 * ((lane >> 4) & 1) + ((j16 & 3) >> 1)) + 8 * (j16 >> 2) + 4 * (j16 & 1);
   auto compute = [&](int t, const uint4* kst, const uint4* vst) {
-    const int64_t base = static_cast<int64_t>(t) * kTileN;
-    if (base > wmax) return;  // every column of the wave precedes the tile
+    const int base = t * kTileN;
+    if (base > wmax32) return;  // every column of the wave precedes the tile
+    // all K operands first, then the 8 MFMAs of S^T
+    bf16x8 ka[8];
+    const uint4* krd = kst + (n >> 4) * 256 + h * 16 + (n & 15);  // + 32 ks slots
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) ka[ks] = as_bf16x8(krd[32 * ks]);
     floatx16 s = {};
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-      const bf16x8 a = as_bf16x8(kst[n * kChunks + ((2 * ks + h) ^ (n & 15))]);
-      s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qb[ks], s, 0, 0, 0);
-    }
-    const bool need_mask = (base + kTileN - 1 > wmin) || (base + kTileN > kend);
-    float x[16];
-    if (__all(carry >= top)) {
+    for (int ks = 0; ks < 8; ++ks) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[ks], qb[ks], s, 0, 0, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // the 8 LDS reads
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);  // then the 8 MFMAs
+    // V^T operands: independent of the softmax, so read now and consumed after
+    // it; byte offset of this lane's read = 1024 h + 64 chunk-in-block +
+    // 16 (key % 4) + 8 half, plus 4096 ks + 2048 r + 256 db
+    bf16x8 va[8];
+    const uint16_t* vrd = reinterpret_cast<const uint16_t*>(vst) + vrd_off;
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        x[v] = s[v] * (kInvSqrtD * kLog2e);
-        if (need_mask) {
-          const int64_t j = base + 8 * (v >> 2) + 4 * h + (v & 3);
-          if (!(j <= qp && j < kend)) x[v] = -INFINITY;
-        }
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const bf16x4_tr lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+            (CS_LDS bf16x4_tr*)(vrd + 2048 * ks + 128 * db));
+        const bf16x4_tr hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+            (CS_LDS bf16x4_tr*)(vrd + 2048 * ks + 1024 + 128 * db));
+        va[4 * ks + db] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
+    const bool need_mask = (base + kTileN - 1 > wmin32) || (base + kTileN > kend32);
+    // key v of the tile (8 (v/4) + 4h + v%4) is visible to the column when
+    // 8 (v/4) + v%4 <= lim
+    const int lim = (qp32 < kend32 - 1 ? qp32 : kend32 - 1) - base - 4 * h;
+    // s becomes the scores in log2 units; when saturated the (softmax-neutral
+    // per column) scale is left to the exponent below
+    float scale = kInvSqrtD * kLog2e;
+    if (__all(carry >= top)) {
+      if (need_mask) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          if (8 * (v >> 2) + (v & 3) > lim) s[v] = -INFINITY;
       }
     } else {
+      scale = 1.f;
       // gates; runs of 4 keys (8 j4 + 4h + 0..3) and their in-run suffix sums
       float gsuf[16], run[4];
 #pragma unroll
@@ -327,18 +375,21 @@ __global__ void __launch_bounds__(kThreads, 2) ccpe_prefill_kernel(prefill_param
 #pragma unroll
         for (int i = 3; i >= 0; --i) {
           const int v = 4 * j4 + i;
-          const int64_t j = base + 8 * j4 + 4 * h + i;
-          const bool ok = j <= qp && j < kend;
+          const bool ok = 8 * j4 + i <= lim;
           const float lg = s[v] * kInvSqrtD;
           acc += ok ? __builtin_amdgcn_rcpf(1.f + __expf(-lg)) : 0.f;
           gsuf[v] = acc;
-          x[v] = ok ? lg : -INFINITY;
+          s[v] = ok ? lg : -INFINITY;
         }
         run[j4] = acc;
       }
       float other[4];
 #pragma unroll
-      for (int j4 = 0; j4 < 4; ++j4) other[j4] = __shfl_xor(run[j4], 32, 64);
+      for (int j4 = 0; j4 < 4; ++j4) {
+        float a, c2;
+        swap_halves(run[j4], a, c2);
+        other[j4] = h ? a : c2;
+      }
       // gate mass of the runs with larger keys: (j4, h=1) follows (j4, h=0)
       float after[4];
       float acc = 0.f;
@@ -358,16 +409,23 @@ __global__ void __launch_bounds__(kThreads, 2) ccpe_prefill_kernel(prefill_param
         const int hi = lo + 1 < p.npos - 1 ? lo + 1 : p.npos - 1;
         const float tlo = tcol[lo];
         const float bias = tlo + (pos - fl) * (tcol[hi] - tlo);
-        x[v] = x[v] == -INFINITY ? -INFINITY : x[v] * kLog2e + bias;
+        s[v] = s[v] == -INFINITY ? -INFINITY : s[v] * kLog2e + bias;
       }
       carry += total;
     }
-    // online softmax over the 32 keys of the column (16 here, 16 in lane n ^ 32)
-    float tmax = x[0];
+    // online softmax over the 32 keys of the column (16 here, 16 in lane n ^ 32);
+    // the running max m_run is kept in scaled (log2) units
+    float tmax = s[0];
 #pragma unroll
-    for (int v = 1; v < 16; ++v) tmax = fmaxf(tmax, x[v]);
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float m_new = fmaxf(m_run, tmax);
+    for (int v = 1; v < 16; ++v) tmax = fmaxf(tmax, s[v]);
+    {
+      float a, c2;
+      swap_halves(tmax, a, c2);
+      tmax = fmaxf(a, c2) * scale;
+    }
+    // The reference max moves only when the tile max exceeds it by more than
+    // 8 (log2 units): probabilities stay <= 2^8 and O is rescaled rarely.
+    const float m_new = tmax > m_run + 8.f ? tmax : m_run;
     const bool live = m_new != -INFINITY;
     const float corr = live ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.f;
     if (__any(corr != 1.f)) {
@@ -376,37 +434,25 @@ __global__ void __launch_bounds__(kThreads, 2) ccpe_prefill_kernel(prefill_param
       for (int d = 0; d < 4; ++d) o[d] *= corr;
     }
     m_run = m_new;
-    bf16x8 pb[2];
+    const float moff = live ? -m_new : 0.f;
+    uint32_t pw[8];
     float psum = 0.f;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const float pv = live ? __builtin_amdgcn_exp2f(x[v] - m_new) : 0.f;
-      psum += pv;
-      pb[v >> 3][v & 7] = static_cast<__bf16>(pv);
+    for (int v = 0; v < 16; v += 2) {
+      const float p0 = __builtin_amdgcn_exp2f(fmaf(s[v], scale, moff));
+      const float p1 = __builtin_amdgcn_exp2f(fmaf(s[v + 1], scale, moff));
+      psum += p0 + p1;
+      pw[v >> 1] = pack_bf16x2(p0, p1);
     }
     l_run += psum;
-    // O^T += V^T P^T: V^T operand by transposed reads of the row-major V tile
-    const int q4 = lane >> 4, j16 = lane & 15;
-    const int dsub = 16 * (q4 & 1) + 4 * (j16 & 3);  // dim of this lane's 8-byte read, less 32 db
-    const int krow = j16 >> 2;                      // key within the 4-key run
+    const bf16x8 pb0 = __builtin_bit_cast(bf16x8, make_uint4(pw[0], pw[1], pw[2], pw[3]));
+    const bf16x8 pb1 = __builtin_bit_cast(bf16x8, make_uint4(pw[4], pw[5], pw[6], pw[7]));
+    // O^T += V^T P^T
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+    for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        bf16x8 a;
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-          const int key = 16 * ks + 8 * r + 4 * h + krow;
-          const int dim = 32 * db + dsub;
-          const int slot = key * kChunks + ((dim >> 3) ^ (2 * (key & 3)));
-          const uint16_t* addr = reinterpret_cast<const uint16_t*>(vst + slot) + (dim & 7);
-          const bf16x4_tr tr = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((CS_LDS bf16x4_tr*)(addr));
-#pragma unroll
-          for (int e = 0; e < 4; ++e) a[4 * r + e] = tr[e];
-        }
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[ks], o[db], 0, 0, 0);
-      }
-    }
+      for (int db = 0; db < 4; ++db)
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[4 * ks + db], ks ? pb1 : pb0, o[db], 0, 0, 0);
   };
 
   // ---- main loop: windows of tiles right to left; inside a window, tiles right
