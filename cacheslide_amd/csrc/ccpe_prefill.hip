@@ -144,22 +144,6 @@ __device__ inline void decode_wg(const prefill_params& p, int& b, int& kvh, int&
   b = rest / p.hkv;
 }
 
-// First element of key j's K (kpart) or V row, or null if its block is invalid.
-template <bool PAGED>
-__device__ inline const uint16_t* key_row(const prefill_params& p, int b, int kvh, int64_t j,
-                                          int32_t blk, bool kpart) {
-  if constexpr (PAGED) {
-    if (blk < 0 || blk >= p.kv.num_blocks) return nullptr;
-    const int64_t off = j & ((int64_t(1) << p.kv.bs_shift) - 1);
-    return p.kv.cache + blk * p.kv.s_block + kvh * p.kv.s_head + off * p.kv.s_offset +
-           (kpart ? 0 : kD);
-  } else {
-    return kpart ? p.kv.k + b * p.kv.k_sb + j * p.kv.k_st + kvh * p.kv.k_sh
-                 : p.kv.v + b * p.kv.v_sb + j * p.kv.v_st + kvh * p.kv.v_sh;
-  }
-}
-
-
 struct stage_t {
   uint4 k[kStageSlots];
   uint4 v[kStageSlots];
@@ -258,6 +242,13 @@ __global__ void __launch_bounds__(kThreads, 2) ccpe_prefill_kernel(prefill_param
   const int64_t wgmax = wg_max_pos;
   const int64_t kend = wgmax + 1 < nk ? wgmax + 1 : (nk > 0 ? nk : 0);  // keys [0, kend)
   const int ntiles = static_cast<int>((kend + kTileN - 1) / kTileN);
+  // key coordinates of the tile loop fit in 32 bits (kend <= nk < 2^31)
+  const int qp32 = qp < 0 ? -1 : static_cast<int>(qp);
+  const int kend32 = static_cast<int>(kend);
+  // wave extremes are wave-uniform after the reduction; keep them scalar so the
+  // tile tests below are uniform branches
+  const int wmax32 = __builtin_amdgcn_readfirstlane(wmax < 0 ? -1 : static_cast<int>(wmax));
+  const int wmin32 = __builtin_amdgcn_readfirstlane(wmin > kend ? kend32 : static_cast<int>(wmin));
 
   // ---- block ids: the table entries of a window of tiles are copied to LDS
   // before the window's tile loop, so that loop issues no vector-memory
@@ -280,18 +271,35 @@ __global__ void __launch_bounds__(kThreads, 2) ccpe_prefill_kernel(prefill_param
   const int v_key = 8 * wave + (lane & 3);
   const int v_chunk = lane >> 2;
   bool bad_block = false;
+  // record base of this request / KV head; per-key offsets below are 32-bit
+  // products (the host checks that the strides fit)
+  const uint16_t* rec_base = PAGED ? p.kv.cache + kvh * p.kv.s_head
+                                   : p.kv.k + b * p.kv.k_sb + kvh * p.kv.k_sh;
+  const uint16_t* vrec_base = PAGED ? rec_base + kD : p.kv.v + b * p.kv.v_sb + kvh * p.kv.v_sh;
+  const uint32_t s_blk = static_cast<uint32_t>(PAGED ? p.kv.s_block : p.kv.k_st);
+  const uint32_t s_off = static_cast<uint32_t>(PAGED ? p.kv.s_offset : 0);
+  const uint32_t v_st = static_cast<uint32_t>(PAGED ? p.kv.s_block : p.kv.v_st);
+  const uint32_t off_mask = PAGED ? (1u << p.kv.bs_shift) - 1u : 0u;
+  const int nblocks = PAGED ? static_cast<int>(p.kv.num_blocks < INT32_MAX ? p.kv.num_blocks : INT32_MAX) : 0;
+  // K (kpart) or V row of key t * 32 + key; the zero record when the key is
+  // past kend or its block is invalid (branch-free)
   auto row_of = [&](int t, int key, bool kpart) -> const uint16_t* {
     const uint16_t* z = reinterpret_cast<const uint16_t*>(g_zero_record) + (kpart ? 0 : kD);
-    const int64_t j = static_cast<int64_t>(t) * kTileN + key;
-    if (j >= kend) return z;
-    int32_t blk = 0;
-    if constexpr (PAGED) blk = bt_lds[(j >> p.kv.bs_shift) - bt_lo];
-    const uint16_t* r = key_row<PAGED>(p, b, kvh, j, blk, kpart);
-    if (!r) {
-      bad_block = true;
-      return z;
+    const int j = t * kTileN + key;
+    const bool in = j < kend32;
+    uint64_t off;
+    bool ok = in;
+    if constexpr (PAGED) {
+      const int blk = bt_lds[(j >> p.kv.bs_shift) - static_cast<int>(bt_lo)];
+      ok = in && blk >= 0 && blk < nblocks;
+      bad_block |= in && !ok;
+      off = static_cast<uint64_t>(static_cast<uint32_t>(blk)) * s_blk +
+            static_cast<uint64_t>(static_cast<uint32_t>(j) & off_mask) * s_off;
+    } else {
+      off = static_cast<uint64_t>(static_cast<uint32_t>(j)) * (kpart ? s_blk : v_st);
     }
-    return r;
+    const uint16_t* r = (kpart ? rec_base : vrec_base) + off;
+    return ok ? r : z;
   };
   auto issue = [&](int t, uint4* kst, uint4* vst) {
     const uint16_t* kr = row_of(t, k_key, true);
@@ -314,13 +322,6 @@ __global__ void __launch_bounds__(kThreads, 2) ccpe_prefill_kernel(prefill_param
 #pragma unroll
   for (int i = 0; i < 4; ++i) o[i] = floatx16{};
 
-  // key coordinates of the tile loop fit in 32 bits (kend <= nk < 2^31)
-  const int qp32 = qp < 0 ? -1 : static_cast<int>(qp);
-  const int kend32 = static_cast<int>(kend);
-  // wave extremes are wave-uniform after the reduction; keep them scalar so the
-  // tile tests below are uniform branches
-  const int wmax32 = __builtin_amdgcn_readfirstlane(wmax < 0 ? -1 : static_cast<int>(wmax));
-  const int wmin32 = __builtin_amdgcn_readfirstlane(wmin > kend ? kend32 : static_cast<int>(wmin));
   const int j16 = lane & 15;
   // element offset of this lane's transposed V read within a stage
   const int vrd_off = 512 * h + 32 * (2 * ((lane >> 4) & 1) + ((j16 & 3) >> 1)) + 8 * (j16 >> 2) + 4 * (j16 & 1);
@@ -586,6 +587,13 @@ extern "C" int cs_ccpe_prefill_bf16(const void* q, int64_t q_s_batch, int64_t q_
   cs::prefill_params p{};
   int st = fill_kv(kv, &p.kv);
   if (st) return st;
+  if (p.kv.block_table ? (p.kv.s_block >= (1ll << 31) || p.kv.s_offset >= (1ll << 31) || p.kv.s_block < 0 ||
+                          p.kv.s_offset < 0)
+                       : (p.kv.k_st >= (1ll << 31) || p.kv.v_st >= (1ll << 31) || p.kv.k_st < 0 ||
+                          p.kv.v_st < 0)) {
+    set_error("the MFMA prefill kernel needs non-negative block / token strides below 2^31");
+    return CS_EUNSUPPORTED;
+  }
   if (p.kv.block_table && p.kv.bs_shift < 0) {
     set_error("the MFMA prefill kernel needs a power-of-two block size (got %d)", kv->block_size);
     return CS_EUNSUPPORTED;
