@@ -54,17 +54,15 @@ typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4_tr;
 #define CS_LDS __attribute__((address_space(3)))
 
 constexpr int kD = 128;
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
-constexpr int kCols = 32;                // (row, head) columns per wave
-constexpr int kWgCols = kCols * kWaves;  // per workgroup
+constexpr int kCols = 32;  // (row, head) columns per wave
 constexpr int kTileN = 32;               // keys per tile
 constexpr int kChunks = 16;              // 16-byte chunks of a 256-byte K or V row
 constexpr int kStageSlots = kTileN * kChunks;  // uint4 slots of one K (or V) stage
 constexpr int kMaxPos = 128;
 constexpr int kPosChunk = 64;  // E^T positions staged per pass (bf16 hi and lo, 16 KB each)
 constexpr int kBtWindow = 1024;  // block-table entries held in LDS at a time
-constexpr size_t kStaticLds = 4 * kStageSlots * 16 + 4 * kBtWindow + 16;
+constexpr int kStages = 3;
+constexpr size_t kStaticLds = kStages * 2 * kStageSlots * 16 + 4 * kBtWindow + 16;
 constexpr size_t kLdsLimit = 160 * 1024;
 constexpr float kInvSqrtD = 0.08838834764831845f;  // 1/sqrt(128)
 constexpr float kLog2e = 1.4426950408889634f;
@@ -149,13 +147,19 @@ struct stage_t {
   uint4 v[kStageSlots];
 };
 
-template <bool PAGED>
-__global__ void __launch_bounds__(kThreads, 2) ccpe_prefill_kernel(prefill_params p) {
+// WAVES wavefronts of 32 columns each; two wavefronts per SIMD
+template <bool PAGED, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(prefill_params p) {
+  constexpr int kThreads = 64 * WAVES;
+  constexpr int kInstr = 8 / WAVES;  // 64-slot loads per wave for each of K and V
   __shared__ __align__(16) stage_t st0;
   __shared__ __align__(16) stage_t st1;
+  __shared__ __align__(16) stage_t st2;
   __shared__ int32_t bt_lds[kBtWindow];  // block ids of blocks [bt_lo, bt_lo + kBtWindow)
   __shared__ int64_t wg_max_pos;
-  extern __shared__ __align__(16) float tab[];  // [kWgCols][tab_stride]: (QE - QE[P-1]) log2e
+  // [32 WAVES columns][tab_stride] QE log2(e), fp16 (the table only enters
+  // bias differences of unsaturated keys; 2^-11 relative precision)
+  extern __shared__ __align__(16) _Float16 tab[];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -200,7 +204,7 @@ __global__ void __launch_bounds__(kThreads, 2) ccpe_prefill_kernel(prefill_param
   // stages, swizzled like K: chunk c of position pos at c ^ (pos % 16).
   uint16_t* ehi = reinterpret_cast<uint16_t*>(&st0);  // [64 pos][128 dims], 16 KB
   uint16_t* elo = reinterpret_cast<uint16_t*>(&st1);
-  float* tcol = tab + c * p.tab_stride;
+  _Float16* tcol = tab + c * p.tab_stride;
   for (int pc = 0; pc < p.npos; pc += kPosChunk) {
     __syncthreads();
     for (int i = tid; i < kPosChunk * kD; i += kThreads) {
@@ -229,15 +233,13 @@ __global__ void __launch_bounds__(kThreads, 2) ccpe_prefill_kernel(prefill_param
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int pv = pc + 32 * pb + 8 * (v >> 2) + 4 * h + (v & 3);
-        if (pv < p.npos) tcol[pv] = acc[v];
+        if (pv < p.npos) tcol[pv] = static_cast<_Float16>(acc[v] * kLog2e);
       }
     }
   }
   __syncthreads();
-  {
-    const float top_qe = tcol[p.npos - 1];
-    for (int pv = h; pv < p.npos; pv += 2) tcol[pv] = (tcol[pv] - top_qe) * kLog2e;
-  }
+  // QE[P-1] of the column: the bias of saturated keys, subtracted from every bias
+  const float top_qe = static_cast<float>(tcol[p.npos - 1]);
 
   const int64_t wgmax = wg_max_pos;
   const int64_t kend = wgmax + 1 < nk ? wgmax + 1 : (nk > 0 ? nk : 0);  // keys [0, kend)
@@ -262,13 +264,11 @@ __global__ void __launch_bounds__(kThreads, 2) ccpe_prefill_kernel(prefill_param
     bt_lo = blo;
   };
 
-  // ---- tile loads.  Wave w issues the loads of slots [128 w, 128 w + 128) of
-  // each stage (two 64-slot loads per stage).  K: one key per lane,
-  // 16 (w / 2) + lane % 16, chunks 8 (w % 2) + lane / 16 and 4 more.  V: keys
-  // 8w + 4i + lane % 4 (i = 0, 1), chunk lane / 4.
-  const int k_key = 16 * (wave >> 1) + (lane & 15);
-  const int k_chunk = 8 * (wave & 1) + (lane >> 4);
-  const int v_key = 8 * wave + (lane & 3);
+  // ---- tile loads.  Load j (0..7) of a stage fills slots [64 j, 64 j + 64) of
+  // K and of V; wave w issues loads j = kInstr w .. kInstr w + kInstr - 1.
+  // K: key 16 (j / 4) + lane % 16, chunk 4 (j % 4) + lane / 16 (the key is
+  // the same for all loads of a wave).  V: key 4j + lane % 4, chunk lane / 4.
+  const int k_key = 16 * ((kInstr * wave) >> 2) + (lane & 15);
   const int v_chunk = lane >> 2;
   bool bad_block = false;
   // record base of this request / KV head; per-key offsets below are 32-bit
@@ -301,17 +301,26 @@ __global__ void __launch_bounds__(kThreads, 2) ccpe_prefill_kernel(prefill_param
     const uint16_t* r = (kpart ? rec_base : vrec_base) + off;
     return ok ? r : z;
   };
-  auto issue = [&](int t, uint4* kst, uint4* vst) {
+  auto issue = [&](int t, stage_t& st) {
     const uint16_t* kr = row_of(t, k_key, true);
-    const uint16_t* vr0 = row_of(t, v_key, false);
-    const uint16_t* vr1 = row_of(t, v_key + 4, false);
-    lds_dma16(kr + 8 * k_chunk, kst + 128 * wave);
-    lds_dma16(kr + 8 * (k_chunk + 4), kst + 128 * wave + 64);
-    lds_dma16(vr0 + 8 * v_chunk, vst + 128 * wave);
-    lds_dma16(vr1 + 8 * v_chunk, vst + 128 * wave + 64);
+    const uint16_t* vr[kInstr];
+#pragma unroll
+    for (int i = 0; i < kInstr; ++i) vr[i] = row_of(t, 4 * (kInstr * wave + i) + (lane & 3), false);
+#pragma unroll
+    for (int i = 0; i < kInstr; ++i) {
+      const int j = kInstr * wave + i;
+      lds_dma16(kr + 8 * (4 * (j & 3) + (lane >> 4)), st.k + 64 * j);
+      lds_dma16(vr[i] + 8 * v_chunk, st.v + 64 * j);
+    }
   };
-  // tile loads issued after a tile's own loads: the next tile's 4
-  constexpr int kAfter = 4;
+  // wait until this wave's loads of the current tile have landed, with the
+  // next tile's loads (2 kInstr of them) possibly still in flight
+  auto wait_tile = [&](bool next_in_flight) {
+    if (next_in_flight)
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kInstr));
+    else
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+  };
 
   // ---- per-tile compute -------------------------------------------------------
   const float top = static_cast<float>(p.npos - 1);
@@ -408,8 +417,8 @@ __global__ void __launch_bounds__(kThreads, 2) ccpe_prefill_kernel(prefill_param
         const float fl = floorf(pos);
         const int lo = static_cast<int>(fl);
         const int hi = lo + 1 < p.npos - 1 ? lo + 1 : p.npos - 1;
-        const float tlo = tcol[lo];
-        const float bias = tlo + (pos - fl) * (tcol[hi] - tlo);
+        const float tlo = static_cast<float>(tcol[lo]);
+        const float bias = tlo + (pos - fl) * (static_cast<float>(tcol[hi]) - tlo) - top_qe;
         s[v] = s[v] == -INFINITY ? -INFINITY : s[v] * kLog2e + bias;
       }
       carry += total;
@@ -457,9 +466,10 @@ __global__ void __launch_bounds__(kThreads, 2) ccpe_prefill_kernel(prefill_param
   };
 
   // ---- main loop: windows of tiles right to left; inside a window, tiles right
-  // to left through two LDS stages with the loads one tile ahead.  Each wave
-  // waits for its own loads of a tile before the barrier that publishes the
-  // stage; the barrier after the compute frees the stage.
+  // to left through three LDS stages with the loads two tiles ahead.  Each wave
+  // waits for its own loads of a tile before the one barrier of the tile, which
+  // both publishes that stage and frees the stage of the tile before, into
+  // which the loads of the tile two ahead are then issued.
   // Every prologue load (Q, E, positions) has landed: without this the
   // compiler keeps a full vector-memory wait inside the tile loop for them.
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
@@ -474,27 +484,23 @@ __global__ void __launch_bounds__(kThreads, 2) ccpe_prefill_kernel(prefill_param
       load_window(tlo, thi);
       __syncthreads();
     }
-    issue(thi - 1, st0.k, st0.v);
-    for (int t = thi - 1; t >= tlo; t -= 2) {
-      if (t - 1 >= tlo) {
-        issue(t - 1, st1.k, st1.v);
-        __builtin_amdgcn_s_waitcnt(waitcnt_vm(kAfter));
-      } else {
-        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-      }
+    issue(thi - 1, st0);
+    if (thi - 2 >= tlo) issue(thi - 2, st1);
+    for (int t = thi - 1; t >= tlo; t -= 3) {
+      wait_tile(t - 1 >= tlo);
       __syncthreads();
+      if (t - 2 >= tlo) issue(t - 2, st2);
       compute(t, st0.k, st0.v);
-      __syncthreads();
       if (t - 1 < tlo) break;
-      if (t - 2 >= tlo) {
-        issue(t - 2, st0.k, st0.v);
-        __builtin_amdgcn_s_waitcnt(waitcnt_vm(kAfter));
-      } else {
-        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-      }
+      wait_tile(t - 2 >= tlo);
       __syncthreads();
+      if (t - 3 >= tlo) issue(t - 3, st0);
       compute(t - 1, st1.k, st1.v);
+      if (t - 2 < tlo) break;
+      wait_tile(t - 3 >= tlo);
       __syncthreads();
+      if (t - 4 >= tlo) issue(t - 4, st1);
+      compute(t - 2, st2.k, st2.v);
     }
     thi = tlo;
   }
@@ -610,28 +616,37 @@ extern "C" int cs_ccpe_prefill_bf16(const void* q, int64_t q_s_batch, int64_t q_
   p.hq = hq;
   p.hkv = hkv;
   p.group = group;
-  p.rows_per_wg = kWgCols / group;
+  // 4 wavefronts (128 columns): two workgroups per CU while the QE table is
+  // small enough, so one workgroup's prologue and barriers overlap the other's
+  // tile loop; larger tables use 8 wavefronts, one workgroup per CU
+  const size_t tab4 = 2 * 4 * kCols * static_cast<size_t>(max_positions + 2);
+  const int waves = 2 * (tab4 + kStaticLds) <= kLdsLimit ? 4 : 8;
+  p.rows_per_wg = kCols * waves / group;
   p.row_blocks = static_cast<int32_t>(ceil_div(nq, p.rows_per_wg));
   p.nk = nk;
   p.e = e;
   p.npos = max_positions;
-  p.tab_stride = max_positions + 1;
+  p.tab_stride = max_positions + 2;  // halfs; an odd number of 32-bit words per column
   p.out = static_cast<uint16_t*>(out);
   p.flags = flags;
   const int64_t total = static_cast<int64_t>(batch) * hkv * p.row_blocks;
   CS_REQUIRE(total < (1ll << 31), "grid too large");
   p.total_wg = static_cast<int32_t>(total);
-  const size_t smem = sizeof(float) * kWgCols * p.tab_stride;
+  const size_t smem = 2 * kCols * waves * static_cast<size_t>(p.tab_stride);
   if (smem + kStaticLds > kLdsLimit) {
     set_error("prefill LDS %zu bytes exceeds the workgroup limit", smem + kStaticLds);
     return CS_EUNSUPPORTED;
   }
-  if (p.kv.block_table)
-    hipLaunchKernelGGL(ccpe_prefill_kernel<true>, dim3(p.total_wg), dim3(kThreads), smem,
-                       as_stream(stream), p);
+  const dim3 grid(p.total_wg), block(64 * waves);
+  hipStream_t s = as_stream(stream);
+  if (p.kv.block_table && waves == 8)
+    hipLaunchKernelGGL((ccpe_prefill_kernel<true, 8>), grid, block, smem, s, p);
+  else if (p.kv.block_table)
+    hipLaunchKernelGGL((ccpe_prefill_kernel<true, 4>), grid, block, smem, s, p);
+  else if (waves == 8)
+    hipLaunchKernelGGL((ccpe_prefill_kernel<false, 8>), grid, block, smem, s, p);
   else
-    hipLaunchKernelGGL(ccpe_prefill_kernel<false>, dim3(p.total_wg), dim3(kThreads), smem,
-                       as_stream(stream), p);
+    hipLaunchKernelGGL((ccpe_prefill_kernel<false, 4>), grid, block, smem, s, p);
   CS_LAUNCH_CHECK("ccpe_prefill");
   return CS_OK;
 }
