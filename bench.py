@@ -228,6 +228,144 @@ def decode_measure(device, steps: int, warmup: int):
     }
 
 
+def note(message: str) -> None:
+    """Progress line on stderr (stdout carries only the JSON record)."""
+    print(f"bench: {message}", file=sys.stderr, flush=True)
+
+
+def slide_measure(device, steps: int, layers: int = 32) -> dict:
+    """SLIDE relocation step on a stacked paged cache [L, 100000 blocks, 8 heads,
+    16, 256] bf16: 512 reused chunks of 64..2048 tokens move from their current
+    slots to a seeded random permutation of free blocks -- whole pages by page
+    copy, the partial last page by slot copy -- then the token -> slot map is
+    rewritten (scatter) and read back (gather), and the source slots return to
+    the free list.  Moves are byte copies; the step is checked bit-exact."""
+    import numpy as np
+    import torch
+
+    from cacheslide_amd import relocate
+
+    NB, HKV, BS, REC, CHUNKS = 100_000, 8, 16, 256, 512
+    rng = np.random.default_rng(3000)
+    lens = rng.integers(64, 2049, CHUNKS)
+    pages = [(int(n) + BS - 1) // BS for n in lens]
+    perm = rng.permutation(NB)
+    need = sum(pages)
+    src_blk = perm[:need]
+    dst_blk = perm[need:2 * need]
+    full_src, full_dst, part_src, part_dst, tok_all, slot_all = [], [], [], [], [], []
+    at, tok0 = 0, 0
+    for n, pg in zip(lens.tolist(), pages):
+        sb, db = src_blk[at:at + pg], dst_blk[at:at + pg]
+        at += pg
+        nfull = n // BS
+        full_src.extend(sb[:nfull].tolist())
+        full_dst.extend(db[:nfull].tolist())
+        for t in range(nfull * BS, n):
+            part_src.append(int(sb[t // BS]) * BS + t % BS)
+            part_dst.append(int(db[t // BS]) * BS + t % BS)
+        slots = (np.repeat(db, BS)[:n] * BS + np.tile(np.arange(BS), pg)[:n]).tolist()
+        tok_all.extend(range(tok0, tok0 + n))
+        slot_all.extend(slots)
+        tok0 += n
+    T = int(lens.sum())
+    torch.cuda.empty_cache()
+    cache = torch.empty((layers, NB, HKV, BS, REC), dtype=torch.bfloat16, device=device)
+    cache.view(torch.int16).random_(generator=torch.Generator(device=device).manual_seed(3001))
+    dev = lambda xs: torch.tensor(xs, dtype=torch.long, device=device)  # noqa: E731
+    fs, fd, ps, pd = dev(full_src), dev(full_dst), dev(part_src), dev(part_dst)
+    tokens, slots = dev(tok_all), dev(slot_all)
+    mapping = torch.full((T,), -1, dtype=torch.long, device=device)
+    free = relocate.SlotFreeList(NB * BS, device)
+    src_slots = dev((np.repeat(src_blk, BS) * BS + np.tile(np.arange(BS), need)).tolist())
+
+    def step():
+        relocate.copy_pages(cache, fs, fd)
+        relocate.copy_slots(cache, ps, pd)
+        relocate.scatter_mapping(mapping, tokens, slots)
+        relocate.gather_mapping(mapping, tokens)
+        free.release(src_slots)
+
+    ms = time_steps(step, steps, 2)
+    rec_bytes = layers * HKV * 2 * REC  # K and V of one token over all layers
+    moved = (len(full_src) * BS + len(part_src)) * rec_bytes
+    traffic = 2 * moved + T * 8 * 3 + src_slots.numel() * 8
+    bits = cache.view(torch.int16)  # compare bit patterns (random fill holds NaN encodings)
+    exact = bool(torch.equal(bits[:, fd[:64]], bits[:, fs[:64]]))
+    if ps.numel():
+        s_, d_ = ps[:64], pd[:64]
+        exact = exact and bool(torch.equal(bits[:, d_ // BS, :, d_ % BS], bits[:, s_ // BS, :, s_ % BS]))
+    exact = exact and bool(torch.equal(mapping, slots))
+    del cache
+    torch.cuda.empty_cache()
+    gbs = traffic / (ms * 1e-3) / 1e9
+    return {
+        "workload": f"slide relocation: {layers} layers x [100000 blocks, 8 heads, 16, 256] bf16, "
+                    f"512 chunks of 64..2048 tokens ({T} tokens) per step",
+        "ms_per_step": round(ms, 4),
+        "bytes_per_step": traffic,
+        "achieved_GBs": round(gbs, 1),
+        "hbm_frac": round(gbs / PEAK_HBM_GBS, 4),
+        "bit_exact": exact,
+    }
+
+
+def wca_measure(device, layers: int = 31) -> dict:
+    """WCA at Mistral-7B KV shape: 4 requests x 8 reused chunks of 2048 tokens
+    (T = 16384), 8 KV heads x 128, bf16; cached KV = recomputed KV + N(0, 0.05)
+    drift; correction fraction 0.15, gate every 4 layers.  Times
+    WCAState.initialize (full-T deviation scoring and top-k selection) and the
+    per-layer WCAState.update (score, weights, blend, gate, commit, promote),
+    host checks included, as the runtime calls them."""
+    import torch
+
+    from cacheslide_amd import WCAConfig, WCAState
+
+    R, T, H, D = 4, 16384, 8, 128
+    gen = torch.Generator(device=device).manual_seed(4000)
+    config = WCAConfig(correction_fraction=0.15)
+    reqs = []
+    for _ in range(R):
+        new_k = torch.randn((T, H, D), generator=gen, device=device).to(torch.bfloat16)
+        new_v = torch.randn((T, H, D), generator=gen, device=device).to(torch.bfloat16)
+        old_k = (new_k.float() + 0.05 * torch.randn((T, H, D), generator=gen, device=device)).to(torch.bfloat16)
+        old_v = (new_v.float() + 0.05 * torch.randn((T, H, D), generator=gen, device=device)).to(torch.bfloat16)
+        reused = torch.ones(T, dtype=torch.bool, device=device)
+        reused[-1] = False
+        mandatory = ~reused
+        reqs.append((new_k, new_v, old_k, old_v, reused, mandatory))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    states = [WCAState.initialize(o_k, n_k, ru, ma, config) for n_k, n_v, o_k, o_v, ru, ma in reqs]
+    torch.cuda.synchronize()
+    init_ms = (time.perf_counter() - t0) * 1e3 / R
+    upd_s, upd_bytes, rows = 0.0, 0, 0
+    for layer in range(2, 2 + layers):
+        for st, (n_k, n_v, o_k, o_v, _, _) in zip(states, reqs):
+            idx = st.active_indices
+            rk, rv = n_k.index_select(0, idx), n_v.index_select(0, idx)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            st.update(layer, o_k, o_v, rk, rv)
+            torch.cuda.synchronize()
+            upd_s += time.perf_counter() - t0
+            a = idx.numel()
+            rows += a
+            upd_bytes += 6 * a * H * D * 2  # old and new K, V rows read; fused K, V written
+    n_upd = layers * R
+    return {
+        "workload": "wca: 4 requests x 8 chunks x 2048 tokens, 8 kv heads x 128, bf16, "
+                    f"fraction 0.15, layer 1 full then {layers} layer updates each",
+        "initialize_ms_per_request": round(init_ms, 4),
+        "initialize_GBs": round(2 * T * H * D * 2 / (init_ms * 1e-3) / 1e9, 1),
+        "update_ms_per_layer": round(upd_s * 1e3 / n_upd, 4),
+        "active_rows_per_update": round(rows / n_upd, 1),
+        "update_GBs": round(upd_bytes / upd_s / 1e9, 1),
+        "note": "update includes the host reads of the numeric-check flags and counts "
+                "(transactional API), which bound it far below HBM speed",
+    }
+
+
 def copy_calibration(device, nbytes: int, steps: int) -> dict:
     """A plain device copy of a known size, for scaling HBM counters
     (FETCH_SIZE / WRITE_SIZE) read under rocprofv3 --pmc."""
@@ -247,10 +385,13 @@ def main() -> int:
                     help="only time a plain device copy of BYTES (counter calibration)")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--cpu-heads", type=int, default=2)
+    ap.add_argument("--no-slide", action="store_true")
+    ap.add_argument("--slide-layers", type=int, default=32)
+    ap.add_argument("--no-wca", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -267,6 +408,7 @@ def main() -> int:
     ms = time_steps(step, args.steps, args.warmup)
     flops = prefill_flops(shape["B"], shape["HQ"], shape["N"], shape["D"], shape["P"])
     tflops = flops / (ms * 1e-3) / 1e12
+    note(f"prefill: {ms:.3f} ms/step")
     check_err = spot_check_prefill(inputs, host, shape)
     if check_err > 2e-2:
         print(f"prefill spot check failed: max abs error {check_err}", file=sys.stderr)
@@ -304,7 +446,18 @@ def main() -> int:
     del inputs
     torch.cuda.empty_cache()
     if not args.no_decode:
-        record["decode"] = decode_measure(device, max(5, args.steps // 5), 2)
+        record["decode"] = decode_measure(device, max(5, args.steps // 5), 5)
+        note(f"decode: {record['decode']['ms_per_call']} ms/call")
+    if not args.no_slide:
+        try:
+            record["slide"] = slide_measure(device, max(3, args.steps // 10), args.slide_layers)
+        except torch.cuda.OutOfMemoryError as error:  # pragma: no cover - depends on the device
+            record["slide"] = {"error": f"out of memory: {error}"}
+            torch.cuda.empty_cache()
+        note(f"slide: {record['slide'].get('ms_per_step')} ms/step")
+    if not args.no_wca:
+        record["wca"] = wca_measure(device)
+        note(f"wca: {record['wca']['update_ms_per_layer']} ms/layer update")
     if not args.no_cpu_baseline:
         record["cpu_baseline"] = cpu_baseline(host, shape, args.cpu_heads)
     print(json.dumps(record), flush=True)
