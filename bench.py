@@ -334,6 +334,12 @@ def wca_measure(device, layers: int = 31) -> dict:
         reused[-1] = False
         mandatory = ~reused
         reqs.append((new_k, new_v, old_k, old_v, reused, mandatory))
+    # untimed warm-up: first-call library and allocator set-up
+    n_k, n_v, o_k, o_v, ru, ma = reqs[0]
+    warm = WCAState.initialize(o_k, n_k, ru, ma, config)
+    idx = warm.active_indices
+    warm.update(2, o_k, o_v, n_k.index_select(0, idx), n_v.index_select(0, idx))
+    del warm
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     states = [WCAState.initialize(o_k, n_k, ru, ma, config) for n_k, n_v, o_k, o_v, ru, ma in reqs]
@@ -361,8 +367,8 @@ def wca_measure(device, layers: int = 31) -> dict:
         "update_ms_per_layer": round(upd_s * 1e3 / n_upd, 4),
         "active_rows_per_update": round(rows / n_upd, 1),
         "update_GBs": round(upd_bytes / upd_s / 1e9, 1),
-        "note": "update includes the host reads of the numeric-check flags and counts "
-                "(transactional API), which bound it far below HBM speed",
+        "note": "wall-clock per call, host validation and the one status readback per call "
+                "included (transactional API)",
     }
 
 

@@ -147,14 +147,14 @@ SIGNATURES = {
     "cs_freelist_acquire": (_I32, [_P, _I64, _I64, _P, _P, _P]),
     "cs_wca_score": (_I32, [_VP, _P, _VP, _P, _P, _P, _P]),
     "cs_wca_alpha": (_I32, [_P, _P, _I64, ctypes.c_double, _I32, _P, _P, _P]),
-    "cs_wca_promote": (_I32, [_P, _P, _P, _P, _I64, _I64, _P, _P, _P, _P]),
+    "cs_wca_promote": (_I32, [_P, _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _I32, _P]),
     "cs_mask_nonzero": (_I32, [_P, _P, _I64, _P, _P, _P]),
     "cs_wca_blend": (_I32, [_VP, _VP, _P, _VP, _VP, _P, _P, _VP, _VP, _P, _P]),
     "cs_wca_head_cosine": (_I32, [_VP, _VP, _P, ctypes.c_double, _P, _P]),
     "cs_wca_init_masks": (_I32, [_P, _P, _P, _I64, _P, _P, _P, _P]),
     "cs_wca_used_alpha": (_I32, [_P, _P, _P, _P, _I64, _I32, _P, _P]),
     "cs_wca_gate": (_I32, [_P, _P, _P, _I64, _I32, ctypes.c_double, _P, _P, _P]),
-    "cs_wca_commit": (_I32, [_P, _P, _P, _I64, _P, _I64, _P, _P, _P, _P]),
+    "cs_wca_commit": (_I32, [_P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _I32, _P]),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -68,7 +68,39 @@ __device__ inline double dd_round(dd v) {
   return s;
 }
 
-// One wavefront per token.
+struct score_acc {
+  dd e{0.0, 0.0}, n{0.0, 0.0};
+  int bad = 0;
+  __device__ void add(double o, double f) {
+    if (!isfinite(o) || !isfinite(f)) bad = 1;
+    const double diff = f - o;
+    const double sq = diff * diff;
+    const double osq = o * o;
+    e = dd_add_double(e, sq);
+    n = dd_add_double(n, osq);
+  }
+  // Wave reduction; lane 0 stores err[i], norm[i] and the flags.
+  __device__ void finish(int lane, int64_t i, double* err, double* norm, int32_t* flags) {
+    e = dd_wave_sum(e);
+    n = dd_wave_sum(n);
+    const int any_bad = __any(bad);
+    if (lane == 0) {
+      double ev = dd_round(e), nv = dd_round(n);
+      // an infinite term makes hi infinite and lo NaN; report it as overflow
+      if (!isfinite(e.hi)) ev = e.hi != e.hi ? e.hi : INFINITY;
+      if (!isfinite(n.hi)) nv = n.hi != n.hi ? n.hi : INFINITY;
+      err[i] = ev;
+      norm[i] = nv;
+      int f = 0;
+      if (any_bad) f |= 1;
+      if (!isfinite(ev)) f |= 2;
+      if (!isfinite(nv)) f |= 16;
+      if (f) atomicOr(flags, f);
+    }
+  }
+};
+
+// One wavefront per token, any dtype and strides.
 __global__ void __launch_bounds__(64 * kWaves) wca_score_kernel(dview old_src,
                                                                 const int64_t* old_rows,
                                                                 dview fresh, double* err,
@@ -78,38 +110,43 @@ __global__ void __launch_bounds__(64 * kWaves) wca_score_kernel(dview old_src,
   const int64_t n = fresh.shape[0], H = fresh.shape[1], D = fresh.shape[2];
   if (i >= n) return;
   const int64_t row = old_rows ? old_rows[i] : i;
-  dd e_acc{0.0, 0.0}, n_acc{0.0, 0.0};
-  int bad = 0;
+  score_acc acc;
   const int64_t HD = H * D;
   for (int64_t x = lane; x < HD; x += 64) {
     int64_t h = x / D, d = x % D;
-    double o = load_as_double(old_src.data, old_src.dtype,
-                              row * old_src.stride[0] + h * old_src.stride[1] + d * old_src.stride[2]);
-    double f = load_as_double(fresh.data, fresh.dtype,
-                              i * fresh.stride[0] + h * fresh.stride[1] + d * fresh.stride[2]);
-    if (!isfinite(o) || !isfinite(f)) bad = 1;
-    double diff = f - o;
-    double sq = diff * diff;
-    double osq = o * o;
-    e_acc = dd_add_double(e_acc, sq);
-    n_acc = dd_add_double(n_acc, osq);
+    acc.add(load_as_double(old_src.data, old_src.dtype,
+                           row * old_src.stride[0] + h * old_src.stride[1] + d * old_src.stride[2]),
+            load_as_double(fresh.data, fresh.dtype,
+                           i * fresh.stride[0] + h * fresh.stride[1] + d * fresh.stride[2]));
   }
-  e_acc = dd_wave_sum(e_acc);
-  n_acc = dd_wave_sum(n_acc);
-  int any_bad = __any(bad);
-  if (lane == 0) {
-    double ev = dd_round(e_acc), nv = dd_round(n_acc);
-    // an infinite term makes hi infinite and lo NaN; report it as overflow
-    if (!isfinite(e_acc.hi)) ev = e_acc.hi != e_acc.hi ? e_acc.hi : INFINITY;
-    if (!isfinite(n_acc.hi)) nv = n_acc.hi != n_acc.hi ? n_acc.hi : INFINITY;
-    err[i] = ev;
-    norm[i] = nv;
-    int f = 0;
-    if (any_bad) f |= 1;
-    if (!isfinite(ev)) f |= 2;
-    if (!isfinite(nv)) f |= 16;
-    if (f) atomicOr(flags, f);
+  acc.finish(lane, i, err, norm, flags);
+}
+
+// bf16 rows whose [H, D] block is contiguous and 16-byte aligned: one
+// wavefront per token, 8 elements per 16-byte load.  The per-token sums are
+// exact, so the result matches the generic kernel's.
+__global__ void __launch_bounds__(64 * kWaves) wca_score_bf16_kernel(
+    const uint16_t* old_base, int64_t old_stride, const int64_t* old_rows,
+    const uint16_t* new_base, int64_t new_stride, int64_t n, int64_t words, double* err,
+    double* norm, int32_t* flags) {
+  const int lane = threadIdx.x & 63;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+  if (i >= n) return;
+  const int64_t row = old_rows ? old_rows[i] : i;
+  const uint4* o = reinterpret_cast<const uint4*>(old_base + row * old_stride);
+  const uint4* f = reinterpret_cast<const uint4*>(new_base + i * new_stride);
+  score_acc acc;
+  for (int64_t w = lane; w < words; w += 64) {
+    const uint4 ov = o[w], fv = f[w];
+    const uint32_t ow[4] = {ov.x, ov.y, ov.z, ov.w}, fw[4] = {fv.x, fv.y, fv.z, fv.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      acc.add(bf16_to_float(static_cast<uint16_t>(ow[q])), bf16_to_float(static_cast<uint16_t>(fw[q])));
+      acc.add(bf16_to_float(static_cast<uint16_t>(ow[q] >> 16)),
+              bf16_to_float(static_cast<uint16_t>(fw[q] >> 16)));
+    }
   }
+  acc.finish(lane, i, err, norm, flags);
 }
 
 __global__ void wca_alpha_kernel(const double* err, const double* norm, int64_t n, double eps,
@@ -127,8 +164,14 @@ __global__ void wca_alpha_kernel(const double* err, const double* norm, int64_t 
   if (f) atomicOr(flags, f);
 }
 
-// ------------------------------------------------------------ promotion
+// ------------------------------------------------------------ selection
+// Selection kernels run as one workgroup of 1024 threads.  Each thread owns a
+// run of kRun consecutive tokens per chunk of kChunk tokens, so one block scan
+// per chunk orders a whole 16384-token request.
 constexpr int kSelThreads = 1024;
+constexpr int kSelWaves = kSelThreads / 64;
+constexpr int kRun = 16;
+constexpr int64_t kChunk = static_cast<int64_t>(kSelThreads) * kRun;
 
 __device__ inline uint64_t key_bits(double k) {
   uint64_t u = __double_as_longlong(k);
@@ -136,45 +179,122 @@ __device__ inline uint64_t key_bits(double k) {
   return (u >> 63) ? 0ull : u;
 }
 
-// Block-wide exclusive scan of one int per thread; returns the total.
-__device__ inline int block_exclusive_scan(int v, int* tmp, int& excl) {
-  const int tid = threadIdx.x;
-  tmp[tid] = v;
-  __syncthreads();
-  for (int o = 1; o < kSelThreads; o <<= 1) {
-    int add = tid >= o ? tmp[tid - o] : 0;
-    __syncthreads();
-    tmp[tid] += add;
-    __syncthreads();
+// Block-wide exclusive scan of one int per thread; returns the total.  Wave
+// scans by lane shifts, then one pass over the 16 wave totals.
+__device__ inline int block_scan(int v, int* wave_tot, int& excl) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int incl = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int t = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += t;
   }
-  int incl = tmp[tid];
-  int total = tmp[kSelThreads - 1];
+  if (lane == 63) wave_tot[w] = incl;
   __syncthreads();
-  excl = incl - v;
+  int before = 0, total = 0;
+#pragma unroll
+  for (int i = 0; i < kSelWaves; ++i) {
+    const int t = wave_tot[i];
+    before += i < w ? t : 0;
+    total += t;
+  }
+  __syncthreads();
+  excl = before + incl - v;
   return total;
 }
 
+// Bit j set when p[start + j] != 0 (j < kRun, start + j < n).
+__device__ inline uint32_t run_mask(const uint8_t* p, int64_t start, int64_t n) {
+  uint32_t m = 0;
+  if (start + kRun <= n && (reinterpret_cast<uintptr_t>(p + start) & 15) == 0) {
+    const uint4 v = *reinterpret_cast<const uint4*>(p + start);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+        if ((w[q] >> (8 * b)) & 0xffu) m |= 1u << (4 * q + b);
+  } else {
+    for (int j = 0; j < kRun; ++j)
+      if (start + j < n && p[start + j]) m |= 1u << j;
+  }
+  return m;
+}
+
+// key_bits of key[start + j], j < kRun: one batch of 16-byte loads when the
+// run is whole (start is a multiple of kRun, so 128-byte aligned for an
+// aligned base), clamped scalar loads for the last partial run.
+__device__ inline void load_key_run(const double* key, int64_t start, int64_t n, uint64_t kb[kRun]) {
+  if (start + kRun <= n && (reinterpret_cast<uintptr_t>(key + start) & 15) == 0) {
+    const uint4* p = reinterpret_cast<const uint4*>(key + start);
+    uint4 v[kRun / 2];
+#pragma unroll
+    for (int q = 0; q < kRun / 2; ++q) v[q] = p[q];
+#pragma unroll
+    for (int q = 0; q < kRun / 2; ++q) {
+      kb[2 * q] = key_bits(__longlong_as_double((static_cast<uint64_t>(v[q].y) << 32) | v[q].x));
+      kb[2 * q + 1] = key_bits(__longlong_as_double((static_cast<uint64_t>(v[q].w) << 32) | v[q].z));
+    }
+  } else {
+    const int64_t last = n - 1;
+#pragma unroll
+    for (int j = 0; j < kRun; ++j) kb[j] = key_bits(key[start + j < n ? start + j : last]);
+  }
+}
+
+// Add one to hist[bin] for every lane with bin >= 0.  Lanes that share the
+// first lane's bin are counted with one atomic (up to four rounds), which
+// removes the serialisation of many equal bins; the rest add individually.
+__device__ inline void hist_add(int* hist, int bin) {
+  const int lane = threadIdx.x & 63;
+  bool pending = bin >= 0;
+#pragma unroll
+  for (int round = 0; round < 4; ++round) {
+    const uint64_t live = __ballot(pending);
+    if (live == 0) return;
+    const int leader = __ffsll(static_cast<unsigned long long>(live)) - 1;
+    const int lb = __shfl(bin, leader, 64);
+    const uint64_t same = __ballot(pending && bin == lb);
+    if (lane == leader) atomicAdd(&hist[lb], __popcll(same));
+    if (pending && bin == lb) pending = false;
+  }
+  if (pending) atomicAdd(&hist[bin], 1);
+}
+
+// WCAState._promote, first half: radix select of the k-th largest available
+// key (8-bit digits, most significant first, stopping once the chosen digit's
+// bucket is taken whole), then one pass that marks the taken tokens selected
+// and compacts them in index order into scratch[0..k), their key bits into
+// scratch[n..n+k).  Skips everything
+// (count 0) when abort_flags has a bit of abort_mask set, so a failed update
+// leaves the selection unchanged.
 __global__ void __launch_bounds__(kSelThreads) wca_promote_kernel(
     const double* key, const uint8_t* candidate, const uint8_t* removed, uint8_t* selected,
-    int64_t n, int64_t budget, int64_t* scratch, int64_t* promoted, int64_t* count_out) {
+    int64_t n, int64_t budget, int64_t* scratch, int64_t* count_out,
+    const int32_t* abort_flags, int32_t abort_mask) {
   __shared__ int hist[256];
-  __shared__ int scan_tmp[kSelThreads];
+  __shared__ int wave_tot[kSelWaves];
   __shared__ uint64_t s_prefix, s_mask;
-  __shared__ int64_t s_remaining, s_k;
-  __shared__ uint64_t tile_key[kSelThreads];
-  __shared__ int tile_sel[kSelThreads];
-  const int tid = threadIdx.x;
+  __shared__ int64_t s_remaining;
+  __shared__ int s_done;
+  const int tid = threadIdx.x, lane = tid & 63;
+  if (abort_flags && (*abort_flags & abort_mask)) {
+    if (tid == 0) *count_out = 0;
+    return;
+  }
 
   // slots = max(0, budget - #selected); available = candidate & ~selected & ~removed
   int cnt_sel = 0, cnt_av = 0;
-  for (int64_t t = tid; t < n; t += kSelThreads) {
-    bool s = selected[t] != 0;
-    cnt_sel += s;
-    cnt_av += (candidate[t] && !s && !removed[t]);
+  for (int64_t c0 = 0; c0 < n; c0 += kChunk) {
+    const int64_t s = c0 + static_cast<int64_t>(tid) * kRun;
+    const uint32_t sel = run_mask(selected, s, n);
+    const uint32_t av = run_mask(candidate, s, n) & ~sel & ~run_mask(removed, s, n);
+    cnt_sel += __popc(sel);
+    cnt_av += __popc(av);
   }
   int ex;
-  int total_sel = block_exclusive_scan(cnt_sel, scan_tmp, ex);
-  int total_av = block_exclusive_scan(cnt_av, scan_tmp, ex);
+  const int total_sel = block_scan(cnt_sel, wave_tot, ex);
+  const int total_av = block_scan(cnt_av, wave_tot, ex);
   int64_t slots = budget - total_sel;
   if (slots < 0) slots = 0;
   const int64_t k = slots < total_av ? slots : total_av;
@@ -182,124 +302,174 @@ __global__ void __launch_bounds__(kSelThreads) wca_promote_kernel(
     s_prefix = 0;
     s_mask = 0;
     s_remaining = k;
-    s_k = k;
+    s_done = k == total_av;  // every available token is taken
     *count_out = k;
   }
   __syncthreads();
   if (k == 0) return;
 
-  // Radix select (8 x 8 bits, most significant first) of the k-th largest key.
-  for (int pass = 0; pass < 8; ++pass) {
+  // A request of at most one chunk keeps its keys and availability in registers.
+  const bool single = n <= kChunk;
+  uint64_t kb[kRun] = {};
+  uint32_t av = 0;
+  if (single) {
+    const int64_t s = static_cast<int64_t>(tid) * kRun;
+    av = run_mask(candidate, s, n) & ~run_mask(selected, s, n) & ~run_mask(removed, s, n);
+    if (s < n) load_key_run(key, s, n, kb);
+  }
+  for (int pass = 0; pass < 8 && !s_done; ++pass) {
     const int shift = 56 - 8 * pass;
     for (int i = tid; i < 256; i += kSelThreads) hist[i] = 0;
     __syncthreads();
     const uint64_t prefix = s_prefix, mask = s_mask;
-    for (int64_t t = tid; t < n; t += kSelThreads) {
-      if (candidate[t] && !selected[t] && !removed[t]) {
-        uint64_t kb = key_bits(key[t]);
-        if ((kb & mask) == prefix) atomicAdd(&hist[(kb >> shift) & 255], 1);
+    for (int64_t c0 = 0; c0 < n; c0 += kChunk) {
+      const int64_t s = c0 + static_cast<int64_t>(tid) * kRun;
+      if (!single) {
+        av = run_mask(candidate, s, n) & ~run_mask(selected, s, n) & ~run_mask(removed, s, n);
+        if (s < n) load_key_run(key, s, n, kb);
+      }
+#pragma unroll
+      for (int j = 0; j < kRun; ++j) {
+        const bool in = ((av >> j) & 1u) && (kb[j] & mask) == prefix;
+        hist_add(hist, in ? static_cast<int>((kb[j] >> shift) & 255) : -1);
       }
     }
     __syncthreads();
-    if (tid == 0) {
-      int64_t need = s_remaining, cum = 0;
-      int chosen = 0;
-      for (int bin = 255; bin >= 0; --bin) {
-        if (cum + hist[bin] >= need) {
-          chosen = bin;
-          need -= cum;
-          break;
+    if (tid < 64) {
+      // Bins 4*lane .. 4*lane+3; find the bin where the count from the top reaches need.
+      int hb[4], mine = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        hb[q] = hist[4 * lane + q];
+        mine += hb[q];
+      }
+      int above = mine;  // inclusive suffix sum over lanes >= lane
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int t = __shfl_down(above, d, 64);
+        if (lane + d < 64) above += t;
+      }
+      above -= mine;  // lanes strictly above
+      const int64_t need = s_remaining;
+      if (above < need && above + mine >= need) {
+        int64_t cum = above;
+        for (int q = 3; q >= 0; --q) {
+          if (cum + hb[q] >= need) {
+            const int bin = 4 * lane + q;
+            s_remaining = need - cum;
+            s_prefix = prefix | (static_cast<uint64_t>(bin) << shift);
+            s_mask = mask | (255ull << shift);
+            s_done = (need - cum) == hb[q];
+            break;
+          }
+          cum += hb[q];
         }
-        cum += hist[bin];
       }
-      s_remaining = need;
-      s_prefix = prefix | (static_cast<uint64_t>(chosen) << shift);
-      s_mask = mask | (255ull << shift);
     }
     __syncthreads();
   }
-  const uint64_t thr = s_prefix;
-  const int64_t need_eq = s_remaining;  // how many keys equal to thr are taken
+  const uint64_t thr = s_prefix, mask = s_mask;
+  const int64_t need_eq = s_remaining;  // keys equal to thr (under mask) taken, lowest index first
 
-  // Mark the selection: all keys > thr, plus the need_eq lowest-index keys == thr.
-  // The new marks go to bit 1 of selected[] until the ordering pass is done.
-  int64_t eq_seen = 0;
-  for (int64_t c0 = 0; c0 < n; c0 += kSelThreads) {
-    int64_t t = c0 + tid;
-    int flag_gt = 0, flag_eq = 0;
-    if (t < n && candidate[t] && !selected[t] && !removed[t]) {
-      uint64_t kb = key_bits(key[t]);
-      flag_gt = kb > thr;
-      flag_eq = kb == thr;
+  // Mark and compact: all keys above thr, plus the need_eq lowest-index keys equal to it.
+  int64_t eq_seen = 0, base = 0;
+  for (int64_t c0 = 0; c0 < n; c0 += kChunk) {
+    const int64_t s = c0 + static_cast<int64_t>(tid) * kRun;
+    if (!single) {
+      av = run_mask(candidate, s, n) & ~run_mask(selected, s, n) & ~run_mask(removed, s, n);
+      if (s < n) load_key_run(key, s, n, kb);
     }
-    int rank;
-    int tot = block_exclusive_scan(flag_eq, scan_tmp, rank);
-    if (t < n && (flag_gt || (flag_eq && eq_seen + rank < need_eq))) selected[t] |= 2;
-    eq_seen += tot;
-  }
-  __threadfence_block();
-  __syncthreads();
-
-  // Compact the new selection (index order) into scratch[0..k).
-  int64_t base = 0;
-  for (int64_t c0 = 0; c0 < n; c0 += kSelThreads) {
-    int64_t t = c0 + tid;
-    int f = (t < n && (selected[t] & 2)) ? 1 : 0;
-    int ex2;
-    int tot = block_exclusive_scan(f, scan_tmp, ex2);
-    if (f) scratch[base + ex2] = t;
+    uint32_t gt = 0, eq = 0;
+#pragma unroll
+    for (int j = 0; j < kRun; ++j) {
+      const uint64_t km = kb[j] & mask;
+      if (((av >> j) & 1u) && km > thr) gt |= 1u << j;
+      if (((av >> j) & 1u) && km == thr) eq |= 1u << j;
+    }
+    int eq_rank;
+    const int eq_tot = block_scan(__popc(eq), wave_tot, eq_rank);
+    uint32_t take = gt;
+    for (uint32_t m = eq; m; m &= m - 1) {
+      if (eq_seen + eq_rank < need_eq) take |= m & (~m + 1);
+      ++eq_rank;
+    }
+    int pos;
+    const int tot = block_scan(__popc(take), wave_tot, pos);
+    for (uint32_t m = take; m; m &= m - 1) {
+      const int j = __ffs(m) - 1;
+      scratch[base + pos] = s + j;
+      scratch[n + base + pos] = static_cast<int64_t>(kb[j]);
+      ++pos;
+      selected[s + j] = 1;
+    }
+    eq_seen += eq_tot;
     base += tot;
   }
-  __threadfence_block();
-  __syncthreads();
-  // Order by (key desc, index asc): rank_i = #{j: key_j > key_i} + #{j: key_j == key_i, j < i}
-  // over the k compacted entries, staged through LDS tiles.
-  for (int64_t c0 = 0; c0 < k; c0 += kSelThreads) {
-    const int64_t i = c0 + tid;
-    const bool mine = i < k;
-    const int64_t ti = mine ? scratch[i] : 0;
-    const uint64_t ki = mine ? key_bits(key[ti]) : 0;
-    int64_t rank = 0;
-    for (int64_t d0 = 0; d0 < k; d0 += kSelThreads) {
-      const int64_t j = d0 + tid;
-      __syncthreads();
-      tile_sel[tid] = j < k ? static_cast<int>(scratch[j]) : -1;
-      tile_key[tid] = j < k ? key_bits(key[scratch[j]]) : 0;
-      __syncthreads();
-      if (mine) {
-        const int lim = (k - d0) < kSelThreads ? static_cast<int>(k - d0) : kSelThreads;
-        for (int x = 0; x < lim; ++x) {
-          const uint64_t kj = tile_key[x];
-          if (kj > ki || (kj == ki && tile_sel[x] < ti)) ++rank;
-        }
-      }
-    }
-    if (mine) promoted[rank] = ti;
-  }
-  __syncthreads();
-  for (int64_t t = tid; t < n; t += kSelThreads)
-    if (selected[t] & 2) selected[t] = 1;
 }
 
-// Ascending indices of (a[t] | b[t]) (b may be null): single workgroup.
+// Second half of the promotion: orders the k = *count promoted tokens
+// (scratch[0..k) in index order, their key bits at scratch[n..n+k)) by (key
+// descending, index ascending): rank_i = #{j: key_j > key_i} + #{j < i:
+// key_j == key_i}.  A workgroup ranks 64 entries (one per lane); each of its
+// 16 wavefronts counts over a sixteenth of the keys, read as wave-uniform
+// scalar loads, and the partial counts are summed through LDS.
+constexpr int kOrderSlices = 16;
+
+__global__ void __launch_bounds__(64 * kOrderSlices) wca_promote_order_kernel(
+    const int64_t* scratch, int64_t n, const int64_t* count, int64_t* promoted) {
+  __shared__ int partial[kOrderSlices][64];
+  const int64_t k = *count;
+  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * 64;
+  if (e0 >= k) return;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint64_t* keys = reinterpret_cast<const uint64_t*>(scratch + n);
+  const int64_t i = e0 + lane;
+  const bool mine = i < k;
+  const uint64_t ki = keys[mine ? i : e0];
+  const int64_t per = (k + kOrderSlices - 1) / kOrderSlices;
+  const int64_t j0 = w * per < k ? w * per : k;
+  const int64_t j1 = j0 + per < k ? j0 + per : k;
+  int rank = 0;
+  int64_t j = j0;
+  for (; j + 8 <= j1; j += 8) {
+    uint64_t kj[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) kj[u] = keys[j + u];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) rank += (kj[u] > ki) || (kj[u] == ki && j + u < i);
+  }
+  for (; j < j1; ++j) {
+    const uint64_t kj = keys[j];
+    rank += (kj > ki) || (kj == ki && j < i);
+  }
+  partial[w][lane] = rank;
+  __syncthreads();
+  if (w == 0 && mine) {
+    int r = 0;
+#pragma unroll
+    for (int q = 0; q < kOrderSlices; ++q) r += partial[q][lane];
+    promoted[r] = scratch[i];
+  }
+}
+
+// Ascending indices of (a[t] | b[t]) (b may be null).
 __global__ void __launch_bounds__(kSelThreads) mask_nonzero_kernel(const uint8_t* a,
                                                                    const uint8_t* b, int64_t n,
-                                                                   int64_t* out,
-                                                                   int64_t* count) {
-  __shared__ int scan_tmp[kSelThreads];
+                                                                   int64_t* out, int64_t* count) {
+  __shared__ int wave_tot[kSelWaves];
   int64_t base = 0;
-  for (int64_t c0 = 0; c0 < n; c0 += kSelThreads) {
-    int64_t t = c0 + threadIdx.x;
-    int f = 0;
-    if (t < n) f = (a[t] != 0) || (b && b[t] != 0);
-    int ex;
-    int tot = block_exclusive_scan(f, scan_tmp, ex);
-    if (f) out[base + ex] = t;
+  for (int64_t c0 = 0; c0 < n; c0 += kChunk) {
+    const int64_t s = c0 + static_cast<int64_t>(threadIdx.x) * kRun;
+    uint32_t m = run_mask(a, s, n);
+    if (b) m |= run_mask(b, s, n);
+    int pos;
+    const int tot = block_scan(__popc(m), wave_tot, pos);
+    for (; m; m &= m - 1) out[base + pos++] = s + (__ffs(m) - 1);
     base += tot;
   }
   if (threadIdx.x == 0) *count = base;
 }
-
 // fused = w * new + (1 - w) * old.  One thread per element of [a, H, D].
 __global__ void wca_blend_kernel(dview old_k, dview old_v, const int64_t* rows, dview new_k,
                                  dview new_v, const double* weight, const uint8_t* mandatory,
@@ -327,6 +497,52 @@ __global__ void wca_blend_kernel(dview old_k, dview old_v, const int64_t* rows, 
       store_from_double(fv.data, fv.dtype, off, f);
       double back = load_as_double(fv.data, fv.dtype, off);
       if (!isfinite(back)) bad = 1;
+    }
+  }
+  if (__any(bad) && (threadIdx.x & 63) == 0) atomicOr(flags, 8);
+}
+
+// bf16 fast path of the blend: rows with contiguous 16-byte aligned [H, D]
+// blocks, one thread per 8 elements of K and of V, same fp64 arithmetic.
+__device__ inline uint32_t blend_pair(uint32_t o, uint32_t nw, double w, double one_minus, int& bad) {
+  uint32_t out = 0;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const double od = bf16_to_float(static_cast<uint16_t>(o >> (16 * h)));
+    const double nd = bf16_to_float(static_cast<uint16_t>(nw >> (16 * h)));
+    const double t1 = w * nd;
+    const double t2 = one_minus * od;
+    const uint16_t r = double_to_bf16(t1 + t2);
+    if ((r & 0x7f80u) == 0x7f80u) bad = 1;
+    out |= static_cast<uint32_t>(r) << (16 * h);
+  }
+  return out;
+}
+
+__global__ void wca_blend_bf16_kernel(const uint16_t* old_k, int64_t ok_s, const uint16_t* old_v,
+                                      int64_t ov_s, const int64_t* rows, const uint16_t* new_k,
+                                      int64_t nk_s, const uint16_t* new_v, int64_t nv_s,
+                                      const double* weight, const uint8_t* mandatory,
+                                      uint16_t* fused_k, int64_t fk_s, uint16_t* fused_v,
+                                      int64_t fv_s, int64_t a, int64_t words, int32_t* flags) {
+  int bad = 0;
+  const int64_t total = a * words;
+  for (int64_t x = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; x < total;
+       x += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t i = x / words, w = x % words;
+    const int64_t row = rows ? rows[i] : i;
+    const double wt = (mandatory && mandatory[i]) ? 1.0 : weight[i];
+    const double one_minus = 1.0 - wt;
+#pragma unroll
+    for (int kv = 0; kv < 2; ++kv) {
+      const uint4 o = reinterpret_cast<const uint4*>((kv ? old_v : old_k) + row * (kv ? ov_s : ok_s))[w];
+      const uint4 nw = reinterpret_cast<const uint4*>((kv ? new_v : new_k) + i * (kv ? nv_s : nk_s))[w];
+      uint4 r;
+      r.x = blend_pair(o.x, nw.x, wt, one_minus, bad);
+      r.y = blend_pair(o.y, nw.y, wt, one_minus, bad);
+      r.z = blend_pair(o.z, nw.z, wt, one_minus, bad);
+      r.w = blend_pair(o.w, nw.w, wt, one_minus, bad);
+      reinterpret_cast<uint4*>((kv ? fused_v : fused_k) + i * (kv ? fv_s : fk_s))[w] = r;
     }
   }
   if (__any(bad) && (threadIdx.x & 63) == 0) atomicOr(flags, 8);
@@ -379,33 +595,127 @@ __global__ void __launch_bounds__(64 * kWaves) wca_cosine_kernel(dview a, dview 
   if (lane == 0) out[i] = total / static_cast<double>(H);
 }
 
+// bf16 fast path of mean_head_cosine: rows with contiguous 16-byte aligned
+// [H, D] blocks and D / 16 a power of two.  One wavefront per token; each head
+// is held by D / 16 lanes of 16 elements, reduced within those lanes; heads
+// are summed in ascending order as in the generic kernel.
+__global__ void __launch_bounds__(64 * kWaves) wca_cosine_bf16_kernel(
+    const uint16_t* a, int64_t a_s, const uint16_t* b, int64_t b_s, const int64_t* b_rows,
+    int64_t n, int H, int D, double eps, double* out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+  if (i >= n) return;
+  const int64_t bi = b_rows ? b_rows[i] : i;
+  const int L = D / 16, per = 64 / L;
+  const double tiny = 2.2250738585072014e-308;
+  double total = 0.0;
+  for (int h0 = 0; h0 < H; h0 += per) {
+    const int h = h0 + lane / L;
+    const int hc = h < H ? h : H - 1;  // lanes past the last head load it and are ignored
+    const int64_t off = static_cast<int64_t>(hc) * D + (lane % L) * 16;
+    const uint4* pa = reinterpret_cast<const uint4*>(a + i * a_s + off);
+    const uint4* pb = reinterpret_cast<const uint4*>(b + bi * b_s + off);
+    const uint4 va[2] = {pa[0], pa[1]}, vb[2] = {pb[0], pb[1]};
+    double x[16], y[16];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint32_t wa[4] = {va[q].x, va[q].y, va[q].z, va[q].w};
+      const uint32_t wb[4] = {vb[q].x, vb[q].y, vb[q].z, vb[q].w};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        x[8 * q + 2 * r] = bf16_to_float(static_cast<uint16_t>(wa[r]));
+        x[8 * q + 2 * r + 1] = bf16_to_float(static_cast<uint16_t>(wa[r] >> 16));
+        y[8 * q + 2 * r] = bf16_to_float(static_cast<uint16_t>(wb[r]));
+        y[8 * q + 2 * r + 1] = bf16_to_float(static_cast<uint16_t>(wb[r] >> 16));
+      }
+    }
+    double amax = 0.0, bmax = 0.0;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      amax = fmax(amax, fabs(x[e]));
+      bmax = fmax(bmax, fabs(y[e]));
+    }
+    for (int o = 1; o < L; o <<= 1) {
+      amax = fmax(amax, __shfl_xor(amax, o, 64));
+      bmax = fmax(bmax, __shfl_xor(bmax, o, 64));
+    }
+    const double as = amax > eps ? amax : eps;
+    const double bs = bmax > eps ? bmax : eps;
+    double na = 0.0, nb = 0.0;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const double xs = x[e] / as, ys = y[e] / bs;
+      na += xs * xs;
+      nb += ys * ys;
+    }
+    for (int o = 1; o < L; o <<= 1) {
+      na += __shfl_xor(na, o, 64);
+      nb += __shfl_xor(nb, o, 64);
+    }
+    na = sqrt(na);
+    nb = sqrt(nb);
+    const double da = na > tiny ? na : tiny;
+    const double db = nb > tiny ? nb : tiny;
+    double dot = 0.0;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) dot += (x[e] / as / da) * (y[e] / bs / db);
+    for (int o = 1; o < L; o <<= 1) dot += __shfl_xor(dot, o, 64);
+    dot = dot < -1.0 ? -1.0 : (dot > 1.0 ? 1.0 : dot);
+    for (int g = 0; g < per; ++g) {
+      const double v = __shfl(dot, g * L, 64);
+      if (h0 + g < H) total += v;
+    }
+  }
+  if (lane == 0) out[i] = total / static_cast<double>(H);
+}
+
 // WCAState.initialize masks (wca.py:161-171): candidate = reused & (err > 0);
 // counts[0] = #reused, counts[1] = #candidates; flag 32 when a token is neither
 // reused nor mandatory.  Single workgroup.
 __global__ void __launch_bounds__(kSelThreads) wca_init_masks_kernel(
     const double* err, const uint8_t* reused, const uint8_t* mandatory, int64_t n,
     uint8_t* candidate, int64_t* counts, int32_t* flags) {
-  __shared__ int scan_tmp[kSelThreads];
+  __shared__ int wave_tot[kSelWaves];
   int nr = 0, nc = 0, bad = 0;
-  for (int64_t t = threadIdx.x; t < n; t += kSelThreads) {
-    bool r = reused[t] != 0;
-    bool c = r && err[t] > 0.0;
-    candidate[t] = c ? 1 : 0;
-    nr += r;
-    nc += c;
-    if (!r && !mandatory[t]) bad = 1;
+  for (int64_t c0 = 0; c0 < n; c0 += kChunk) {
+    const int64_t s = c0 + static_cast<int64_t>(threadIdx.x) * kRun;
+    if (s >= n) continue;
+    const uint32_t r = run_mask(reused, s, n);
+    const uint32_t mand = run_mask(mandatory, s, n);
+    const uint32_t live = s + kRun <= n ? 0xffffu : (1u << (n - s)) - 1u;
+    uint64_t kb[kRun];
+    load_key_run(err, s, n, kb);  // err >= 0 or NaN: key_bits > 0 exactly when err > 0
+    uint32_t c = 0;
+#pragma unroll
+    for (int j = 0; j < kRun; ++j) {
+      const double e = __longlong_as_double(kb[j]);
+      if (((r >> j) & 1u) && e > 0.0) c |= 1u << j;
+    }
+    c &= live;
+    if (s + kRun <= n && (reinterpret_cast<uintptr_t>(candidate + s) & 15) == 0) {
+      uint32_t w[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        w[q] = ((c >> (4 * q)) & 1u) | (((c >> (4 * q + 1)) & 1u) << 8) |
+               (((c >> (4 * q + 2)) & 1u) << 16) | (((c >> (4 * q + 3)) & 1u) << 24);
+      *reinterpret_cast<uint4*>(candidate + s) = make_uint4(w[0], w[1], w[2], w[3]);
+    } else {
+      for (int j = 0; j < kRun && s + j < n; ++j) candidate[s + j] = (c >> j) & 1u;
+    }
+    nr += __popc(r);
+    nc += __popc(c);
+    if (~(r | mand) & live) bad = 1;
   }
   int ex;
-  int tr = block_exclusive_scan(nr, scan_tmp, ex);
-  int tc = block_exclusive_scan(nc, scan_tmp, ex);
-  int tb = block_exclusive_scan(bad, scan_tmp, ex);
+  const int tr = block_scan(nr, wave_tot, ex);
+  const int tc = block_scan(nc, wave_tot, ex);
+  const int tb = block_scan(bad, wave_tot, ex);
   if (threadIdx.x == 0) {
     counts[0] = tr;
     counts[1] = tc;
     if (tb) atomicOr(flags, 32);
   }
 }
-
 // used[i] = 1 if mandatory[rows[i]] else (previous ? alpha[rows[i]] : next[i])
 // (wca.py:257-265).
 __global__ void wca_used_alpha_kernel(const double* alpha, const double* next, const int64_t* rows,
@@ -423,38 +733,45 @@ __global__ void wca_used_alpha_kernel(const double* alpha, const double* next, c
 __global__ void __launch_bounds__(kSelThreads) wca_gate_kernel(
     const double* cosine, const int64_t* rows, const uint8_t* selected, int64_t a,
     int32_t distance, double threshold, int64_t* removed, int64_t* count) {
-  __shared__ int scan_tmp[kSelThreads];
+  __shared__ int wave_tot[kSelWaves];
   int64_t base = 0;
-  for (int64_t c0 = 0; c0 < a; c0 += kSelThreads) {
-    int64_t i = c0 + threadIdx.x;
-    int f = 0;
-    if (i < a) {
-      double metric = distance ? 1.0 - cosine[i] : cosine[i];
-      f = selected[rows[i]] && metric < threshold;
+  for (int64_t c0 = 0; c0 < a; c0 += kChunk) {
+    const int64_t s = c0 + static_cast<int64_t>(threadIdx.x) * kRun;
+    uint32_t f = 0;
+    for (int j = 0; j < kRun && s + j < a; ++j) {
+      const double metric = distance ? 1.0 - cosine[s + j] : cosine[s + j];
+      if (selected[rows[s + j]] && metric < threshold) f |= 1u << j;
     }
-    int ex;
-    int tot = block_exclusive_scan(f, scan_tmp, ex);
-    if (f) removed[base + ex] = rows[i];
+    int pos;
+    const int tot = block_scan(__popc(f), wave_tot, pos);
+    for (; f; f &= f - 1) {
+      const int64_t i = s + (__ffs(f) - 1);
+      removed[base + pos++] = rows[i];
+    }
     base += tot;
   }
   if (threadIdx.x == 0) *count = base;
 }
 
-// Commit (wca.py:289-293): alpha[rows[i]] = next[i]; removed tokens leave the
-// selection and the candidates and are marked removed.
+// Commit (wca.py:289-293): alpha[rows[i]] = next[i]; the nrem[0] removed
+// tokens (nrem may be null: none) leave the selection and the candidates and
+// are marked removed.  Nothing is written when abort_flags has a bit of
+// abort_mask set (the update failed a check), which keeps the state unchanged.
 __global__ void wca_commit_kernel(double* alpha, const double* next, const int64_t* rows, int64_t a,
-                                  const int64_t* removed, int64_t nrem, uint8_t* selected,
-                                  uint8_t* candidate, uint8_t* removed_mask) {
-  int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+                                  const int64_t* removed, const int64_t* nrem, uint8_t* selected,
+                                  uint8_t* candidate, uint8_t* removed_mask,
+                                  const int32_t* abort_flags, int32_t abort_mask) {
+  if (abort_flags && (*abort_flags & abort_mask)) return;
+  const int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
   if (i < a) alpha[rows[i]] = next[i];
-  if (i < nrem) {
-    int64_t t = removed[i];
+  const int64_t r = nrem ? *nrem : 0;
+  if (i < r) {
+    const int64_t t = removed[i];
     selected[t] = 0;
     candidate[t] = 0;
     removed_mask[t] = 1;
   }
 }
-
 int grid_for(int64_t total, int threads) {
   int64_t g = ceil_div(total, threads);
   if (g > 65535 * 16) g = 65535 * 16;
@@ -496,19 +813,28 @@ extern "C" int cs_wca_gate(const double* cosine, const int64_t* rows, const uint
 }
 
 extern "C" int cs_wca_commit(double* alpha, const double* next, const int64_t* rows, int64_t a,
-                             const int64_t* removed, int64_t nrem, uint8_t* selected,
-                             uint8_t* candidate, uint8_t* removed_mask, void* stream) {
-  int64_t n = a > nrem ? a : nrem;
-  if (n == 0) return CS_OK;
-  CS_REQUIRE(alpha && selected && candidate && removed_mask, "null arguments");
-  hipLaunchKernelGGL(cs::wca_commit_kernel, dim3(cs::ceil_div(n, 256)), dim3(256), 0,
+                             const int64_t* removed, const int64_t* nrem, uint8_t* selected,
+                             uint8_t* candidate, uint8_t* removed_mask, const int32_t* abort_flags,
+                             int32_t abort_mask, void* stream) {
+  if (a == 0) return CS_OK;  // removed tokens are a subset of the active rows
+  CS_REQUIRE(alpha && next && rows && selected && candidate && removed_mask, "null arguments");
+  CS_REQUIRE(!nrem || removed, "removed list missing");
+  hipLaunchKernelGGL(cs::wca_commit_kernel, dim3(cs::ceil_div(a, 256)), dim3(256), 0,
                      cs::as_stream(stream), alpha, next, rows, a, removed, nrem, selected,
-                     candidate, removed_mask);
+                     candidate, removed_mask, abort_flags, abort_mask);
   CS_LAUNCH_CHECK("wca_commit");
   return CS_OK;
 }
 
 using namespace cs;
+
+// True when v is a bf16 [n, H, D] view whose [H, D] rows are contiguous with
+// 16-byte aligned starts (row stride a multiple of 8 elements).
+static bool bf16_rows16(const cs_view* v) {
+  return v->dtype == CS_BF16 && v->stride[2] == 1 && v->stride[1] == v->shape[2] &&
+         (v->shape[1] * v->shape[2]) % 8 == 0 && v->stride[0] % 8 == 0 &&
+         (reinterpret_cast<uintptr_t>(v->data) & 15) == 0;
+}
 
 extern "C" int cs_wca_score(const cs_view* old_rows_src, const int64_t* old_rows,
                             const cs_view* fresh, double* err, double* norm, int32_t* flags,
@@ -520,9 +846,16 @@ extern "C" int cs_wca_score(const cs_view* old_rows_src, const int64_t* old_rows
              "old/new head shapes differ");
   int64_t n = fresh->shape[0];
   if (n == 0) return CS_OK;
-  hipLaunchKernelGGL(wca_score_kernel, dim3(ceil_div(n, kWaves)), dim3(64 * kWaves), 0,
-                     as_stream(stream), to_dview(old_rows_src), old_rows, to_dview(fresh), err,
-                     norm, flags);
+  if (bf16_rows16(old_rows_src) && bf16_rows16(fresh)) {
+    hipLaunchKernelGGL(wca_score_bf16_kernel, dim3(ceil_div(n, kWaves)), dim3(64 * kWaves), 0,
+                       as_stream(stream), static_cast<const uint16_t*>(old_rows_src->data),
+                       old_rows_src->stride[0], old_rows, static_cast<const uint16_t*>(fresh->data),
+                       fresh->stride[0], n, fresh->shape[1] * fresh->shape[2] / 8, err, norm, flags);
+  } else {
+    hipLaunchKernelGGL(wca_score_kernel, dim3(ceil_div(n, kWaves)), dim3(64 * kWaves), 0,
+                       as_stream(stream), to_dview(old_rows_src), old_rows, to_dview(fresh), err,
+                       norm, flags);
+  }
   CS_LAUNCH_CHECK("wca_score");
   return CS_OK;
 }
@@ -539,12 +872,18 @@ extern "C" int cs_wca_alpha(const double* err, const double* norm, int64_t n, do
 
 extern "C" int cs_wca_promote(const double* key, const uint8_t* candidate, const uint8_t* removed,
                               uint8_t* selected, int64_t n, int64_t budget, int64_t* scratch,
-                              int64_t* promoted, int64_t* count_out, void* stream) {
+                              int64_t* promoted, int64_t* count_out, const int32_t* abort_flags,
+                              int32_t abort_mask, void* stream) {
   CS_REQUIRE(key && candidate && removed && selected && scratch && promoted && count_out,
              "null arguments");
   CS_REQUIRE(n >= 0 && n <= (1ll << 24), "at most 2^24 tokens");
-  hipLaunchKernelGGL(wca_promote_kernel, dim3(1), dim3(kSelThreads), 0, as_stream(stream), key,
-                     candidate, removed, selected, n, budget, scratch, promoted, count_out);
+  hipStream_t s = as_stream(stream);
+  hipLaunchKernelGGL(wca_promote_kernel, dim3(1), dim3(kSelThreads), 0, s, key, candidate, removed,
+                     selected, n, budget, scratch, count_out, abort_flags, abort_mask);
+  const int64_t kmax = budget < n ? (budget > 0 ? budget : 0) : n;  // bound on the device count
+  if (kmax > 0)
+    hipLaunchKernelGGL(wca_promote_order_kernel, dim3(ceil_div(kmax, 64)), dim3(64 * kOrderSlices),
+                       0, s, scratch, n, count_out, promoted);
   CS_LAUNCH_CHECK("wca_promote");
   return CS_OK;
 }
@@ -569,6 +908,26 @@ extern "C" int cs_wca_blend(const cs_view* old_k, const cs_view* old_v, const in
              "3-d views required");
   int64_t total = new_k->shape[0] * new_k->shape[1] * new_k->shape[2];
   if (total == 0) return CS_OK;
+  const bool same_rows = old_k->shape[1] == new_k->shape[1] && old_k->shape[2] == new_k->shape[2] &&
+                         old_v->shape[1] == new_k->shape[1] && old_v->shape[2] == new_k->shape[2] &&
+                         new_v->shape[1] == new_k->shape[1] && new_v->shape[2] == new_k->shape[2] &&
+                         fused_k->shape[1] == new_k->shape[1] && fused_k->shape[2] == new_k->shape[2] &&
+                         fused_v->shape[1] == new_k->shape[1] && fused_v->shape[2] == new_k->shape[2];
+  if (same_rows && bf16_rows16(old_k) && bf16_rows16(old_v) && bf16_rows16(new_k) &&
+      bf16_rows16(new_v) && bf16_rows16(fused_k) && bf16_rows16(fused_v)) {
+    const int64_t words = new_k->shape[1] * new_k->shape[2] / 8;
+    const int64_t a = new_k->shape[0];
+    hipLaunchKernelGGL(wca_blend_bf16_kernel, dim3(grid_for(a * words, 256)), dim3(256), 0,
+                       as_stream(stream), static_cast<const uint16_t*>(old_k->data),
+                       old_k->stride[0], static_cast<const uint16_t*>(old_v->data),
+                       old_v->stride[0], rows, static_cast<const uint16_t*>(new_k->data),
+                       new_k->stride[0], static_cast<const uint16_t*>(new_v->data),
+                       new_v->stride[0], weight, mandatory, static_cast<uint16_t*>(fused_k->data),
+                       fused_k->stride[0], static_cast<uint16_t*>(fused_v->data), fused_v->stride[0],
+                       a, words, flags);
+    CS_LAUNCH_CHECK("wca_blend");
+    return CS_OK;
+  }
   hipLaunchKernelGGL(wca_blend_kernel, dim3(grid_for(total, 256)), dim3(256), 0,
                      as_stream(stream), to_dview(old_k), to_dview(old_v), rows, to_dview(new_k),
                      to_dview(new_v), weight, mandatory, to_dview(fused_k), to_dview(fused_v),
@@ -582,8 +941,18 @@ extern "C" int cs_wca_head_cosine(const cs_view* a, const cs_view* b, const int6
   CS_REQUIRE(a && b && out && a->ndim == 3 && b->ndim == 3, "3-d views required");
   int64_t n = a->shape[0];
   if (n == 0) return CS_OK;
-  hipLaunchKernelGGL(wca_cosine_kernel, dim3(ceil_div(n, kWaves)), dim3(64 * kWaves), 0,
-                     as_stream(stream), to_dview(a), to_dview(b), b_rows, eps, out);
+  const int64_t H = a->shape[1], D = a->shape[2];
+  const int64_t L = D / 16;
+  if (bf16_rows16(a) && bf16_rows16(b) && b->shape[1] == H && b->shape[2] == D && D % 16 == 0 &&
+      L >= 1 && L <= 64 && (L & (L - 1)) == 0 && H <= (1 << 20)) {
+    hipLaunchKernelGGL(wca_cosine_bf16_kernel, dim3(ceil_div(n, kWaves)), dim3(64 * kWaves), 0,
+                       as_stream(stream), static_cast<const uint16_t*>(a->data), a->stride[0],
+                       static_cast<const uint16_t*>(b->data), b->stride[0], b_rows, n,
+                       static_cast<int>(H), static_cast<int>(D), eps, out);
+  } else {
+    hipLaunchKernelGGL(wca_cosine_kernel, dim3(ceil_div(n, kWaves)), dim3(64 * kWaves), 0,
+                       as_stream(stream), to_dview(a), to_dview(b), b_rows, eps, out);
+  }
   CS_LAUNCH_CHECK("wca_head_cosine");
   return CS_OK;
 }

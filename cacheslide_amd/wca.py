@@ -9,8 +9,9 @@ exactly where the reference's separate tensor operations round.
 
 from __future__ import annotations
 
+import ctypes
 import math
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 
 import torch
 from torch import Tensor
@@ -28,24 +29,48 @@ class WCANumericalError(ValueError):
 
 
 class _Flags:
-    def __init__(self, device):
+    """Device status block: int32 check flags in word 0, then int64 counters.
+
+    Kernels OR check bits into the flags and write counts into the counters;
+    ``finish`` reads the whole block back with one synchronising copy and
+    raises the first registered check that fired (registration order is the
+    reference's order of checks).
+    """
+
+    def __init__(self, device, counters: int = 0):
         self.device = device
-        self.tensor = _hip.new_flags(device)
+        # torch.zeros launches a fill kernel (no memset node under graph capture)
+        self.block = torch.zeros(1 + counters, dtype=torch.int64, device=device)
         self.steps: list[tuple[int, type, str]] = []
+        self.counts: list[int] = []
 
     @property
     def ptr(self):
-        return ptr(self.tensor)
+        return ctypes.c_void_p(self.block.data_ptr())
+
+    def counter(self, i: int):
+        return ctypes.c_void_p(self.block.data_ptr() + 8 * (1 + i))
 
     @property
     def stream(self):
         return _hip.stream_of(self.device)
 
+    @property
+    def abort_mask(self) -> int:
+        """Every registered check bit: device commits skip when one is set."""
+        mask = 0
+        for bits, _, _ in self.steps:
+            mask |= bits
+        return mask
+
     def step(self, bits: int, exc: type, message: str) -> None:
         self.steps.append((bits, exc, message))
 
-    def finish(self, pending: BaseException | None = None) -> None:
-        value = _hip.read_flags(self.tensor)[0] if self.steps else 0
+    def finish(self, pending: BaseException | None = None, *, read: bool = False) -> None:
+        value = 0
+        if self.steps or read:
+            words = [int(x) for x in self.block.cpu().tolist()]
+            value, self.counts = words[0] & 0xFFFFFFFF, words[1:]
         for bits, exc, message in self.steps:
             if value & bits:
                 raise exc(message)
@@ -169,13 +194,20 @@ class WCAUpdate:
     next_indices: Tensor
 
 
-def _nonzero(a: Tensor, b: Tensor | None) -> Tensor:
-    """Ascending indices of a | b on the device (one readback for the count)."""
+def _nonzero_launch(a: Tensor, b: Tensor | None, count) -> Tensor:
+    """Ascending indices of a | b into a device buffer; the count goes to ``count``."""
     n = a.numel()
     out = torch.empty(max(n, 1), dtype=torch.long, device=a.device)
-    count = torch.zeros(1, dtype=torch.long, device=a.device)
-    call("cs_mask_nonzero", ptr(a), ptr(b), n, ptr(out), ptr(count), _hip.stream_of(a.device))
-    return out[: int(count.item())]
+    call("cs_mask_nonzero", ptr(a), ptr(b), n, ptr(out), count, _hip.stream_of(a.device))
+    return out
+
+
+def _nonzero(a: Tensor, b: Tensor | None) -> Tensor:
+    """Ascending indices of a | b on the device (one readback for the count)."""
+    fl = _Flags(a.device, 1)
+    out = _nonzero_launch(a, b, fl.counter(0))
+    fl.finish(read=True)
+    return out[: fl.counts[0]]
 
 
 @dataclass
@@ -192,6 +224,12 @@ class WCAState:
     alpha: Tensor
     budget: int
     last_layer: int = 1
+    # active_indices of the current masks, kept with the tensor versions it
+    # was computed from: kernels here update the masks in place, and refresh
+    # it themselves; any other in-place change to a mask (or to the cached
+    # index tensor) bumps a version and forces a recount.
+    _active: Tensor | None = field(default=None, repr=False, compare=False)
+    _active_key: tuple = field(default=(), repr=False, compare=False)
 
     @classmethod
     def initialize(
@@ -204,7 +242,7 @@ class WCAState:
     ) -> "WCAState":
         config = config or WCAConfig()
         device = _hip.require_device(cached_k)
-        fl = _Flags(device)
+        fl = _Flags(device, 2)
         _kv("cached_k", cached_k, fl)
         _matching("recomputed_k", recomputed_k, cached_k.shape, cached_k, fl)
         err, norm = _score(cached_k, recomputed_k, None, fl)
@@ -216,13 +254,12 @@ class WCAState:
         except ValueError as error:
             fl.finish(error)
         candidate = torch.empty(n, dtype=torch.bool, device=device)
-        counts = torch.zeros(2, dtype=torch.long, device=device)
         call("cs_wca_init_masks", ptr(err), ptr(reused_mask), ptr(mandatory_mask), n,
-             ptr(candidate), ptr(counts), fl.ptr, fl.stream)
+             ptr(candidate), fl.counter(0), fl.ptr, fl.stream)
         fl.step(32, ValueError, "every dynamic/non-reused token must be mandatory")
         alpha = _alpha(err, norm, config.epsilon, config.clamp_alpha, fl)
-        fl.finish()
-        n_reused, n_candidates = (int(x) for x in counts.cpu().tolist())
+        fl.finish(read=True)
+        n_reused, n_candidates = fl.counts
         budget = min(math.ceil(config.correction_fraction * n_reused), n_candidates)
         state = cls(
             config=config,
@@ -238,26 +275,51 @@ class WCAState:
         state._promote()
         return state
 
+    def _mask_key(self) -> tuple:
+        sel, mand = self.selected_mask, self.mandatory_mask
+        return (id(sel), sel._version, id(mand), mand._version)
+
+    def _cache_active(self, buffer: Tensor, count: int) -> Tensor:
+        self._active = buffer[:count]
+        self._active_key = self._mask_key() + (self._active._version,)
+        return self._active
+
     @property
     def active_indices(self) -> Tensor:
         """Sorted global token indices to compute at the next layer."""
-        return _nonzero(self.selected_mask, self.mandatory_mask)
+        active = self._active
+        if active is not None and self._active_key == self._mask_key() + (active._version,):
+            return active
+        fl = _Flags(self.selected_mask.device, 1)
+        buffer = _nonzero_launch(self.selected_mask, self.mandatory_mask, fl.counter(0))
+        fl.finish(read=True)
+        return self._cache_active(buffer, fl.counts[0])
 
     @property
     def selected_indices(self) -> Tensor:
         return _nonzero(self.selected_mask, None)
 
-    def _promote(self) -> Tensor:
-        """Fill the budget with the largest initial deviations, ties to lower index."""
+    def _promote_launch(self, fl: _Flags, counter: int, abort_mask: int = 0) -> Tensor:
+        """Launch the promotion; its count goes to counter ``counter`` of ``fl``.
+        With ``abort_mask`` it promotes nothing when fl's flags hold one of those bits."""
         n = self.selected_mask.numel()
         device = self.selected_mask.device
-        scratch = torch.empty(max(n, 1), dtype=torch.long, device=device)
+        scratch = torch.empty(max(2 * n, 1), dtype=torch.long, device=device)
         promoted = torch.empty(max(n, 1), dtype=torch.long, device=device)
-        count = torch.zeros(1, dtype=torch.long, device=device)
         call("cs_wca_promote", ptr(self.initial_deviation), ptr(self.candidate_mask),
              ptr(self.removed_mask), ptr(self.selected_mask), n, self.budget, ptr(scratch),
-             ptr(promoted), ptr(count), _hip.stream_of(device))
-        return promoted[: int(count.item())]
+             ptr(promoted), fl.counter(counter), fl.ptr if abort_mask else ctypes.c_void_p(None),
+             abort_mask, _hip.stream_of(device))
+        return promoted
+
+    def _promote(self) -> Tensor:
+        """Fill the budget with the largest initial deviations, ties to lower index."""
+        fl = _Flags(self.selected_mask.device, 2)
+        promoted = self._promote_launch(fl, 0)
+        active = _nonzero_launch(self.selected_mask, self.mandatory_mask, fl.counter(1))
+        fl.finish(read=True)
+        self._cache_active(active, fl.counts[1])
+        return promoted[: fl.counts[0]]
 
     def update(
         self,
@@ -272,7 +334,8 @@ class WCAState:
         if layer_index != self.last_layer + 1:
             raise ValueError("layers must update consecutively after full layer one")
         device = _hip.require_device(cached_k)
-        fl = _Flags(device)
+        # counters: removed, promoted, next active
+        fl = _Flags(device, 3)
         _kv("cached_k", cached_k, fl)
         _matching("cached_v", cached_v, cached_k.shape, cached_k, fl)
         if cached_k.shape[0] != self.reused_mask.numel():
@@ -304,24 +367,30 @@ class WCAState:
              fl.stream)
         fl.step(8, WCANumericalError, "weighted K/V overflowed the cache dtype")
 
-        removed = indices[:0]
-        if layer_index % self.config.gate_interval == 0 and a:
+        gate = layer_index % self.config.gate_interval == 0 and a > 0
+        removed_buf = None
+        if gate:
             cosine = torch.empty(a, dtype=torch.float64, device=device)
             call("cs_wca_head_cosine", vref(recomputed_k), vref(cached_k), ptr(indices),
                  float(self.config.epsilon), ptr(cosine), fl.stream)
             removed_buf = torch.empty(a, dtype=torch.long, device=device)
-            count = torch.zeros(1, dtype=torch.long, device=device)
             call("cs_wca_gate", ptr(cosine), ptr(indices), ptr(self.selected_mask), a,
                  1 if self.config.convergence_mode == "distance_lt" else 0,
-                 float(self.config.convergence_threshold), ptr(removed_buf), ptr(count), fl.stream)
-            fl.finish()  # nothing is committed before the numeric checks pass
-            removed = removed_buf[: int(count.item())]
-        else:
-            fl.finish()
-        call("cs_wca_commit", ptr(self.alpha), ptr(next_alpha), ptr(indices), a, ptr(removed),
-             removed.numel(), ptr(self.selected_mask), ptr(self.candidate_mask),
-             ptr(self.removed_mask), fl.stream)
-        promoted = self._promote()
+                 float(self.config.convergence_threshold), ptr(removed_buf), fl.counter(0),
+                 fl.stream)
+        # Commit and promotion run on the device only when no check fired
+        # (wca.py:289-295 commits after its checks); one readback follows.
+        abort = fl.abort_mask
+        call("cs_wca_commit", ptr(self.alpha), ptr(next_alpha), ptr(indices), a, ptr(removed_buf),
+             fl.counter(0) if gate else ctypes.c_void_p(None), ptr(self.selected_mask),
+             ptr(self.candidate_mask), ptr(self.removed_mask), fl.ptr, abort, fl.stream)
+        promoted_buf = self._promote_launch(fl, 1, abort)
+        active_buf = _nonzero_launch(self.selected_mask, self.mandatory_mask, fl.counter(2))
+        fl.finish(read=True)
+        n_removed, n_promoted, n_active = fl.counts
+        removed = removed_buf[:n_removed] if gate else indices[:0]
+        promoted = promoted_buf[:n_promoted]
+        next_indices = self._cache_active(active_buf, n_active)
         self.last_layer = layer_index
         return WCAUpdate(
             indices=indices,
@@ -330,5 +399,5 @@ class WCAState:
             alpha=used,
             removed_indices=removed,
             promoted_indices=promoted,
-            next_indices=self.active_indices,
+            next_indices=next_indices,
         )

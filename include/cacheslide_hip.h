@@ -285,11 +285,15 @@ int cs_wca_alpha(const double* err, const double* norm, int64_t n, double eps, i
  * ~removed; slots = max(0, budget - #selected).  Takes the min(slots,
  * #available) available tokens with the largest key[t] (ties: lower index
  * first), sets selected[t] = 1 and writes them in that order to promoted[0..k).
- * scratch and promoted hold n int64 each; *count_out (device) receives k.
- * n <= 1<<24.  Single workgroup. */
+ * scratch holds 2n int64 and promoted n; *count_out (device) receives k.
+ * When abort_flags (device, may be NULL) has a bit of abort_mask set, nothing
+ * changes and k = 0: an update that failed its checks promotes nothing.
+ * n <= 1<<24.  Two launches: a one-workgroup select/mark/compact pass and an
+ * ordering pass over min(budget, n) / 256 workgroups. */
 int cs_wca_promote(const double* key, const uint8_t* candidate, const uint8_t* removed,
                    uint8_t* selected, int64_t n, int64_t budget, int64_t* scratch,
-                   int64_t* promoted, int64_t* count_out, void* stream);
+                   int64_t* promoted, int64_t* count_out, const int32_t* abort_flags,
+                   int32_t abort_mask, void* stream);
 
 /* Ascending indices t with a[t] | b[t] (b may be NULL) -> out[0..*count)
  * (WCAState.active_indices / selected_indices, wca.py:193-200). */
@@ -329,11 +333,15 @@ int cs_wca_gate(const double* cosine, const int64_t* rows, const uint8_t* select
                 int32_t distance_mode, double threshold, int64_t* removed, int64_t* count,
                 void* stream);
 
-/* Commit (wca.py:289-293): alpha[rows[i]] = next[i]; removed tokens are cleared
- * from selected and candidate and set in removed_mask. */
+/* Commit (wca.py:289-293): alpha[rows[i]] = next[i]; the *nrem (device int64,
+ * NULL = none) tokens of removed[] -- a subset of rows -- are cleared from
+ * selected and candidate and set in removed_mask.  When abort_flags (device,
+ * may be NULL) has a bit of abort_mask set nothing is written, so the
+ * transactional commit of wca.py:289-295 needs no host round trip. */
 int cs_wca_commit(double* alpha, const double* next, const int64_t* rows, int64_t a,
-                  const int64_t* removed, int64_t nrem, uint8_t* selected, uint8_t* candidate,
-                  uint8_t* removed_mask, void* stream);
+                  const int64_t* removed, const int64_t* nrem, uint8_t* selected,
+                  uint8_t* candidate, uint8_t* removed_mask, const int32_t* abort_flags,
+                  int32_t abort_mask, void* stream);
 
 #ifdef __cplusplus
 }

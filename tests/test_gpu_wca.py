@@ -240,3 +240,57 @@ def test_promotion_ties_and_large_budget(device):
     promoted_dev = dst._promote().tolist()
     promoted_orc = fresh_order().tolist()
     assert promoted_dev == promoted_orc
+
+
+def test_bf16_head_cosine_matches_oracle(device):
+    """bf16 rows take the vectorised cosine kernel: same values as the fp64
+    oracle up to summation order, including zero heads and the clamp."""
+    a = seeded((300, 8, 128), 700, dtype=torch.bfloat16)
+    b = (a.double() + seeded((300, 8, 128), 701, scale=0.5).double()).to(torch.bfloat16)
+    a[3] = 0  # all-zero rows: eps scaling, cosine 0
+    b[4] = a[4]  # identical rows: cosine clamps at 1
+    got = mean_head_cosine(a.to(device), b.to(device)).cpu().numpy()
+    want = orc.mean_head_cosine(a.double().numpy(), b.double().numpy())
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-14)
+    assert got[3] == 0.0 and abs(got[4] - 1.0) < 1e-14
+
+
+def test_promotion_multi_chunk_beyond_lds_rank(device):
+    """40000 tokens (three selection chunks) and a budget of 10400 (ranked
+    from global memory): same selection and promotion order as the oracle."""
+    T = 40000
+    rng = np.random.default_rng(13)
+    levels = rng.integers(0, 300, T).astype(np.float64)  # ties across chunks
+    fresh = torch.from_numpy(np.sqrt(levels)[:, None, None]).float()
+    cached = torch.zeros((T, 1, 1))
+    reused = torch.ones(T, dtype=torch.bool)
+    reused[T - 5:] = False
+    mandatory = ~reused
+    ost = orc.State(cached.double().numpy(), fresh.double().numpy(), reused.numpy(), mandatory.numpy(),
+                    fraction=0.26)
+    dst = WCAState.initialize(cached.to(device), fresh.to(device), reused.to(device), mandatory.to(device),
+                              WCAConfig(correction_fraction=0.26))
+    assert dst.budget == ost.budget > 4096
+    assert dst.selected_indices.tolist() == np.flatnonzero(ost.selected).tolist()
+    assert dst.active_indices.tolist() == ost.active.tolist()
+    dst.selected_mask.zero_()  # in-place change: the cached active indices must be recounted
+    ost.selected[:] = False
+    assert dst.active_indices.tolist() == ost.active.tolist()
+    assert dst._promote().tolist() == ost.promote().tolist()
+    assert dst.active_indices.tolist() == ost.active.tolist()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32, torch.float64])
+def test_finite_check_vector_path(device, dtype):
+    """Contiguous tensors are checked 16 bytes at a time: one inf or NaN anywhere
+    (first, last, middle element) is found; finite extremes are not flagged."""
+    x = seeded((513, 8, 128), 702, dtype=dtype).to(device)
+    x[7, 3, 5] = torch.finfo(dtype).max
+    x[8, 0, 0] = -torch.finfo(dtype).max
+    squared_deviation(x, x.clone())  # finite extremes pass the check
+    for where, bad in (((0, 0, 0), float("inf")), ((512, 7, 127), float("nan")),
+                       ((300, 4, 64), float("-inf"))):
+        y = x.clone()
+        y[where] = bad
+        with pytest.raises(WCANumericalError, match="cached_k must have finite values"):
+            squared_deviation(y, x)
