@@ -70,3 +70,30 @@ def fill_paged(cache: torch.Tensor, rows: list[list[int]], keys: list[torch.Tens
             blk, off = row[t // bs], t % bs
             cache[blk, :, off, :d] = k[t]
             cache[blk, :, off, d:] = v[t]
+
+
+class HostMover:
+    """Host stand-in for the slot kernels, for tests of the paged-arena rules
+    without a GPU: native slot s is cache[s // bs, :, s % bs] (K in the first
+    half of the record, V in the second), slot native + i is sidecar row i."""
+
+    def scatter(self, cache, side_k, side_v, slots, key, value, rows=None):
+        bs, native, d = cache.shape[2], cache.shape[0] * cache.shape[2], cache.shape[3] // 2
+        for i, slot in enumerate(slots):
+            r = i if rows is None else rows[i]
+            if slot < native:
+                cache[slot // bs, :, slot % bs, :d] = key[r]
+                cache[slot // bs, :, slot % bs, d:] = value[r]
+            else:
+                side_k[slot - native] = key[r]
+                side_v[slot - native] = value[r]
+
+    def gather(self, cache, side_k, side_v, slots, key, value):
+        bs, native, d = cache.shape[2], cache.shape[0] * cache.shape[2], cache.shape[3] // 2
+        for i, slot in enumerate(slots):
+            if slot < native:
+                key[i] = cache[slot // bs, :, slot % bs, :d]
+                value[i] = cache[slot // bs, :, slot % bs, d:]
+            else:
+                key[i] = side_k[slot - native]
+                value[i] = side_v[slot - native]
