@@ -8,7 +8,6 @@ batched relocation (relocate).
 """
 
 from .attention import CanonicalPositionPolicy, SelectedAssociationPolicy
-from .config import CacheSlideSettings
 from .contracts import RequestPlan
 from .paged import NativePagedKV
 from .policy import WCAConfig
@@ -36,7 +35,7 @@ __version__ = "0.1.0"
 
 __all__ = [
     "CCPEPositionError", "CCPEProfile", "CacheCapacityError", "CacheIntegrityError",
-    "CacheSlideSettings", "CanonicalPositionPolicy", "ChunkIdentity", "CoPE",
+    "CanonicalPositionPolicy", "ChunkIdentity", "CoPE",
     "CoPEPositionTrace", "LayerSlotMap", "NativePagedKV", "RequestPlan",
     "SelectedAssociationPolicy", "SlotWrite", "StaleCompletionError", "WCAConfig",
     "WCANumericalError", "WCAState", "WCAUpdate", "adaptation_weight", "coalesce_slot_writes",

@@ -1,4 +1,8 @@
-"""WCA policy parameters (src/cacheslide_vllm/policy.py:21-45), pure Python."""
+"""WCA parameters (src/cacheslide_vllm/policy.py:21-45), pure Python.
+
+Same fields, defaults, accepted values and ValueError messages as the
+reference's WCAConfig; the checks are table-driven here.
+"""
 
 from __future__ import annotations
 
@@ -8,15 +12,26 @@ from typing import Literal
 
 
 def _finite_number(name: str, value: object) -> None:
-    """Accept int/float (not bool, not str, not complex) with a finite value."""
+    """Accept an int or float (bool, str and complex are not) with a finite value."""
     if type(value) not in (int, float):
         raise ValueError(f"{name} must be a finite real number, not a boolean")
     try:
-        ok = math.isfinite(value)
-    except OverflowError:  # ints too large for a float
-        ok = False
-    if not ok:
+        finite = math.isfinite(value)
+    except OverflowError:  # an int beyond the float range
+        finite = False
+    if not finite:
         raise ValueError(f"{name} must be a finite real number")
+
+
+# name -> (test, message) for each scalar field after the finiteness checks
+_RULES = (
+    ("correction_fraction", lambda x: 0 <= x <= 1, "correction_fraction must be in [0, 1]"),
+    ("epsilon", lambda x: x > 0, "epsilon must be finite and positive"),
+    ("gate_interval", lambda x: type(x) is int and x >= 1, "gate_interval must be a positive integer"),
+    ("clamp_alpha", lambda x: type(x) is bool, "clamp_alpha must be a boolean"),
+    ("convergence_mode", lambda x: x in ("paper_cosine_lt", "distance_lt"), "unknown convergence_mode"),
+    ("weight_update", lambda x: x in ("previous_layer", "same_layer"), "unknown weight_update"),
+)
 
 
 @dataclass(frozen=True)
@@ -30,17 +45,8 @@ class WCAConfig:
     clamp_alpha: bool = False
 
     def __post_init__(self) -> None:
-        for field in ("correction_fraction", "epsilon", "convergence_threshold"):
-            _finite_number(field, getattr(self, field))
-        if not 0 <= self.correction_fraction <= 1:
-            raise ValueError("correction_fraction must be in [0, 1]")
-        if self.epsilon <= 0:
-            raise ValueError("epsilon must be finite and positive")
-        if type(self.gate_interval) is not int or self.gate_interval < 1:
-            raise ValueError("gate_interval must be a positive integer")
-        if type(self.clamp_alpha) is not bool:
-            raise ValueError("clamp_alpha must be a boolean")
-        if self.convergence_mode not in ("paper_cosine_lt", "distance_lt"):
-            raise ValueError("unknown convergence_mode")
-        if self.weight_update not in ("previous_layer", "same_layer"):
-            raise ValueError("unknown weight_update")
+        for name in ("correction_fraction", "epsilon", "convergence_threshold"):
+            _finite_number(name, getattr(self, name))
+        for name, test, message in _RULES:
+            if not test(getattr(self, name)):
+                raise ValueError(message)

@@ -14,6 +14,7 @@ from __future__ import annotations
 
 import math
 import re
+from collections import Counter
 from collections.abc import Callable, Sequence
 from dataclasses import dataclass
 
@@ -788,80 +789,25 @@ class CCPEProfile:
         histogram_bin_width: float = 0.25,
         max_elements: int = 1_000_000,
     ) -> "CCPEProfile":
-        """Most frequent joint quantised pattern, returning its first real sample.
+        """The modal calibration sample (position.py:594-699).
 
-        Each trace's positions are re-derived on the device from its masked
-        logits (contextual_positions) and must agree within 1e-6.  Ties between
-        patterns are broken lexicographically (position.py:594-699).
+        Every trace's positions are recomputed on the device from its masked
+        logits and must agree within 1e-6; the samples are quantised to
+        ``histogram_bin_width`` as whole joint patterns, and the first sample of
+        the most frequent pattern (ties: the lexicographically smallest pattern)
+        becomes the canonical table.  No pattern is assembled from per-cell modes.
         """
-        if not traces or not trained_profile_version.strip():
-            raise ValueError("calibration needs traces and a trained profile version")
-        if not math.isfinite(histogram_bin_width) or histogram_bin_width <= 0:
-            raise ValueError("histogram_bin_width must be finite and positive")
-        if not isinstance(traces[0], CoPEPositionTrace):
-            raise ValueError("calibration requires genuine CoPEPositionTrace inputs")
-        first = traces[0]
-        if not chunks or sum(c.length for c in chunks) != first.key_positions.numel():
-            raise ValueError("ordered chunk lengths must exactly match trace keys")
-        budget = sum(
-            t.positions.numel() + t.masked_logits.numel()
-            for t in traces
-            if isinstance(t, CoPEPositionTrace)
-        )
-        if budget > max_elements:
-            raise ValueError("CCPE calibration exceeds max_elements")
-        if first.positions.ndim != 3 or first.max_positions < 2:
-            raise ValueError("invalid contextual trace dimensions")
-        if not first.checkpoint_id.strip():
-            raise ValueError("trace must identify a trained CoPE checkpoint")
-        samples = []
+        first = _calibration_layout(traces, chunks, trained_profile_version, histogram_bin_width,
+                                    max_elements)
         device = torch.device("cuda", torch.cuda.current_device())
-        for trace in traces:
-            if not isinstance(trace, CoPEPositionTrace):
-                raise ValueError("calibration requires genuine CoPEPositionTrace inputs")
-            if (
-                trace.positions.shape != first.positions.shape
-                or trace.max_positions != first.max_positions
-                or trace.checkpoint_id != first.checkpoint_id
-                or not torch.equal(trace.query_positions, first.query_positions)
-                or not torch.equal(trace.key_positions, first.key_positions)
-            ):
-                raise ValueError("calibration trace layout/checkpoint mismatch")
-            allowed = trace.allowed_mask
-            if (
-                trace.masked_logits.ndim != 3
-                or trace.masked_logits.shape[0] != trace.positions.shape[0]
-                or allowed.shape != trace.masked_logits.shape
-                or allowed.dtype != torch.bool
-            ):
-                raise ValueError("invalid masked contextual trace")
-            expected = _trace_positions(trace, device)
-            if expected is None:
-                raise ValueError("invalid masked contextual trace")
-            if trace.source_query_indices is not None:
-                expected = expected[:, trace.source_query_indices.tolist()]
-            if trace.source_key_indices is not None:
-                expected = expected[:, :, trace.source_key_indices.tolist()]
-            if expected.shape != trace.positions.shape:
-                raise ValueError("projected trace source mapping has an invalid shape")
-            if not _close(trace.positions, expected, device):
-                raise ValueError("trace positions were not produced by CoPE gates")
-            samples.append(trace.positions.detach().cpu())
-        # joint histogram of quantised patterns; first sample represents a pattern
-        histogram: dict[tuple[int, ...], list[int]] = {}
-        for index, sample in enumerate(samples):
-            pattern = tuple(_quantise(v, histogram_bin_width) for v in sample.flatten().tolist())
-            entry = histogram.setdefault(pattern, [0, index])
-            entry[0] += 1
-        winner = min(histogram, key=lambda pattern: (-histogram[pattern][0], pattern))
-        canonical = samples[histogram[winner][1]].clone()
+        samples = [_verified_positions(trace, first, device) for trace in traces]
         return cls(
             trained_profile_version=trained_profile_version,
             checkpoint_id=first.checkpoint_id,
             chunks=tuple(chunks),
             query_positions=first.query_positions.detach().cpu().clone(),
             key_positions=first.key_positions.detach().cpu().clone(),
-            canonical_positions=canonical,
+            canonical_positions=_modal_sample(samples, histogram_bin_width).clone(),
             max_positions=first.max_positions,
             histogram_bin_width=histogram_bin_width,
             sample_count=len(traces),
@@ -921,6 +867,75 @@ class CCPEProfile:
             device=device or query_positions.device,
             dtype=dtype or self.canonical_positions.dtype,
         )
+
+
+def _calibration_layout(traces, chunks, version, bin_width, max_elements) -> CoPEPositionTrace:
+    """Checks on the calibration set as a whole, in the reference's order; returns
+    the first trace, whose layout every other trace must share."""
+    if not traces or not version.strip():
+        raise ValueError("calibration needs traces and a trained profile version")
+    if not math.isfinite(bin_width) or bin_width <= 0:
+        raise ValueError("histogram_bin_width must be finite and positive")
+    first = traces[0]
+    if not isinstance(first, CoPEPositionTrace):
+        raise ValueError("calibration requires genuine CoPEPositionTrace inputs")
+    if not chunks or sum(c.length for c in chunks) != first.key_positions.numel():
+        raise ValueError("ordered chunk lengths must exactly match trace keys")
+    elements = sum(t.positions.numel() + t.masked_logits.numel()
+                   for t in traces if isinstance(t, CoPEPositionTrace))
+    if elements > max_elements:
+        raise ValueError("CCPE calibration exceeds max_elements")
+    if first.positions.ndim != 3 or first.max_positions < 2:
+        raise ValueError("invalid contextual trace dimensions")
+    if not first.checkpoint_id.strip():
+        raise ValueError("trace must identify a trained CoPE checkpoint")
+    return first
+
+
+def _verified_positions(trace, first: CoPEPositionTrace, device: torch.device) -> Tensor:
+    """A trace's positions (host copy) once its layout matches ``first`` and the
+    positions are what the CoPE gates give for its masked logits."""
+    if not isinstance(trace, CoPEPositionTrace):
+        raise ValueError("calibration requires genuine CoPEPositionTrace inputs")
+    same_layout = (
+        trace.positions.shape == first.positions.shape
+        and trace.max_positions == first.max_positions
+        and trace.checkpoint_id == first.checkpoint_id
+        and torch.equal(trace.query_positions, first.query_positions)
+        and torch.equal(trace.key_positions, first.key_positions)
+    )
+    if not same_layout:
+        raise ValueError("calibration trace layout/checkpoint mismatch")
+    logits, allowed = trace.masked_logits, trace.allowed_mask
+    if (logits.ndim != 3 or logits.shape[0] != trace.positions.shape[0]
+            or allowed.shape != logits.shape or allowed.dtype != torch.bool):
+        raise ValueError("invalid masked contextual trace")
+    expected = _trace_positions(trace, device)
+    if expected is None:
+        raise ValueError("invalid masked contextual trace")
+    if trace.source_query_indices is not None:
+        expected = expected[:, trace.source_query_indices.tolist()]
+    if trace.source_key_indices is not None:
+        expected = expected[:, :, trace.source_key_indices.tolist()]
+    if expected.shape != trace.positions.shape:
+        raise ValueError("projected trace source mapping has an invalid shape")
+    if not _close(trace.positions, expected, device):
+        raise ValueError("trace positions were not produced by CoPE gates")
+    return trace.positions.detach().cpu()
+
+
+def _modal_sample(samples: list[Tensor], bin_width: float) -> Tensor:
+    """First sample of the most frequent quantised joint pattern; among equally
+    frequent patterns the lexicographically smallest wins."""
+    counts: Counter[tuple[int, ...]] = Counter()
+    first_seen: dict[tuple[int, ...], int] = {}
+    for index, sample in enumerate(samples):
+        pattern = tuple(_quantise(v, bin_width) for v in sample.flatten().tolist())
+        counts[pattern] += 1
+        first_seen.setdefault(pattern, index)
+    top = max(counts.values())
+    winner = min(pattern for pattern, n in counts.items() if n == top)
+    return samples[first_seen[winner]]
 
 
 def _quantise(value: float, width: float) -> int:
