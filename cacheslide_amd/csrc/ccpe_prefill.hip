@@ -117,15 +117,21 @@ struct prefill_params {
 
 __device__ inline bf16x8 as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
 
-// Direct global -> LDS load of 16 bytes per lane: lane i's bytes land at
-// lds_base + 16 i (lds_base wave-uniform).  Issued through inline assembly so
-// the compiler does not tie later LDS reads to it; completion is made visible
-// only by the explicit vmcnt wait and barrier of the tile loop.
-__device__ inline void lds_dma16(const void* gptr, const void* lds_base) {
-  const uint32_t base = __builtin_amdgcn_readfirstlane(
-      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((CS_LDS const void*)lds_base)));
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" : : "s"(base), "v"(gptr)
-               : "memory", "m0");
+// Direct global -> LDS load of 16 bytes per lane: lane i's bytes land at LDS
+// byte address lds + 16 i (lds wave-uniform, in an SGPR).  Issued through
+// inline assembly so the compiler does not tie later LDS reads to it;
+// completion is made visible only by the explicit vmcnt wait and barrier of
+// the tile loop.
+__device__ inline void lds_dma16(const void* gptr, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+               : : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(gptr) : "memory", "m0");
+}
+
+// LDS byte address of a __shared__ object (the generic -> LDS conversion,
+// done once outside the tile loop)
+__device__ inline uint32_t lds_address(const void* p) {
+  return __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((CS_LDS const void*)p)));
 }
 
 // Flat workgroup id -> (batch, kv head, row block).  Dispatch is round-robin
@@ -301,16 +307,19 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
     const uint16_t* r = (kpart ? rec_base : vrec_base) + off;
     return ok ? r : z;
   };
-  auto issue = [&](int t, stage_t& st) {
+  // LDS byte addresses of the stages; K at +0, V at +kStageSlots * 16
+  const uint32_t st_lds[kStages] = {lds_address(&st0), lds_address(&st1), lds_address(&st2)};
+  auto issue = [&](int t, int stage) {
     const uint16_t* kr = row_of(t, k_key, true);
     const uint16_t* vr[kInstr];
 #pragma unroll
     for (int i = 0; i < kInstr; ++i) vr[i] = row_of(t, 4 * (kInstr * wave + i) + (lane & 3), false);
+    const uint32_t kbase = st_lds[stage], vbase = kbase + kStageSlots * 16;
 #pragma unroll
     for (int i = 0; i < kInstr; ++i) {
       const int j = kInstr * wave + i;
-      lds_dma16(kr + 8 * (4 * (j & 3) + (lane >> 4)), st.k + 64 * j);
-      lds_dma16(vr[i] + 8 * v_chunk, st.v + 64 * j);
+      lds_dma16(kr + 8 * (4 * (j & 3) + (lane >> 4)), kbase + 1024 * j);
+      lds_dma16(vr[i] + 8 * v_chunk, vbase + 1024 * j);
     }
   };
   // wait until this wave's loads of the current tile have landed, with the
@@ -347,21 +356,6 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
     for (int ks = 0; ks < 8; ++ks) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[ks], qb[ks], s, 0, 0, 0);
     __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // the 8 LDS reads
     __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);  // then the 8 MFMAs
-    // V^T operands: independent of the softmax, so read now and consumed after
-    // it; byte offset of this lane's read = 1024 h + 64 chunk-in-block +
-    // 16 (key % 4) + 8 half, plus 4096 ks + 2048 r + 256 db
-    bf16x8 va[8];
-    const uint16_t* vrd = reinterpret_cast<const uint16_t*>(vst) + vrd_off;
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        const bf16x4_tr lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-            (CS_LDS bf16x4_tr*)(vrd + 2048 * ks + 128 * db));
-        const bf16x4_tr hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-            (CS_LDS bf16x4_tr*)(vrd + 2048 * ks + 1024 + 128 * db));
-        va[4 * ks + db] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-      }
     const bool need_mask = (base + kTileN - 1 > wmin32) || (base + kTileN > kend32);
     // key v of the tile (8 (v/4) + 4h + v%4) is visible to the column when
     // 8 (v/4) + v%4 <= lim
@@ -419,10 +413,27 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
         const int hi = lo + 1 < p.npos - 1 ? lo + 1 : p.npos - 1;
         const float tlo = static_cast<float>(tcol[lo]);
         const float bias = tlo + (pos - fl) * (static_cast<float>(tcol[hi]) - tlo) - top_qe;
-        s[v] = s[v] == -INFINITY ? -INFINITY : s[v] * kLog2e + bias;
+        // a select, not a branch around the table reads (the indices are always in range)
+        const float biased = s[v] * kLog2e + bias;
+        s[v] = __builtin_unpredictable(s[v] == -INFINITY) ? -INFINITY : biased;
       }
       carry += total;
     }
+    // V^T operands, read after the bias work (not live across it, which keeps
+    // registers for the 8 K operands above) and consumed after the softmax; byte offset of this lane's read = 1024 h + 64 chunk-in-block +
+    // 16 (key % 4) + 8 half, plus 4096 ks + 2048 r + 256 db
+    bf16x8 va[8];
+    const uint16_t* vrd = reinterpret_cast<const uint16_t*>(vst) + vrd_off;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const bf16x4_tr lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+            (CS_LDS bf16x4_tr*)(vrd + 2048 * ks + 128 * db));
+        const bf16x4_tr hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+            (CS_LDS bf16x4_tr*)(vrd + 2048 * ks + 1024 + 128 * db));
+        va[4 * ks + db] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
     // online softmax over the 32 keys of the column (16 here, 16 in lane n ^ 32);
     // the running max m_run is kept in scaled (log2) units
     float tmax = s[0];
@@ -484,22 +495,22 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
       load_window(tlo, thi);
       __syncthreads();
     }
-    issue(thi - 1, st0);
-    if (thi - 2 >= tlo) issue(thi - 2, st1);
+    issue(thi - 1, 0);
+    if (thi - 2 >= tlo) issue(thi - 2, 1);
     for (int t = thi - 1; t >= tlo; t -= 3) {
       wait_tile(t - 1 >= tlo);
       __syncthreads();
-      if (t - 2 >= tlo) issue(t - 2, st2);
+      if (t - 2 >= tlo) issue(t - 2, 2);
       compute(t, st0.k, st0.v);
       if (t - 1 < tlo) break;
       wait_tile(t - 2 >= tlo);
       __syncthreads();
-      if (t - 3 >= tlo) issue(t - 3, st0);
+      if (t - 3 >= tlo) issue(t - 3, 0);
       compute(t - 1, st1.k, st1.v);
       if (t - 2 < tlo) break;
       wait_tile(t - 3 >= tlo);
       __syncthreads();
-      if (t - 4 >= tlo) issue(t - 4, st1);
+      if (t - 4 >= tlo) issue(t - 4, 1);
       compute(t - 2, st2.k, st2.v);
     }
     thi = tlo;
