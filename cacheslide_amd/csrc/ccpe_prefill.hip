@@ -38,9 +38,11 @@
 // LDS tile layouts (16-byte chunk c of key k, in 16-byte slots), chosen so
 // every read is one per-lane base plus an immediate offset and no two lanes
 // of a 16-lane phase share a bank:
-//   K: slot (k / 16) * 256 + c * 16 + k % 16   (A reads: 16 keys x one chunk)
-//   V: slot (k / 4) * 64 + c * 4 + k % 4       (transposed reads: 4 keys x 2 chunks)
-// The direct loads pick, per lane, the (key, chunk) that lands in its slot.
+//   K: slot (k / 4) * 64 + (c ^ (k / 4 % 4)) * 4 + k % 4   (A reads: 16 keys x one chunk)
+//   V: slot (k / 4) * 64 + c * 4 + k % 4                   (transposed reads: 4 keys x 2 chunks)
+// so one direct load (64 lanes x 16 bytes = slots 64 j .. 64 j + 63) covers the
+// same four keys 4j .. 4j+3 in K and in V, and each lane loads key 4j + lane % 4
+// of both: the record address of a key is computed once for K and V.
 
 #include "common.h"
 
@@ -271,11 +273,10 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
   };
 
   // ---- tile loads.  Load j (0..7) of a stage fills slots [64 j, 64 j + 64) of
-  // K and of V; wave w issues loads j = kInstr w .. kInstr w + kInstr - 1.
-  // K: key 16 (j / 4) + lane % 16, chunk 4 (j % 4) + lane / 16 (the key is
-  // the same for all loads of a wave).  V: key 4j + lane % 4, chunk lane / 4.
-  const int k_key = 16 * ((kInstr * wave) >> 2) + (lane & 15);
-  const int v_chunk = lane >> 2;
+  // K and of V with keys 4j .. 4j+3, lane l taking key 4j + l % 4: K chunk
+  // (l / 4) ^ (j % 4), V chunk l / 4.  Wave w issues loads j = kInstr w ..
+  // kInstr w + kInstr - 1, so its lanes need kInstr records per tile.
+  const int chunk = lane >> 2;
   bool bad_block = false;
   // record base of this request / KV head; per-key offsets below are 32-bit
   // products (the host checks that the strides fit)
@@ -287,39 +288,34 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
   const uint32_t v_st = static_cast<uint32_t>(PAGED ? p.kv.s_block : p.kv.v_st);
   const uint32_t off_mask = PAGED ? (1u << p.kv.bs_shift) - 1u : 0u;
   const int nblocks = PAGED ? static_cast<int>(p.kv.num_blocks < INT32_MAX ? p.kv.num_blocks : INT32_MAX) : 0;
-  // K (kpart) or V row of key t * 32 + key; the zero record when the key is
-  // past kend or its block is invalid (branch-free)
-  auto row_of = [&](int t, int key, bool kpart) -> const uint16_t* {
-    const uint16_t* z = reinterpret_cast<const uint16_t*>(g_zero_record) + (kpart ? 0 : kD);
-    const int j = t * kTileN + key;
-    const bool in = j < kend32;
-    uint64_t off;
-    bool ok = in;
-    if constexpr (PAGED) {
-      const int blk = bt_lds[(j >> p.kv.bs_shift) - static_cast<int>(bt_lo)];
-      ok = in && blk >= 0 && blk < nblocks;
-      bad_block |= in && !ok;
-      off = static_cast<uint64_t>(static_cast<uint32_t>(blk)) * s_blk +
-            static_cast<uint64_t>(static_cast<uint32_t>(j) & off_mask) * s_off;
-    } else {
-      off = static_cast<uint64_t>(static_cast<uint32_t>(j)) * (kpart ? s_blk : v_st);
-    }
-    const uint16_t* r = (kpart ? rec_base : vrec_base) + off;
-    return ok ? r : z;
-  };
+  const uint16_t* zrec = reinterpret_cast<const uint16_t*>(g_zero_record);
   // LDS byte addresses of the stages; K at +0, V at +kStageSlots * 16
   const uint32_t st_lds[kStages] = {lds_address(&st0), lds_address(&st1), lds_address(&st2)};
   auto issue = [&](int t, int stage) {
-    const uint16_t* kr = row_of(t, k_key, true);
-    const uint16_t* vr[kInstr];
-#pragma unroll
-    for (int i = 0; i < kInstr; ++i) vr[i] = row_of(t, 4 * (kInstr * wave + i) + (lane & 3), false);
     const uint32_t kbase = st_lds[stage], vbase = kbase + kStageSlots * 16;
 #pragma unroll
     for (int i = 0; i < kInstr; ++i) {
       const int j = kInstr * wave + i;
-      lds_dma16(kr + 8 * (4 * (j & 3) + (lane >> 4)), kbase + 1024 * j);
-      lds_dma16(vr[i] + 8 * v_chunk, vbase + 1024 * j);
+      // K and V rows of key t * 32 + 4j + lane % 4; the zero record (branch-free)
+      // when the key is past kend or its block is invalid
+      const int key = t * kTileN + 4 * j + (lane & 3);
+      const bool in = key < kend32;
+      const uint16_t* kr;
+      const uint16_t* vr;
+      if constexpr (PAGED) {
+        const int blk = bt_lds[(key >> p.kv.bs_shift) - static_cast<int>(bt_lo)];
+        const bool ok = in && blk >= 0 && blk < nblocks;
+        bad_block |= in && !ok;
+        const uint64_t off = static_cast<uint64_t>(static_cast<uint32_t>(blk)) * s_blk +
+                             static_cast<uint64_t>(static_cast<uint32_t>(key) & off_mask) * s_off;
+        kr = ok ? rec_base + off : zrec;
+        vr = kr + kD;
+      } else {
+        kr = in ? rec_base + static_cast<uint64_t>(static_cast<uint32_t>(key)) * s_blk : zrec;
+        vr = in ? vrec_base + static_cast<uint64_t>(static_cast<uint32_t>(key)) * v_st : zrec + kD;
+      }
+      lds_dma16(kr + 8 * (chunk ^ (j & 3)), kbase + 1024 * j);
+      lds_dma16(vr + 8 * chunk, vbase + 1024 * j);
     }
   };
   // wait until this wave's loads of the current tile have landed, with the
@@ -347,10 +343,14 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
     const int base = t * kTileN;
     if (base > wmax32) return;  // every column of the wave precedes the tile
     // all K operands first, then the 8 MFMAs of S^T
+    // key n, chunk 2 ks + h: slot (n / 4) * 64 + ((2 ks + h) ^ g) * 4 + n % 4 with
+    // g = n / 4 % 4, i.e. one of two per-lane bases (ks even / odd) + 16 (ks / 2)
     bf16x8 ka[8];
-    const uint4* krd = kst + (n >> 4) * 256 + h * 16 + (n & 15);  // + 32 ks slots
+    const int g = (n >> 2) & 3;
+    const uint4* krd0 = kst + (n >> 2) * 64 + (n & 3) + 4 * (h ^ g);
+    const uint4* krd1 = kst + (n >> 2) * 64 + (n & 3) + 4 * ((2 + h) ^ g);
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) ka[ks] = as_bf16x8(krd[32 * ks]);
+    for (int ks = 0; ks < 8; ++ks) ka[ks] = as_bf16x8((ks & 1 ? krd1 : krd0)[16 * (ks >> 1)]);
     floatx16 s = {};
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[ks], qb[ks], s, 0, 0, 0);
