@@ -51,6 +51,7 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4_tr;
 #define CS_LDS __attribute__((address_space(3)))
@@ -78,7 +79,6 @@ __device__ inline void swap_halves(float x, float& lo, float& hi) {
 }
 
 __device__ inline uint32_t pack_bf16x2(float a, float b) {
-  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
   const bf16x2 v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
   return __builtin_bit_cast(uint32_t, v);
 }
@@ -214,12 +214,23 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
   uint16_t* elo = reinterpret_cast<uint16_t*>(&st1);
   _Float16* tcol = tab + c * p.tab_stride;
   for (int pc = 0; pc < p.npos; pc += kPosChunk) {
-    __syncthreads();
-    for (int i = tid; i < kPosChunk * kD; i += kThreads) {
-      const int pos = i % kPosChunk, d = i / kPosChunk;  // consecutive threads: consecutive positions
-      const float ev = pc + pos < p.npos ? p.e[d * p.npos + pc + pos] : 0.f;
-      const __bf16 hb = static_cast<__bf16>(ev);
-      const __bf16 lb = static_cast<__bf16>(ev - static_cast<float>(hb));
+    // thread: position pc + tid % 64, dims tid / 64 + (kThreads / 64) r; all its
+    // loads are issued before any is used (one memory latency, not one per value)
+    constexpr int kPer = kPosChunk * kD / kThreads;
+    const int pos = tid % kPosChunk, d0 = tid / kPosChunk;
+    float ev[kPer];
+    const bool pos_ok = pc + pos < p.npos;
+#pragma unroll
+    for (int r = 0; r < kPer; ++r) {
+      const int d = d0 + (kThreads / kPosChunk) * r;
+      ev[r] = pos_ok ? p.e[d * p.npos + pc + pos] : 0.f;
+    }
+    __syncthreads();  // the previous chunk's MFMAs have read the stage
+#pragma unroll
+    for (int r = 0; r < kPer; ++r) {
+      const int d = d0 + (kThreads / kPosChunk) * r;
+      const __bf16 hb = static_cast<__bf16>(ev[r]);
+      const __bf16 lb = static_cast<__bf16>(ev[r] - static_cast<float>(hb));
       const int slot = pos * kChunks + ((d >> 3) ^ (pos & 15));
       ehi[slot * 8 + (d & 7)] = __builtin_bit_cast(uint16_t, hb);
       elo[slot * 8 + (d & 7)] = __builtin_bit_cast(uint16_t, lb);
@@ -406,13 +417,14 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         float pos = carry + after[v >> 2] + gsuf[v];
-        pos = pos < top ? pos : top;
-        pos = pos > 0.f ? pos : 0.f;  // also maps NaN to 0: table reads stay in range
-        const float fl = floorf(pos);
-        const int lo = static_cast<int>(fl);
+        pos = pos < top ? pos : top;  // NaN becomes top: table reads stay in range
+        pos = pos > 0.f ? pos : 0.f;
+        const int lo = static_cast<int>(pos);  // pos >= 0: truncation is floor
+        const float frac = __builtin_amdgcn_fractf(pos);
+        // hi clamped (not lo + 1): two 16-bit reads, never one misaligned 32-bit read
         const int hi = lo + 1 < p.npos - 1 ? lo + 1 : p.npos - 1;
         const float tlo = static_cast<float>(tcol[lo]);
-        const float bias = tlo + (pos - fl) * (static_cast<float>(tcol[hi]) - tlo) - top_qe;
+        const float bias = tlo + frac * (static_cast<float>(tcol[hi]) - tlo) - top_qe;
         // a select, not a branch around the table reads (the indices are always in range)
         const float biased = s[v] * kLog2e + bias;
         s[v] = __builtin_unpredictable(s[v] == -INFINITY) ? -INFINITY : biased;
@@ -457,14 +469,18 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
     m_run = m_new;
     const float moff = live ? -m_new : 0.f;
     uint32_t pw[8];
-    float psum = 0.f;
 #pragma unroll
     for (int v = 0; v < 16; v += 2) {
       const float p0 = __builtin_amdgcn_exp2f(fmaf(s[v], scale, moff));
       const float p1 = __builtin_amdgcn_exp2f(fmaf(s[v + 1], scale, moff));
-      psum += p0 + p1;
       pw[v >> 1] = pack_bf16x2(p0, p1);
     }
+    // the column sum of the bf16 probabilities the PV MFMAs use, two per dot2
+    const bf16x2 ones = {static_cast<__bf16>(1.f), static_cast<__bf16>(1.f)};
+    float psum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      psum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pw[i]), ones, psum, false);
     l_run += psum;
     const bf16x8 pb0 = __builtin_bit_cast(bf16x8, make_uint4(pw[0], pw[1], pw[2], pw[3]));
     const bf16x8 pb1 = __builtin_bit_cast(bf16x8, make_uint4(pw[4], pw[5], pw[6], pw[7]));
