@@ -129,6 +129,18 @@ __device__ inline void lds_dma16(const void* gptr, uint32_t lds) {
                : : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(gptr) : "memory", "m0");
 }
 
+// The same with a wave-uniform 64-bit base in SGPRs and a 32-bit per-lane
+// byte offset (the instruction's saddr form): no per-lane address arithmetic.
+__device__ inline void lds_dma16_s(uint32_t voff, uint64_t sbase, uint32_t lds) {
+  // readfirstlane returns int: each half goes through uint32_t so that widening
+  // never sign-extends the low word
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(sbase >> 32)));
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(sbase)));
+  const uint64_t base = (static_cast<uint64_t>(hi) << 32) | lo;
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+               : : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(base) : "memory", "m0");
+}
+
 // LDS byte address of a __shared__ object (the generic -> LDS conversion,
 // done once outside the tile loop)
 __device__ inline uint32_t lds_address(const void* p) {
@@ -171,7 +183,7 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (an SGPR)
   const int n = lane & 31;  // column within the wave
   const int h = lane >> 5;  // k half of the MFMA operands
 
@@ -302,31 +314,65 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
   const uint16_t* zrec = reinterpret_cast<const uint16_t*>(g_zero_record);
   // LDS byte addresses of the stages; K at +0, V at +kStageSlots * 16
   const uint32_t st_lds[kStages] = {lds_address(&st0), lds_address(&st1), lds_address(&st2)};
+  // Per-lane byte offsets within the four records of a load (key 4j + lane % 4),
+  // fixed for the kernel: K chunk (lane / 4) ^ (j % 4) for each of the wave's
+  // loads, V chunk lane / 4.
+  const uint32_t key_stride_k = 2u * (PAGED ? s_off : s_blk);  // bytes between keys of a load
+  const uint32_t key_stride_v = 2u * (PAGED ? s_off : v_st);
+  uint32_t lane_koff[kInstr];
+#pragma unroll
+  for (int i = 0; i < kInstr; ++i)
+    lane_koff[i] = (lane & 3) * key_stride_k + 16u * (chunk ^ ((kInstr * wave + i) & 3));
+  const uint32_t lane_voff = (lane & 3) * key_stride_v + 16u * chunk + (PAGED ? 2u * kD : 0u);
+  const uint64_t kbase_bytes = reinterpret_cast<uint64_t>(rec_base);
+  const uint64_t vbase_bytes = PAGED ? kbase_bytes : reinterpret_cast<uint64_t>(vrec_base);
   auto issue = [&](int t, int stage) {
     const uint32_t kbase = st_lds[stage], vbase = kbase + kStageSlots * 16;
 #pragma unroll
     for (int i = 0; i < kInstr; ++i) {
       const int j = kInstr * wave + i;
-      // K and V rows of key t * 32 + 4j + lane % 4; the zero record (branch-free)
-      // when the key is past kend or its block is invalid
-      const int key = t * kTileN + 4 * j + (lane & 3);
-      const bool in = key < kend32;
-      const uint16_t* kr;
-      const uint16_t* vr;
+      const int key0 = t * kTileN + 4 * j;  // wave-uniform first key of the load
+      // Fast path: all four keys before kend and (paged) their block valid and
+      // at least 4 keys long, so the four keys share it: the record base is
+      // wave-uniform and computed in scalar registers.
+      bool fast = key0 + 3 < kend32;
+      uint64_t sk = 0, sv = 0;
       if constexpr (PAGED) {
-        const int blk = bt_lds[(key >> p.kv.bs_shift) - static_cast<int>(bt_lo)];
-        const bool ok = in && blk >= 0 && blk < nblocks;
-        bad_block |= in && !ok;
-        const uint64_t off = static_cast<uint64_t>(static_cast<uint32_t>(blk)) * s_blk +
-                             static_cast<uint64_t>(static_cast<uint32_t>(key) & off_mask) * s_off;
-        kr = ok ? rec_base + off : zrec;
-        vr = kr + kD;
+        const int blk = __builtin_amdgcn_readfirstlane(
+            bt_lds[(key0 >> p.kv.bs_shift) - static_cast<int>(bt_lo)]);
+        fast = fast && blk >= 0 && blk < nblocks && p.kv.bs_shift >= 2;  // blocks of >= 4 keys
+        sk = kbase_bytes + 2ull * (static_cast<uint64_t>(static_cast<uint32_t>(blk)) * s_blk +
+                                   static_cast<uint64_t>(static_cast<uint32_t>(key0) & off_mask) * s_off);
+        sv = sk;
       } else {
-        kr = in ? rec_base + static_cast<uint64_t>(static_cast<uint32_t>(key)) * s_blk : zrec;
-        vr = in ? vrec_base + static_cast<uint64_t>(static_cast<uint32_t>(key)) * v_st : zrec + kD;
+        sk = kbase_bytes + 2ull * static_cast<uint64_t>(static_cast<uint32_t>(key0)) * s_blk;
+        sv = vbase_bytes + 2ull * static_cast<uint64_t>(static_cast<uint32_t>(key0)) * v_st;
       }
-      lds_dma16(kr + 8 * (chunk ^ (j & 3)), kbase + 1024 * j);
-      lds_dma16(vr + 8 * chunk, vbase + 1024 * j);
+      if (fast) {
+        lds_dma16_s(lane_koff[i], sk, kbase + 1024 * j);
+        lds_dma16_s(lane_voff, sv, vbase + 1024 * j);
+      } else {
+        // K and V rows of key key0 + lane % 4; the zero record when the key is
+        // past kend or its block is invalid
+        const int key = key0 + (lane & 3);
+        const bool in = key < kend32;
+        const uint16_t* kr;
+        const uint16_t* vr;
+        if constexpr (PAGED) {
+          const int blk = bt_lds[(key >> p.kv.bs_shift) - static_cast<int>(bt_lo)];
+          const bool ok = in && blk >= 0 && blk < nblocks;
+          bad_block |= in && !ok;
+          const uint64_t off = static_cast<uint64_t>(static_cast<uint32_t>(blk)) * s_blk +
+                               static_cast<uint64_t>(static_cast<uint32_t>(key) & off_mask) * s_off;
+          kr = ok ? rec_base + off : zrec;
+          vr = kr + kD;
+        } else {
+          kr = in ? rec_base + static_cast<uint64_t>(static_cast<uint32_t>(key)) * s_blk : zrec;
+          vr = in ? vrec_base + static_cast<uint64_t>(static_cast<uint32_t>(key)) * v_st : zrec + kD;
+        }
+        lds_dma16(kr + 8 * (chunk ^ (j & 3)), kbase + 1024 * j);
+        lds_dma16(vr + 8 * chunk, vbase + 1024 * j);
+      }
     }
   };
   // wait until this wave's loads of the current tile have landed, with the
