@@ -264,7 +264,8 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int pv = pc + 32 * pb + 8 * (v >> 2) + 4 * h + (v & 3);
-        if (pv < p.npos) tcol[pv] = static_cast<_Float16>(acc[v] * kLog2e);
+        // finite in fp16 (clamped; NaN becomes -65000), so bias + (-inf) stays -inf
+        if (pv < p.npos) tcol[pv] = static_cast<_Float16>(fminf(fmaxf(acc[v] * kLog2e, -65000.f), 65000.f));
       }
     }
   }
@@ -437,10 +438,11 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
         for (int i = 3; i >= 0; --i) {
           const int v = 4 * j4 + i;
           const bool ok = 8 * j4 + i <= lim;
-          const float lg = s[v] * kInvSqrtD;
-          acc += ok ? __builtin_amdgcn_rcpf(1.f + __expf(-lg)) : 0.f;
+          // sigmoid(s / sqrt(D)) = 1 / (1 + 2^(-s log2(e) / sqrt(D))); s stays raw
+          const float e = __builtin_amdgcn_exp2f(s[v] * (-kInvSqrtD * kLog2e));
+          acc += ok ? __builtin_amdgcn_rcpf(1.f + e) : 0.f;
           gsuf[v] = acc;
-          s[v] = ok ? lg : -INFINITY;
+          s[v] = ok ? s[v] : -INFINITY;
         }
         run[j4] = acc;
       }
@@ -460,9 +462,12 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
         acc += run[j4] + other[j4];
       }
       const float total = acc;
+      float start[4];  // position of the first (right-most) key of each run
+#pragma unroll
+      for (int j4 = 0; j4 < 4; ++j4) start[j4] = carry + after[j4];
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        float pos = carry + after[v >> 2] + gsuf[v];
+        float pos = start[v >> 2] + gsuf[v];
         pos = pos < top ? pos : top;  // NaN becomes top: table reads stay in range
         pos = pos > 0.f ? pos : 0.f;
         const int lo = static_cast<int>(pos);  // pos >= 0: truncation is floor
@@ -470,10 +475,9 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
         // hi clamped (not lo + 1): two 16-bit reads, never one misaligned 32-bit read
         const int hi = lo + 1 < p.npos - 1 ? lo + 1 : p.npos - 1;
         const float tlo = static_cast<float>(tcol[lo]);
-        const float bias = tlo + frac * (static_cast<float>(tcol[hi]) - tlo) - top_qe;
-        // a select, not a branch around the table reads (the indices are always in range)
-        const float biased = s[v] * kLog2e + bias;
-        s[v] = __builtin_unpredictable(s[v] == -INFINITY) ? -INFINITY : biased;
+        const float bias = fmaf(frac, static_cast<float>(tcol[hi]) - tlo, tlo - top_qe);
+        // log2-scaled score plus bias; a masked key stays -inf (table entries are finite)
+        s[v] = fmaf(s[v], kInvSqrtD * kLog2e, bias);
       }
       carry += total;
     }
