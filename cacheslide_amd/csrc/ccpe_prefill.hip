@@ -18,9 +18,9 @@
 // Work decomposition.  A workgroup of 4 wavefronts owns 128 (row, head)
 // columns of one GQA group: 128/G rows x the G query heads of one KV head
 // (column c = row_local * G + head_local); each wave owns 32 columns.  Key
-// tiles of 32 are walked from the right-most causal key leftwards through two
+// tiles of 32 are walked from the right-most causal key leftwards through three
 // LDS stages filled by direct global->LDS loads (global_load_lds_dwordx4),
-// one tile ahead.
+// two tiles ahead.
 //
 // MFMA layout (32x32x16 bf16, lane l, n = l % 32, h = l / 32):
 //   A[m][k]: lane holds row m = n, k = 8h .. 8h+7
