@@ -13,7 +13,10 @@
 // Softmax is invariant to a per-row constant, so the kernel adds
 // bias_j - QE[P-1] instead of bias_j: keys whose position saturates at P-1
 // add nothing, and a tile whose columns all carry gate mass >= P-1 is plain
-// attention.
+// attention.  The score MFMAs accumulate onto minus the column's running max,
+// so a probability is exp2 of one multiply of the accumulator; the scores
+// themselves stay unscaled fp32 sums of exact bf16 products, which keeps the
+// gates (whose errors add up along the position sum) at fp32 accuracy.
 //
 // Work decomposition.  A workgroup of 4 wavefronts owns 128 (row, head)
 // columns of one GQA group: 128/G rows x the G query heads of one KV head
@@ -69,6 +72,8 @@ constexpr size_t kStaticLds = kStages * 2 * kStageSlots * 16 + 4 * kBtWindow + 1
 constexpr size_t kLdsLimit = 160 * 1024;
 constexpr float kInvSqrtD = 0.08838834764831845f;  // 1/sqrt(128)
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kSqrtD = 11.313708498984761f;  // sqrt(128)
+constexpr float kLn2 = 0.6931471805599453f;
 
 // Exchange with lane l ^ 32: v_permlane32_swap of x with itself leaves
 // {x[l], x[l ^ 32]} in the two results, in an order that depends on the half.
@@ -327,7 +332,33 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
   const uint32_t lane_voff = (lane & 3) * key_stride_v + 16u * chunk + (PAGED ? 2u * kD : 0u);
   const uint64_t kbase_bytes = reinterpret_cast<uint64_t>(rec_base);
   const uint64_t vbase_bytes = PAGED ? kbase_bytes : reinterpret_cast<uint64_t>(vrec_base);
+  // Paged fast-path record offsets of the wave's loads, 64 tiles at a time:
+  // lane L holds, for tile fo_top - L, the byte offset from rec_base of the
+  // record of the first key of load i, or ~0 in the high word when that load
+  // takes the per-lane path (a key at or past kend, an invalid block, blocks
+  // of fewer than 4 keys, a tile outside the block-table window).
+  uint32_t fo_lo[kInstr], fo_hi[kInstr];
+  int fo_top = 0, win_lo = 0;
+  auto preload = [&](int ttop) {
+    fo_top = ttop;
+    const int tl = ttop - lane;
+#pragma unroll
+    for (int i = 0; i < kInstr; ++i) {
+      const int key0 = tl * kTileN + 4 * (kInstr * wave + i);
+      bool ok = tl >= win_lo && key0 + 3 < kend32 && p.kv.bs_shift >= 2;
+      const int idx = ok ? (key0 >> p.kv.bs_shift) - static_cast<int>(bt_lo) : 0;
+      const int blk = bt_lds[idx];
+      ok = ok && blk >= 0 && blk < nblocks;
+      const uint64_t off = 2ull * (static_cast<uint64_t>(static_cast<uint32_t>(blk)) * s_blk +
+                                   static_cast<uint64_t>(static_cast<uint32_t>(key0) & off_mask) * s_off);
+      fo_lo[i] = ok ? static_cast<uint32_t>(off) : 0u;
+      fo_hi[i] = ok ? static_cast<uint32_t>(off >> 32) : 0xFFFFFFFFu;
+    }
+  };
   auto issue = [&](int t, int stage) {
+    if constexpr (PAGED) {
+      if (t <= fo_top - 64) preload(t);
+    }
     const uint32_t kbase = st_lds[stage], vbase = kbase + kStageSlots * 16;
 #pragma unroll
     for (int i = 0; i < kInstr; ++i) {
@@ -339,11 +370,11 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
       bool fast = key0 + 3 < kend32;
       uint64_t sk = 0, sv = 0;
       if constexpr (PAGED) {
-        const int blk = __builtin_amdgcn_readfirstlane(
-            bt_lds[(key0 >> p.kv.bs_shift) - static_cast<int>(bt_lo)]);
-        fast = fast && blk >= 0 && blk < nblocks && p.kv.bs_shift >= 2;  // blocks of >= 4 keys
-        sk = kbase_bytes + 2ull * (static_cast<uint64_t>(static_cast<uint32_t>(blk)) * s_blk +
-                                   static_cast<uint64_t>(static_cast<uint32_t>(key0) & off_mask) * s_off);
+        const int L = fo_top - t;
+        const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(fo_hi[i]), L));
+        const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(fo_lo[i]), L));
+        fast = hi != 0xFFFFFFFFu;
+        sk = kbase_bytes + ((static_cast<uint64_t>(hi) << 32) | lo);
         sv = sk;
       } else {
         sk = kbase_bytes + 2ull * static_cast<uint64_t>(static_cast<uint32_t>(key0)) * s_blk;
@@ -388,7 +419,14 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
   // ---- per-tile compute -------------------------------------------------------
   const float top = static_cast<float>(p.npos - 1);
   float carry = row_ok ? 0.f : 3.0e38f;  // padded columns count as saturated
-  float m_run = -INFINITY;               // running max (log2 domain) of the column
+  // Running max of the column's raw scores q.k.  S^T accumulates onto minit =
+  // -m_base in every register (m_base = m_run once finite, 0 before), so the
+  // scores arrive shifted by the running max: exp2 of a score is one multiply
+  // away, with no per-score subtract and no per-tile rescale test beyond the
+  // max itself.
+  float m_run = -INFINITY;
+  float m_base = 0.f;
+  floatx16 minit = {};
   float l_run = 0.f;                     // this lane's share of the column sum
   floatx16 o[4];
 #pragma unroll
@@ -409,18 +447,16 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
     const uint4* krd1 = kst + (n >> 2) * 64 + (n & 3) + 4 * ((2 + h) ^ g);
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) ka[ks] = as_bf16x8((ks & 1 ? krd1 : krd0)[16 * (ks >> 1)]);
-    floatx16 s = {};
+    floatx16 s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[0], qb[0], minit, 0, 0, 0);
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[ks], qb[ks], s, 0, 0, 0);
+    for (int ks = 1; ks < 8; ++ks) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[ks], qb[ks], s, 0, 0, 0);
     __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // the 8 LDS reads
     __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);  // then the 8 MFMAs
     const bool need_mask = (base + kTileN - 1 > wmin32) || (base + kTileN > kend32);
     // key v of the tile (8 (v/4) + 4h + v%4) is visible to the column when
     // 8 (v/4) + v%4 <= lim
     const int lim = (qp32 < kend32 - 1 ? qp32 : kend32 - 1) - base - 4 * h;
-    // s becomes the scores in log2 units; when saturated the (softmax-neutral
-    // per column) scale is left to the exponent below
-    float scale = kInvSqrtD * kLog2e;
+    // s holds the raw scores minus m_base
     if (__all(carry >= top)) {
       if (need_mask) {
 #pragma unroll
@@ -428,7 +464,7 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
           if (8 * (v >> 2) + (v & 3) > lim) s[v] = -INFINITY;
       }
     } else {
-      scale = 1.f;
+      const float gate_off = -m_base * (kInvSqrtD * kLog2e);
       // gates; runs of 4 keys (8 j4 + 4h + 0..3) and their in-run suffix sums
       float gsuf[16], run[4];
 #pragma unroll
@@ -438,8 +474,8 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
         for (int i = 3; i >= 0; --i) {
           const int v = 4 * j4 + i;
           const bool ok = 8 * j4 + i <= lim;
-          // sigmoid(s / sqrt(D)) = 1 / (1 + 2^(-s log2(e) / sqrt(D))); s stays raw
-          const float e = __builtin_amdgcn_exp2f(s[v] * (-kInvSqrtD * kLog2e));
+          // sigmoid(q.k / sqrt(D)) = 1 / (1 + 2^(-(s + m_base) log2(e) / sqrt(D)))
+          const float e = __builtin_amdgcn_exp2f(fmaf(s[v], -kInvSqrtD * kLog2e, gate_off));
           acc += ok ? __builtin_amdgcn_rcpf(1.f + e) : 0.f;
           gsuf[v] = acc;
           s[v] = ok ? s[v] : -INFINITY;
@@ -476,8 +512,9 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
         const int hi = lo + 1 < p.npos - 1 ? lo + 1 : p.npos - 1;
         const float tlo = static_cast<float>(tcol[lo]);
         const float bias = fmaf(frac, static_cast<float>(tcol[hi]) - tlo, tlo - top_qe);
-        // log2-scaled score plus bias; a masked key stays -inf (table entries are finite)
-        s[v] = fmaf(s[v], kInvSqrtD * kLog2e, bias);
+        // raw score plus the bias in raw units (the table holds QE log2(e));
+        // a masked key stays -inf (table entries are finite)
+        s[v] = fmaf(bias, kSqrtD * kLn2, s[v]);
       }
       carry += total;
     }
@@ -504,25 +541,31 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
     {
       float a, c2;
       swap_halves(tmax, a, c2);
-      tmax = fmaxf(a, c2) * scale;
+      tmax = fmaxf(a, c2);
     }
-    // The reference max moves only when the tile max exceeds it by more than
-    // 8 (log2 units): probabilities stay <= 2^8 and O is rescaled rarely.
-    const float m_new = tmax > m_run + 8.f ? tmax : m_run;
-    const bool live = m_new != -INFINITY;
-    const float corr = live ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.f;
-    if (__any(corr != 1.f)) {
-      l_run *= corr;
+    // The max moves only when the tile max exceeds it by more than 8 in log2
+    // units (the first finite tile max always moves it): probabilities stay
+    // <= 2^8 and O is rescaled rarely.
+    const bool move = tmax > (m_run == -INFINITY ? -INFINITY : 8.f * kSqrtD * kLn2);
+    if (__any(move)) {
+      const float shift = move ? tmax : 0.f;
+      const float m_new = move ? m_base + tmax : m_run;
+      const float corr = move ? __builtin_amdgcn_exp2f((m_run - m_new) * (kInvSqrtD * kLog2e)) : 1.f;
+      l_run *= corr;  // corr = 0 when the max was -inf: nothing accumulated yet
 #pragma unroll
       for (int d = 0; d < 4; ++d) o[d] *= corr;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) s[v] -= shift;
+      m_run = m_new;
+      m_base = m_new == -INFINITY ? 0.f : m_new;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) minit[v] = -m_base;
     }
-    m_run = m_new;
-    const float moff = live ? -m_new : 0.f;
     uint32_t pw[8];
 #pragma unroll
     for (int v = 0; v < 16; v += 2) {
-      const float p0 = __builtin_amdgcn_exp2f(fmaf(s[v], scale, moff));
-      const float p1 = __builtin_amdgcn_exp2f(fmaf(s[v + 1], scale, moff));
+      const float p0 = __builtin_amdgcn_exp2f(s[v] * (kInvSqrtD * kLog2e));
+      const float p1 = __builtin_amdgcn_exp2f(s[v + 1] * (kInvSqrtD * kLog2e));
       pw[v >> 1] = pack_bf16x2(p0, p1);
     }
     // the column sum of the bf16 probabilities the PV MFMAs use, two per dot2
@@ -560,6 +603,8 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
       __syncthreads();
       load_window(tlo, thi);
       __syncthreads();
+      win_lo = tlo;
+      preload(thi - 1);
     }
     issue(thi - 1, 0);
     if (thi - 2 >= tlo) issue(thi - 2, 1);
