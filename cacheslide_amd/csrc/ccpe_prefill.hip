@@ -533,21 +533,40 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
             (CS_LDS bf16x4_tr*)(vrd + 2048 * ks + 1024 + 128 * db));
         va[4 * ks + db] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
       }
-    // online softmax over the 32 keys of the column (16 here, 16 in lane n ^ 32);
-    // the running max m_run is kept in scaled (log2) units
-    float tmax = s[0];
+    // Online softmax.  The probabilities are taken against the running max as
+    // it stands (the scores arrive shifted by it); a tile only needs the max
+    // when its probabilities could grow too large (a lane's sum above 2^16) or
+    // when the column has no max yet.  Such a tile (rare: the first one, or
+    // scores rising well above every earlier key) takes the exact max, moves
+    // the running max to it, rescales O and the sum, and recomputes.
+    const bf16x2 ones = {static_cast<__bf16>(1.f), static_cast<__bf16>(1.f)};
+    uint32_t pw[8];
+    auto probs = [&]() {
+      float sum = 0.f;
 #pragma unroll
-    for (int v = 1; v < 16; ++v) tmax = fmaxf(tmax, s[v]);
-    {
-      float a, c2;
-      swap_halves(tmax, a, c2);
-      tmax = fmaxf(a, c2);
-    }
-    // The max moves only when the tile max exceeds it by more than 8 in log2
-    // units (the first finite tile max always moves it): probabilities stay
-    // <= 2^8 and O is rescaled rarely.
-    const bool move = tmax > (m_run == -INFINITY ? -INFINITY : 8.f * kSqrtD * kLn2);
-    if (__any(move)) {
+      for (int v = 0; v < 16; v += 2) {
+        const float p0 = __builtin_amdgcn_exp2f(s[v] * (kInvSqrtD * kLog2e));
+        const float p1 = __builtin_amdgcn_exp2f(s[v + 1] * (kInvSqrtD * kLog2e));
+        pw[v >> 1] = pack_bf16x2(p0, p1);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        sum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pw[i]), ones, sum, false);
+      return sum;
+    };
+    float psum = probs();
+    if (__any(!(psum <= 65536.f) || m_run == -INFINITY)) {
+      float tmax = s[0];
+#pragma unroll
+      for (int v = 1; v < 16; ++v) tmax = fmaxf(tmax, s[v]);
+      {
+        float a, c2;
+        swap_halves(tmax, a, c2);
+        tmax = fmaxf(a, c2);
+      }
+      // move to the tile max when it lies above the running max (always when
+      // there is none yet); a fully masked tile (-inf) leaves it alone
+      const bool move = tmax > (m_run == -INFINITY ? -INFINITY : 0.f);
       const float shift = move ? tmax : 0.f;
       const float m_new = move ? m_base + tmax : m_run;
       const float corr = move ? __builtin_amdgcn_exp2f((m_run - m_new) * (kInvSqrtD * kLog2e)) : 1.f;
@@ -560,20 +579,8 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
       m_base = m_new == -INFINITY ? 0.f : m_new;
 #pragma unroll
       for (int v = 0; v < 16; ++v) minit[v] = -m_base;
+      psum = probs();
     }
-    uint32_t pw[8];
-#pragma unroll
-    for (int v = 0; v < 16; v += 2) {
-      const float p0 = __builtin_amdgcn_exp2f(s[v] * (kInvSqrtD * kLog2e));
-      const float p1 = __builtin_amdgcn_exp2f(s[v + 1] * (kInvSqrtD * kLog2e));
-      pw[v >> 1] = pack_bf16x2(p0, p1);
-    }
-    // the column sum of the bf16 probabilities the PV MFMAs use, two per dot2
-    const bf16x2 ones = {static_cast<__bf16>(1.f), static_cast<__bf16>(1.f)};
-    float psum = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      psum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pw[i]), ones, psum, false);
     l_run += psum;
     const bf16x8 pb0 = __builtin_bit_cast(bf16x8, make_uint4(pw[0], pw[1], pw[2], pw[3]));
     const bf16x8 pb1 = __builtin_bit_cast(bf16x8, make_uint4(pw[4], pw[5], pw[6], pw[7]));
