@@ -231,26 +231,33 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
   uint16_t* elo = reinterpret_cast<uint16_t*>(&st1);
   _Float16* tcol = tab + c * p.tab_stride;
   for (int pc = 0; pc < p.npos; pc += kPosChunk) {
-    // thread: position pc + tid % 64, dims tid / 64 + (kThreads / 64) r; all its
-    // loads are issued before any is used (one memory latency, not one per value)
-    constexpr int kPer = kPosChunk * kD / kThreads;
-    const int pos = tid % kPosChunk, d0 = tid / kPosChunk;
-    float ev[kPer];
-    const bool pos_ok = pc + pos < p.npos;
+    // item (position pc + i % 64, dims 8 (i / 64) .. + 7) for i = tid + kThreads r:
+    // its 8 values become one 16-byte chunk of E^T hi and one of lo.  All of a
+    // thread's loads are issued before any is used.
+    constexpr int kItems = kPosChunk * kChunks / kThreads;
+    float ev[kItems][8];
 #pragma unroll
-    for (int r = 0; r < kPer; ++r) {
-      const int d = d0 + (kThreads / kPosChunk) * r;
-      ev[r] = pos_ok ? p.e[d * p.npos + pc + pos] : 0.f;
+    for (int r = 0; r < kItems; ++r) {
+      const int i = tid + kThreads * r;
+      const int pos = i % kPosChunk, dg = i / kPosChunk;
+      const bool pos_ok = pc + pos < p.npos;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ev[r][e] = pos_ok ? p.e[(8 * dg + e) * p.npos + pc + pos] : 0.f;
     }
     __syncthreads();  // the previous chunk's MFMAs have read the stage
 #pragma unroll
-    for (int r = 0; r < kPer; ++r) {
-      const int d = d0 + (kThreads / kPosChunk) * r;
-      const __bf16 hb = static_cast<__bf16>(ev[r]);
-      const __bf16 lb = static_cast<__bf16>(ev[r] - static_cast<float>(hb));
-      const int slot = pos * kChunks + ((d >> 3) ^ (pos & 15));
-      ehi[slot * 8 + (d & 7)] = __builtin_bit_cast(uint16_t, hb);
-      elo[slot * 8 + (d & 7)] = __builtin_bit_cast(uint16_t, lb);
+    for (int r = 0; r < kItems; ++r) {
+      const int i = tid + kThreads * r;
+      const int pos = i % kPosChunk, dg = i / kPosChunk;
+      bf16x8 hv, lv;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        hv[e] = static_cast<__bf16>(ev[r][e]);
+        lv[e] = static_cast<__bf16>(ev[r][e] - static_cast<float>(hv[e]));
+      }
+      const int slot = pos * kChunks + (dg ^ (pos & 15));
+      *reinterpret_cast<bf16x8*>(ehi + slot * 8) = hv;
+      *reinterpret_cast<bf16x8*>(elo + slot * 8) = lv;
     }
     __syncthreads();
 #pragma unroll
@@ -266,11 +273,17 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
         acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, qb[ks], acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, qb[ks], acc, 0, 0, 0);
       }
+      // finite in fp16 (clamped; NaN becomes -65000), so bias + (-inf) stays -inf;
+      // positions 2i, 2i + 1 in one 32-bit store (rows are 4-byte aligned, P is even)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
+      for (int v = 0; v < 16; v += 2) {
         const int pv = pc + 32 * pb + 8 * (v >> 2) + 4 * h + (v & 3);
-        // finite in fp16 (clamped; NaN becomes -65000), so bias + (-inf) stays -inf
-        if (pv < p.npos) tcol[pv] = static_cast<_Float16>(fminf(fmaxf(acc[v] * kLog2e, -65000.f), 65000.f));
+        if (pv < p.npos) {
+          typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+          const half2_t w = {static_cast<_Float16>(fminf(fmaxf(acc[v] * kLog2e, -65000.f), 65000.f)),
+                             static_cast<_Float16>(fminf(fmaxf(acc[v + 1] * kLog2e, -65000.f), 65000.f))};
+          *reinterpret_cast<half2_t*>(tcol + pv) = w;
+        }
       }
     }
   }
@@ -748,14 +761,19 @@ extern "C" int cs_ccpe_prefill_bf16(const void* q, int64_t q_s_batch, int64_t q_
   // 4 wavefronts (128 columns): two workgroups per CU while the QE table is
   // small enough, so one workgroup's prologue and barriers overlap the other's
   // tile loop; larger tables use 8 wavefronts, one workgroup per CU
-  const size_t tab4 = 2 * 4 * kCols * static_cast<size_t>(max_positions + 2);
+  // QE table row length in halfs: even (rows 4-byte aligned for the paired
+  // table stores) and an odd number of 32-bit words (no bank conflicts
+  // between columns)
+  int tab_stride = (max_positions + 1) / 2 * 2 + 2;
+  if ((tab_stride / 2) % 2 == 0) tab_stride += 2;
+  const size_t tab4 = 2 * 4 * kCols * static_cast<size_t>(tab_stride);
   const int waves = 2 * (tab4 + kStaticLds) <= kLdsLimit ? 4 : 8;
   p.rows_per_wg = kCols * waves / group;
   p.row_blocks = static_cast<int32_t>(ceil_div(nq, p.rows_per_wg));
   p.nk = nk;
   p.e = e;
   p.npos = max_positions;
-  p.tab_stride = max_positions + 2;  // halfs; an odd number of 32-bit words per column
+  p.tab_stride = tab_stride;
   p.out = static_cast<uint16_t*>(out);
   p.flags = flags;
   const int64_t total = static_cast<int64_t>(batch) * hkv * p.row_blocks;
