@@ -480,6 +480,22 @@ def test_mfma_prefill_dense_matches_oracle(device, hq, hkv, n):
     assert_close_bf16(actual, expected)
 
 
+@pytest.mark.parametrize("npos", [2, 3, 37, 127])
+def test_mfma_prefill_odd_and_small_tables(device, npos):
+    """Table lengths that are odd or tiny: P = 2, 3, 37 keep two 4-wave
+    workgroups per CU, P = 127 takes the 8-wave layout; the QE rows are padded
+    to an even length with an odd number of 32-bit words."""
+    n, hq, hkv = 333, 8, 2
+    q = seeded((n, hq, 128), 60 + npos, dtype=torch.bfloat16)
+    k = seeded((n, hkv, 128), 61 + npos, dtype=torch.bfloat16)
+    v = seeded((n, hkv, 128), 62 + npos, dtype=torch.bfloat16)
+    e = seeded((128, npos), 63 + npos, scale=0.1)
+    expected = orc.cope_attention(acc_np(q), acc_np(k), acc_np(v), e.numpy(), np.arange(n))
+    cope = cope_on(device, 128, npos, table=e)
+    actual = cope_attention(q.to(device), k.to(device), v.to(device), cope, torch.arange(n, device=device))
+    assert_close_bf16(actual, expected)
+
+
 @pytest.mark.parametrize("npos", [128, 256])
 def test_prefill_large_table_and_sparse_rows(device, npos):
     # unsorted sparse query rows and a strong table; P = 128 runs the MFMA kernel
