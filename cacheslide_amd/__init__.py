@@ -3,8 +3,8 @@
 Drop-in counterparts of the reference's cacheslide_vllm modules for CCPE
 attention (position, attention), WCA (wca, policy) and SLIDE slot management
 (slide, paged), computing on hand-written gfx950 kernels in
-_lib/libcacheslide_hip.so; plus fused paged-cache entry points (ccpe) and
-batched relocation (relocate).
+_lib/libcacheslide_hip.so; plus fused paged-cache entry points (ccpe),
+batched relocation (relocate) and the CCPE profile artifacts (profiles).
 """
 
 from .attention import CanonicalPositionPolicy, SelectedAssociationPolicy
