@@ -372,6 +372,74 @@ def wca_measure(device, layers: int = 31) -> dict:
     }
 
 
+def rows_measure(device, steps: int = 50) -> dict:
+    """Selective-prefill row bookkeeping (runtime.py:408-456) at Mistral-7B
+    hidden size: T = 16384 tokens, hidden 4096 bf16, 13926 fixed tokens; the
+    previous layer ran 2459 rows (15% of the fixed tokens plus 370 dynamic
+    ones), the next one runs 2459 rows of which 246 are newly promoted fixed
+    tokens restored from the snapshot.  Times the remap kernel (hidden and
+    residual rows) through the C ABI with prebuilt arguments, and the final
+    zero-filled [T, H] scatter; HIP events on the launch stream."""
+    import ctypes
+
+    import torch
+
+    from cacheslide_amd import _hip
+
+    T, H, F = 16384, 4096, 13926
+    g = torch.Generator().manual_seed(5000)
+    perm = torch.randperm(T, generator=g)
+    fixed = perm[:F].sort().values
+    dynamic = perm[F:F + 370].sort().values
+    sel = fixed[torch.randperm(F, generator=g)[:2089]]
+    previous = torch.cat([sel, dynamic]).sort().values
+    promoted = fixed[~torch.isin(fixed, previous)][torch.randperm(F - 2089, generator=g)[:246]]
+    keep = previous[torch.randperm(len(previous), generator=g)[246:]]
+    active = torch.cat([keep, promoted]).sort().values
+    dev = lambda x: x.to(device).contiguous()
+    fixed, previous, active = dev(fixed), dev(previous), dev(active)
+    hidden = torch.randn(len(previous), H, device=device, dtype=torch.bfloat16)
+    residual = torch.randn_like(hidden)
+    snap_h = torch.randn(F, H, device=device, dtype=torch.bfloat16)
+    snap_r = torch.randn_like(snap_h)
+    out_h = torch.empty(len(active), H, device=device, dtype=torch.bfloat16)
+    out_r = torch.empty_like(out_h)
+    final = torch.empty(T, H, device=device, dtype=torch.bfloat16)
+    restored = torch.zeros(1, dtype=torch.long, device=device)
+    flags = torch.zeros(1, dtype=torch.int32, device=device)
+    lib = _hip.load()
+    views = [_hip.view(x) for x in (hidden, residual, snap_h, snap_r, out_h, out_r, final)]
+    refs = [ctypes.byref(v) for v in views]
+    stream = _hip.stream_of(device)
+    P = _hip.ptr
+
+    def remap():
+        _hip.check(lib.cs_rows_remap(refs[0], refs[1], refs[2], refs[3], refs[4], refs[5], P(previous),
+                                     len(previous), P(active), len(active), P(fixed), F, P(restored),
+                                     P(flags), stream), "cs_rows_remap")
+
+    def scatter():
+        _hip.check(lib.cs_rows_scatter(refs[4], P(active), len(active), refs[6], P(flags), stream),
+                   "cs_rows_scatter")
+
+    ms_remap = time_steps(remap, steps, 5)
+    ms_scatter = time_steps(scatter, steps, 5)
+    torch.cuda.synchronize()
+    ok = int(flags.item()) == 0 and int(restored.item()) == 246 * (steps + 5)
+    remap_bytes = 2 * 2 * len(active) * H * 2           # hidden + residual rows, read and written
+    scatter_bytes = len(active) * H * 2 + T * H * 2     # rows read, the whole output written
+    return {
+        "workload": "selective prefill rows: 16384 tokens, hidden 4096 bf16, 2459 active rows "
+                    "(246 restored from the fixed-token snapshot), final [16384, 4096] scatter",
+        "remap_us_per_call": round(ms_remap * 1e3, 2),
+        "remap_GBs": round(remap_bytes / (ms_remap * 1e-3) / 1e9, 1),
+        "scatter_us_per_call": round(ms_scatter * 1e3, 2),
+        "scatter_GBs": round(scatter_bytes / (ms_scatter * 1e-3) / 1e9, 1),
+        "hbm_frac_remap": round(remap_bytes / (ms_remap * 1e-3) / 8e12, 4),
+        "checked": ok,
+    }
+
+
 def copy_calibration(device, nbytes: int, steps: int) -> dict:
     """A plain device copy of a known size, for scaling HBM counters
     (FETCH_SIZE / WRITE_SIZE) read under rocprofv3 --pmc."""
@@ -398,6 +466,7 @@ def main() -> int:
     ap.add_argument("--no-slide", action="store_true")
     ap.add_argument("--slide-layers", type=int, default=32)
     ap.add_argument("--no-wca", action="store_true")
+    ap.add_argument("--no-rows", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -464,6 +533,10 @@ def main() -> int:
     if not args.no_wca:
         record["wca"] = wca_measure(device)
         note(f"wca: {record['wca']['update_ms_per_layer']} ms/layer update")
+    if not args.no_rows:
+        record["rows"] = rows_measure(device)
+        note(f"rows: remap {record['rows']['remap_us_per_call']} us, "
+             f"scatter {record['rows']['scatter_us_per_call']} us")
     if not args.no_cpu_baseline:
         record["cpu_baseline"] = cpu_baseline(host, shape, args.cpu_heads)
     print(json.dumps(record), flush=True)

@@ -36,6 +36,9 @@ FLAG_PATH_NEGATIVE = 1 << 16
 FLAG_PATH_AVAILABLE = 1 << 17
 FLAG_PATH_INCREASING = 1 << 18
 FLAG_PATH_GAP = 1 << 19
+FLAG_ROW_LOST = 1 << 20
+FLAG_ROWS_UNSORTED = 1 << 21
+FLAG_ROW_INDEX = 1 << 22
 
 _DTYPE_CODES = {
     torch.float32: CS_F32,
@@ -144,6 +147,10 @@ SIGNATURES = {
     "cs_mapping_scatter": (_I32, [_P, _I64, _P, _P, _I64, _P]),
     "cs_mapping_gather": (_I32, [_P, _I64, _P, _P, _I64, _P]),
     "cs_freelist_release": (_I32, [_P, _I64, _P, _I64, _P]),
+    "cs_rows_remap": (_I32, [_VP, _VP, _VP, _VP, _VP, _VP, _P, _I64, _P, _I64, _P, _I64, _P, _P, _P]),
+    "cs_rows_missing": (_I32, [_P, _I64, _P, _I64, _P, _P]),
+    "cs_rows_scatter": (_I32, [_VP, _P, _I64, _VP, _P, _P]),
+    "cs_rows_gather": (_I32, [_VP, _P, _I64, _VP, _P, _P]),
     "cs_freelist_acquire": (_I32, [_P, _I64, _I64, _P, _P, _P]),
     "cs_wca_score": (_I32, [_VP, _P, _VP, _P, _P, _P, _P]),
     "cs_wca_alpha": (_I32, [_P, _P, _I64, ctypes.c_double, _I32, _P, _P, _P]),

@@ -18,6 +18,7 @@
  *                                     mean_head_cosine, WCAState
  *   src/cacheslide_vllm/paged.py      NativePagedKV._write_slots / gather
  *   src/cacheslide_vllm/slide.py      LayerSlotMap._fresh_slot (free-slot order)
+ *   src/cacheslide_vllm/runtime.py    CacheSlideRuntime._prefill row bookkeeping
  */
 #ifndef CACHESLIDE_HIP_H
 #define CACHESLIDE_HIP_H
@@ -75,7 +76,11 @@ enum cs_flag {
   CS_FLAG_PATH_NEGATIVE = 1 << 16,
   CS_FLAG_PATH_AVAILABLE = 1 << 17,
   CS_FLAG_PATH_INCREASING = 1 << 18,
-  CS_FLAG_PATH_GAP = 1 << 19
+  CS_FLAG_PATH_GAP = 1 << 19,
+  /* selective-prefill row bookkeeping, runtime.py:408-456 */
+  CS_FLAG_ROW_LOST = 1 << 20,         /* an active token in neither the previous rows nor the snapshot */
+  CS_FLAG_ROWS_UNSORTED = 1 << 21,    /* a token list is not ascending and distinct */
+  CS_FLAG_ROW_INDEX = 1 << 22         /* a gather index outside the source rows */
 };
 
 /* ------------------------------------------------------------------------ *
@@ -342,6 +347,43 @@ int cs_wca_commit(double* alpha, const double* next, const int64_t* rows, int64_
                   const int64_t* removed, const int64_t* nrem, uint8_t* selected,
                   uint8_t* candidate, uint8_t* removed_mask, const int32_t* abort_flags,
                   int32_t abort_mask, void* stream);
+
+/* ------------------------------------------------------------------------ *
+ * Row bookkeeping of the selective prefill (runtime.py:408-456).  Row views
+ * are [rows, H] with contiguous H; rows move bit for bit (any dtype).  Token
+ * lists named "ascending" must be ascending and distinct (else
+ * CS_FLAG_ROWS_UNSORTED).
+ * ------------------------------------------------------------------------ */
+
+/* Next layer's rows (runtime.py:408-432, replaces the lookup tables and masked
+ * copies of CacheSlideRuntime._prefill): out row i takes token active[i]; it
+ * continues from in row r with previous[r] == active[i] (previous ascending),
+ * else it is restored from snapshot row o with fixed[o] == active[i] (fixed
+ * ascending) and *restored (device int64) is incremented; a token in neither
+ * list raises CS_FLAG_ROW_LOST (ReuseFailure "a mandatory dynamic row was
+ * lost") and its out rows are zeros.  The residual views are optional
+ * together; the snapshot views may be absent when no row is restored. */
+int cs_rows_remap(const cs_view* hidden_in, const cs_view* residual_in, const cs_view* snap_hidden,
+                  const cs_view* snap_residual, cs_view* hidden_out, cs_view* residual_out,
+                  const int64_t* previous, int64_t n_prev, const int64_t* active, int64_t n_active,
+                  const int64_t* fixed, int64_t n_fixed, int64_t* restored, int32_t* flags,
+                  void* stream);
+
+/* *count (device int64) += number of active tokens not in previous (ascending):
+ * the rows cs_rows_remap restores (runtime.py:415-418 `continuing`). */
+int cs_rows_missing(const int64_t* previous, int64_t n_prev, const int64_t* active,
+                    int64_t n_active, int64_t* count, void* stream);
+
+/* out[j] = rows[k] for tokens[k] == j (tokens ascending), zeros for every other
+ * row of out (runtime.py:454-456: output = zeros; output[previous] = hidden);
+ * a token outside [0, rows of out) raises CS_FLAG_ROW_INDEX. */
+int cs_rows_scatter(const cs_view* rows, const int64_t* tokens, int64_t m, cs_view* out,
+                    int32_t* flags, void* stream);
+
+/* out[i] = src[idx[i]] (the hidden[fixed] / residual[fixed] snapshots of
+ * runtime.py:420-431); an index outside src raises CS_FLAG_ROW_INDEX. */
+int cs_rows_gather(const cs_view* src, const int64_t* idx, int64_t m, cs_view* out,
+                   int32_t* flags, void* stream);
 
 #ifdef __cplusplus
 }

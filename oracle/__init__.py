@@ -13,6 +13,7 @@ Modules:
   wca    -- WCA deviation/weights/cosine/state and the fp64 blend (wca.py)
   slide  -- paged-slot scatter/gather, relocation, free-slot order
             (paged.py, slide.py)
+  rows   -- the selective prefill's row bookkeeping (runtime.py)
 
 Pinning: every function is checked in tests/test_oracle.py against the
 reference's own closed-form test vectors (tests/test_position.py,

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 import torch
 
-from oracle import ccpe, slide, wca
+from oracle import ccpe, rows, slide, wca
 
 
 def f32(x):
@@ -399,3 +399,61 @@ def test_page_and_slot_copy():
     slide.slot_copy(cache2, [0, 9], [21, 2])
     np.testing.assert_array_equal(cache2[:, 5, :, 1], ref[:, 0, :, 0])
     np.testing.assert_array_equal(cache2[:, 0, :, 2], ref[:, 2, :, 1])
+
+
+# ------------------------------------------------------------ runtime rows
+def _brute_next_rows(hidden, residual, previous, active, fixed, snap_h, snap_r):
+    """Row by row from the definition: a continuing token keeps its previous
+    row, a newly active fixed token takes its snapshot row, anything else is
+    lost (runtime.py:408-432)."""
+    prev, fix = list(previous), list(fixed)
+    out_h, out_r, restored = [], [], 0
+    for t in active:
+        if t in prev:
+            out_h.append(hidden[prev.index(t)])
+            out_r.append(residual[prev.index(t)])
+        elif t in fix:
+            out_h.append(snap_h[fix.index(t)])
+            out_r.append(snap_r[fix.index(t)])
+            restored += 1
+        else:
+            raise rows.RowLost
+    return np.array(out_h), np.array(out_r), restored
+
+
+def test_next_layer_rows_against_the_definition():
+    rng = np.random.default_rng(5)
+    n, h = 40, 6
+    for trial in range(20):
+        fixed = np.sort(rng.choice(n, 25, replace=False))
+        mandatory = np.setdiff1d(np.arange(n), fixed)[:3]
+        previous = np.sort(np.concatenate([rng.choice(fixed, 8, replace=False), mandatory]))
+        active = np.sort(np.concatenate([rng.choice(fixed, 6, replace=False), mandatory]))
+        # every row carries its token and its source, so any mix-up shows
+        hidden = previous[:, None] * 10.0 + np.arange(h) / 10
+        residual = -hidden
+        snap_h = fixed[:, None] * 10.0 + 1000 + np.arange(h) / 10
+        snap_r = -snap_h
+        got = rows.next_layer_rows(hidden, residual, previous, active, fixed, snap_h, snap_r, n)
+        want = _brute_next_rows(hidden, residual, previous, active, fixed, snap_h, snap_r)
+        np.testing.assert_array_equal(got[0], want[0])
+        np.testing.assert_array_equal(got[1], want[1])
+        assert got[2] == want[2]
+    # unordered lists give the same rows (the lookup tables need no order)
+    perm = rng.permutation(len(previous))
+    a = rows.next_layer_rows(hidden, residual, previous, active, fixed, snap_h, snap_r, n)
+    b = rows.next_layer_rows(hidden[perm], residual[perm], previous[perm], active, fixed, snap_h, snap_r, n)
+    np.testing.assert_array_equal(a[0], b[0])
+    # a dynamic (non-fixed) token that was dropped is lost
+    keep = previous != mandatory[0]
+    with pytest.raises(rows.RowLost):
+        rows.next_layer_rows(hidden[keep], residual[keep], previous[keep], active, fixed, snap_h, snap_r, n)
+
+
+def test_scatter_and_gather_rows():
+    x = np.arange(12.0).reshape(4, 3)
+    out = rows.scatter_rows(x, [1, 4, 5, 9], 10)
+    assert out.shape == (10, 3)
+    np.testing.assert_array_equal(out[[1, 4, 5, 9]], x)
+    assert not out[[0, 2, 3, 6, 7, 8]].any()
+    np.testing.assert_array_equal(rows.gather_rows(out, [9, 1]), x[[3, 0]])
