@@ -435,8 +435,7 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
   // Running max of the column's raw scores q.k.  S^T accumulates onto minit =
   // -m_base in every register (m_base = m_run once finite, 0 before), so the
   // scores arrive shifted by the running max: exp2 of a score is one multiply
-  // away, with no per-score subtract and no per-tile rescale test beyond the
-  // max itself.
+  // away, with no per-score subtract.
   float m_run = -INFINITY;
   float m_base = 0.f;
   floatx16 minit = {};
@@ -532,8 +531,9 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
       carry += total;
     }
     // V^T operands, read after the bias work (not live across it, which keeps
-    // registers for the 8 K operands above) and consumed after the softmax; byte offset of this lane's read = 1024 h + 64 chunk-in-block +
-    // 16 (key % 4) + 8 half, plus 4096 ks + 2048 r + 256 db
+    // registers for the 8 K operands above) and consumed after the softmax.
+    // Byte offset of this lane's read = 1024 h + 64 chunk-in-block +
+    // 16 (key % 4) + 8 half, plus 4096 ks + 2048 r + 256 db.
     bf16x8 va[8];
     const uint16_t* vrd = reinterpret_cast<const uint16_t*>(vst) + vrd_off;
 #pragma unroll
