@@ -147,6 +147,7 @@ SIGNATURES = {
     "cs_mapping_scatter": (_I32, [_P, _I64, _P, _P, _I64, _P]),
     "cs_mapping_gather": (_I32, [_P, _I64, _P, _P, _I64, _P]),
     "cs_freelist_release": (_I32, [_P, _I64, _P, _I64, _P]),
+    "cs_wca_same_rows": (_I32, [_P, _P, _I64, _I32, _P, _P]),
     "cs_rows_remap": (_I32, [_VP, _VP, _VP, _VP, _VP, _VP, _P, _I64, _P, _I64, _P, _I64, _P, _P, _P]),
     "cs_rows_missing": (_I32, [_P, _I64, _P, _I64, _P, _P]),
     "cs_rows_scatter": (_I32, [_VP, _P, _I64, _VP, _P, _P]),

@@ -897,6 +897,30 @@ extern "C" int cs_mask_nonzero(const uint8_t* a, const uint8_t* b, int64_t n, in
   return CS_OK;
 }
 
+namespace cs {
+namespace {
+// ORs bit into *flags when a[i] != b[i] for some i < n.
+__global__ void same_rows_kernel(const int64_t* a, const int64_t* b, int64_t n, int32_t bit, int32_t* flags) {
+  bool diff = false;
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    diff |= a[i] != b[i];
+  if (__any(diff) && (threadIdx.x & 63) == 0) atomicOr(flags, bit);
+}
+}  // namespace
+}  // namespace cs
+
+extern "C" int cs_wca_same_rows(const int64_t* a, const int64_t* b, int64_t n, int32_t bit,
+                                int32_t* flags, void* stream) {
+  CS_REQUIRE(flags && n >= 0 && (n == 0 || (a && b)), "null arguments");
+  if (n == 0) return CS_OK;
+  const int64_t blocks = ceil_div(n, 256);
+  hipLaunchKernelGGL(same_rows_kernel, dim3(static_cast<unsigned>(blocks < 1024 ? blocks : 1024)), dim3(256), 0,
+                     as_stream(stream), a, b, n, bit, flags);
+  CS_LAUNCH_CHECK("same_rows");
+  return CS_OK;
+}
+
 extern "C" int cs_wca_blend(const cs_view* old_k, const cs_view* old_v, const int64_t* rows,
                             const cs_view* new_k, const cs_view* new_v, const double* weight,
                             const uint8_t* mandatory, cs_view* fused_k, cs_view* fused_v,

@@ -43,6 +43,7 @@ class _Flags:
         self.block = torch.zeros(1 + counters, dtype=torch.int64, device=device)
         self.steps: list[tuple[int, type, str]] = []
         self.counts: list[int] = []
+        self.stream = _hip.stream_of(device)  # the launch stream of every call of this block
 
     @property
     def ptr(self):
@@ -50,10 +51,6 @@ class _Flags:
 
     def counter(self, i: int):
         return ctypes.c_void_p(self.block.data_ptr() + 8 * (1 + i))
-
-    @property
-    def stream(self):
-        return _hip.stream_of(self.device)
 
     @property
     def abort_mask(self) -> int:
@@ -82,18 +79,19 @@ _NONFINITE_BIT = {"cached_k": 1 << 20, "recomputed_k": 1 << 21, "cached_v": 1 <<
                   "recomputed_v": 1 << 23, "a": 1 << 20, "b": 1 << 21}
 
 
-def _kv(name: str, tensor: Tensor, fl: _Flags) -> None:
+def _kv(name: str, tensor: Tensor, fl: _Flags, view=None) -> None:
     """wca.py:31-37."""
     if not isinstance(tensor, Tensor) or tensor.ndim != 3 or not tensor.is_floating_point():
         fl.finish(ValueError(f"{name} must be floating [token, head, dimension]"))
     if min(tensor.shape[1:]) < 1:
         fl.finish(ValueError(f"{name} must have nonempty heads/dimension"))
     bit = _NONFINITE_BIT[name]
-    call("cs_check_finite", vref(tensor), bit, fl.ptr, fl.stream)
+    call("cs_check_finite", view if view is not None else vref(tensor), bit, fl.ptr, fl.stream)
     fl.step(bit, WCANumericalError, f"{name} must have finite values")
 
 
-def _matching(name: str, tensor: Tensor, reference_shape, reference: Tensor, fl: _Flags) -> None:
+def _matching(name: str, tensor: Tensor, reference_shape, reference: Tensor, fl: _Flags,
+              view=None) -> None:
     """wca.py:40-47: same shape, dtype and device as the reference rows."""
     if not isinstance(tensor, Tensor) or (tensor.shape, tensor.dtype, tensor.device) != (
         reference_shape,
@@ -101,7 +99,7 @@ def _matching(name: str, tensor: Tensor, reference_shape, reference: Tensor, fl:
         reference.device,
     ):
         fl.finish(ValueError(f"{name} shape, dtype and device must match its reference"))
-    _kv(name, tensor, fl)
+    _kv(name, tensor, fl, view)
 
 
 def _mask(name: str, tensor: Tensor, n: int, device) -> None:
@@ -109,11 +107,15 @@ def _mask(name: str, tensor: Tensor, n: int, device) -> None:
         raise ValueError(f"{name} must be a bool [{n}] tensor on {device}")
 
 
-def _score(old: Tensor, fresh: Tensor, rows: Tensor | None, fl: _Flags) -> tuple[Tensor, Tensor]:
+def _score(old: Tensor, fresh: Tensor, rows: Tensor | None, fl: _Flags, out=None,
+           views=None) -> tuple[Tensor, Tensor]:
     n = fresh.shape[0]
-    err = torch.empty(n, dtype=torch.float64, device=fresh.device)
-    norm = torch.empty(n, dtype=torch.float64, device=fresh.device)
-    call("cs_wca_score", vref(old), ptr(rows), vref(fresh), ptr(err), ptr(norm), fl.ptr, fl.stream)
+    if out is None:
+        out = (torch.empty(n, dtype=torch.float64, device=fresh.device),
+               torch.empty(n, dtype=torch.float64, device=fresh.device))
+    err, norm = out
+    old_view, fresh_view = views if views is not None else (vref(old), vref(fresh))
+    call("cs_wca_score", old_view, ptr(rows), fresh_view, ptr(err), ptr(norm), fl.ptr, fl.stream)
     return err, norm
 
 
@@ -134,8 +136,8 @@ def squared_deviation(cached_k: Tensor, recomputed_k: Tensor) -> Tensor:
     return err
 
 
-def _alpha(err, norm, epsilon, clamp, fl: _Flags) -> Tensor:
-    alpha = torch.empty_like(err)
+def _alpha(err, norm, epsilon, clamp, fl: _Flags, out: Tensor | None = None) -> Tensor:
+    alpha = torch.empty_like(err) if out is None else out
     call("cs_wca_alpha", ptr(err), ptr(norm), err.numel(), float(epsilon), 1 if clamp else 0,
          ptr(alpha), fl.ptr, fl.stream)
     fl.step(2 | 16, WCANumericalError, "adaptation weight overflowed float64")
@@ -230,6 +232,11 @@ class WCAState:
     # index tensor) bumps a version and forces a recount.
     _active: Tensor | None = field(default=None, repr=False, compare=False)
     _active_key: tuple = field(default=(), repr=False, compare=False)
+    # device work space of the updates, reused from call to call (launches of
+    # one state are ordered on its stream): fp64 deviation, norm, next weight
+    # and cosine rows; the int64 promotion scratch
+    _work_f64: Tensor | None = field(default=None, repr=False, compare=False)
+    _work_i64: Tensor | None = field(default=None, repr=False, compare=False)
 
     @classmethod
     def initialize(
@@ -299,17 +306,24 @@ class WCAState:
     def selected_indices(self) -> Tensor:
         return _nonzero(self.selected_mask, None)
 
+    def _workspace(self) -> tuple[Tensor, Tensor]:
+        n = self.selected_mask.numel()
+        if self._work_f64 is None:
+            device = self.selected_mask.device
+            self._work_f64 = torch.empty(max(4 * n, 1), dtype=torch.float64, device=device)
+            self._work_i64 = torch.empty(max(2 * n, 1), dtype=torch.long, device=device)
+        return self._work_f64, self._work_i64
+
     def _promote_launch(self, fl: _Flags, counter: int, abort_mask: int = 0) -> Tensor:
         """Launch the promotion; its count goes to counter ``counter`` of ``fl``.
         With ``abort_mask`` it promotes nothing when fl's flags hold one of those bits."""
         n = self.selected_mask.numel()
-        device = self.selected_mask.device
-        scratch = torch.empty(max(2 * n, 1), dtype=torch.long, device=device)
-        promoted = torch.empty(max(n, 1), dtype=torch.long, device=device)
+        scratch = self._workspace()[1]
+        promoted = torch.empty(max(n, 1), dtype=torch.long, device=self.selected_mask.device)
         call("cs_wca_promote", ptr(self.initial_deviation), ptr(self.candidate_mask),
              ptr(self.removed_mask), ptr(self.selected_mask), n, self.budget, ptr(scratch),
              ptr(promoted), fl.counter(counter), fl.ptr if abort_mask else ctypes.c_void_p(None),
-             abort_mask, _hip.stream_of(device))
+             abort_mask, fl.stream)
         return promoted
 
     def _promote(self) -> Tensor:
@@ -336,43 +350,55 @@ class WCAState:
         device = _hip.require_device(cached_k)
         # counters: removed, promoted, next active
         fl = _Flags(device, 3)
-        _kv("cached_k", cached_k, fl)
-        _matching("cached_v", cached_v, cached_k.shape, cached_k, fl)
+        # each tensor's view is built once for all the calls below
+        ck, cv = ctypes.byref(_hip.view(cached_k)), ctypes.byref(_hip.view(cached_v))
+        _kv("cached_k", cached_k, fl, ck)
+        _matching("cached_v", cached_v, cached_k.shape, cached_k, fl, cv)
         if cached_k.shape[0] != self.reused_mask.numel():
             fl.finish(ValueError("cache token count differs from the request"))
         if cached_k.device != self.reused_mask.device:
             fl.finish(ValueError("cache device differs from the request"))
         indices = self.active_indices
+        a = indices.numel()
         if computed_indices is not None:
             if (
-                computed_indices.dtype != torch.long
+                not isinstance(computed_indices, Tensor)
+                or computed_indices.dtype != torch.long
                 or computed_indices.device != indices.device
-                or computed_indices.cpu().tolist() != indices.cpu().tolist()
+                or computed_indices.shape != indices.shape
             ):
                 fl.finish(ValueError("computed_indices must equal sorted active_indices"))
-        a = indices.numel()
+            # element equality on the device, raised in this place of the check order
+            call("cs_wca_same_rows", ptr(computed_indices.contiguous()), ptr(indices), a, 64, fl.ptr,
+                 fl.stream)
+            fl.step(64, ValueError, "computed_indices must equal sorted active_indices")
         rows_shape = (a, *cached_k.shape[1:])
-        _matching("recomputed_k", recomputed_k, rows_shape, cached_k, fl)
-        _matching("recomputed_v", recomputed_v, rows_shape, cached_v, fl)
-        err, norm = _score(cached_k, recomputed_k, indices, fl)
-        next_alpha = _alpha(err, norm, self.config.epsilon, self.config.clamp_alpha, fl)
+        rk = ctypes.byref(_hip.view(recomputed_k)) if isinstance(recomputed_k, Tensor) else None
+        rv = ctypes.byref(_hip.view(recomputed_v)) if isinstance(recomputed_v, Tensor) else None
+        _matching("recomputed_k", recomputed_k, rows_shape, cached_k, fl, rk)
+        _matching("recomputed_v", recomputed_v, rows_shape, cached_v, fl, rv)
+        work = self._workspace()[0]
+        n = self.selected_mask.numel()
+        err, norm = _score(cached_k, recomputed_k, indices, fl, out=(work[:a], work[n:n + a]),
+                           views=(ck, rk))
+        next_alpha = _alpha(err, norm, self.config.epsilon, self.config.clamp_alpha, fl,
+                            out=work[2 * n:2 * n + a])
         used = torch.empty(a, dtype=torch.float64, device=device)
         call("cs_wca_used_alpha", ptr(self.alpha), ptr(next_alpha), ptr(indices),
              ptr(self.mandatory_mask), a, 1 if self.config.weight_update == "previous_layer" else 0,
              ptr(used), fl.stream)
         fused_k = torch.empty(rows_shape, dtype=cached_k.dtype, device=device)
         fused_v = torch.empty(rows_shape, dtype=cached_v.dtype, device=device)
-        call("cs_wca_blend", vref(cached_k), vref(cached_v), ptr(indices), vref(recomputed_k),
-             vref(recomputed_v), ptr(used), ptr(None), vref(fused_k), vref(fused_v), fl.ptr,
-             fl.stream)
+        call("cs_wca_blend", ck, cv, ptr(indices), rk, rv, ptr(used), ptr(None), vref(fused_k),
+             vref(fused_v), fl.ptr, fl.stream)
         fl.step(8, WCANumericalError, "weighted K/V overflowed the cache dtype")
 
         gate = layer_index % self.config.gate_interval == 0 and a > 0
         removed_buf = None
         if gate:
-            cosine = torch.empty(a, dtype=torch.float64, device=device)
-            call("cs_wca_head_cosine", vref(recomputed_k), vref(cached_k), ptr(indices),
-                 float(self.config.epsilon), ptr(cosine), fl.stream)
+            cosine = work[3 * n:3 * n + a]
+            call("cs_wca_head_cosine", rk, ck, ptr(indices), float(self.config.epsilon), ptr(cosine),
+                 fl.stream)
             removed_buf = torch.empty(a, dtype=torch.long, device=device)
             call("cs_wca_gate", ptr(cosine), ptr(indices), ptr(self.selected_mask), a,
                  1 if self.config.convergence_mode == "distance_lt" else 0,
@@ -385,7 +411,9 @@ class WCAState:
              fl.counter(0) if gate else ctypes.c_void_p(None), ptr(self.selected_mask),
              ptr(self.candidate_mask), ptr(self.removed_mask), fl.ptr, abort, fl.stream)
         promoted_buf = self._promote_launch(fl, 1, abort)
-        active_buf = _nonzero_launch(self.selected_mask, self.mandatory_mask, fl.counter(2))
+        active_buf = torch.empty(max(n, 1), dtype=torch.long, device=device)
+        call("cs_mask_nonzero", ptr(self.selected_mask), ptr(self.mandatory_mask), n, ptr(active_buf),
+             fl.counter(2), fl.stream)
         fl.finish(read=True)
         n_removed, n_promoted, n_active = fl.counts
         removed = removed_buf[:n_removed] if gate else indices[:0]

@@ -305,6 +305,11 @@ int cs_wca_promote(const double* key, const uint8_t* candidate, const uint8_t* r
 int cs_mask_nonzero(const uint8_t* a, const uint8_t* b, int64_t n, int64_t* out, int64_t* count,
                     void* stream);
 
+/* ORs bit into *flags when a[i] != b[i] for some i < n: the device-side
+ * `computed_indices` equality check of WCAState.update (wca.py:241-247). */
+int cs_wca_same_rows(const int64_t* a, const int64_t* b, int64_t n, int32_t bit, int32_t* flags,
+                     void* stream);
+
 /* fused = w * new + (1 - w) * old in fp64 (no contraction), stored in the
  * cache dtype (fp64 -> fp32 -> 16-bit, as torch converts); w = 1 where
  * mandatory[i].  rows [a] index old (NULL = identity); fused_k/v [a,H,D].

@@ -129,6 +129,10 @@ def test_sparse_identity_validation(device):
     assert second.selected_indices.tolist() == [0, 1]
     with pytest.raises(ValueError, match="computed_indices"):
         second.update(2, cached, cached, cached[rows], cached[rows], rows.flip(0))
+    with pytest.raises(ValueError, match="computed_indices"):
+        second.update(2, cached, cached, cached[rows], cached[rows], rows[:1])
+    # the device-side mismatch left the state as it was
+    assert second.selected_indices.tolist() == [0, 1] and second.last_layer == 1
     with pytest.raises(ValueError, match="consecutively"):
         second.update(3, cached, cached, cached[rows], cached[rows])
     with pytest.raises(ValueError, match="shape, dtype"):
