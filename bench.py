@@ -440,6 +440,165 @@ def rows_measure(device, steps: int = 50) -> dict:
     }
 
 
+def snapshot_measure(device, reps: int = 5) -> dict:
+    """Layer K/V snapshot reads (runtime.py:192-272) at Mistral-7B geometry: one
+    page holds the 13926 fixed tokens' K and V, 8 kv heads x 128, bf16 (57 MB).
+
+    Wall clock per page, page bytes already in host memory:
+    * decode: bytes -> checked device tensors through SnapshotUploader
+      (staging, DMA, device finite check, flag readback);
+    * reference_decode: the reference's steps on the same bytes
+      (safetensors load, torch.isfinite on the CPU, .to(device)), synchronized;
+    * store_read: TieredPageStore.read of a resident page (its sha256 check),
+      the same cost in both implementations;
+    * h2d_GBs: the bare pinned-to-HBM DMA of the data region, HIP events on its stream;
+    * layer_loop: 8 layers of (read this layer's page, prefetch the next, a GPU
+      compute stand-in), wall clock per layer: compute alone, the reference's
+      flow (decode and the next page's checksum on the compute thread), and
+      LayerSnapshots at prefetch depth 1 (the reference's policy) and 4.
+    """
+    import ctypes
+    import tempfile
+    import time
+
+    import torch
+    from safetensors.torch import load as st_load
+
+    from cacheslide_amd import RequestPlan, _hip
+    from cacheslide_amd.snapshot import LayerSnapshots, SnapshotUploader, encode_snapshot
+    from cacheslide_amd.storage import TieredPageStore
+
+    F, HKV, D = 13926, 8, 128
+    shapes = {"k": (F, HKV, D), "v": (F, HKV, D)}
+    g = torch.Generator(device=device).manual_seed(6000)
+    kv = {n: torch.randn(F, HKV, D, device=device, generator=g).bfloat16() for n in ("k", "v")}
+    data = encode_snapshot(kv)
+    region = 2 * F * HKV * D * 2
+    uploader = SnapshotUploader(device)
+
+    def wall(fn, n=reps):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n * 1e3
+
+    def ours():
+        SnapshotUploader.take(uploader.submit(lambda: data, shapes, torch.bfloat16))
+
+    def reference():
+        tensors = st_load(data)
+        for t in tensors.values():
+            if not torch.isfinite(t).all():
+                raise ValueError("nonfinite")
+        return {n: t.to(device=device, dtype=torch.bfloat16) for n, t in tensors.items()}
+
+    got = SnapshotUploader.take(uploader.submit(lambda: data, shapes, torch.bfloat16))
+    ok = all(torch.equal(got[n].view(torch.int16), kv[n].view(torch.int16)) for n in kv)
+    ms_ours, ms_ref = wall(ours), wall(reference)
+
+    # bare DMA from pinned memory on a side stream
+    pinned = torch.empty(region, dtype=torch.uint8, pin_memory=True)
+    dst = torch.empty(region, dtype=torch.uint8, device=device)
+    side = torch.cuda.Stream(device)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    h = ctypes.c_void_p(side.cuda_stream)
+    copy = lambda: _hip.call("cs_copy_async", _hip.ptr(dst), ctypes.c_void_p(pinned.data_ptr()), region,
+                             _hip.COPY_H2D, h)
+    copy()
+    ev0.record(side)
+    for _ in range(reps):
+        copy()
+    ev1.record(side)
+    ev1.synchronize()
+    ms_dma = ev0.elapsed_time(ev1) / reps
+
+    doc = {"version": 1, "operation": "reuse", "namespace": "bench", "task_id": "snapshot",
+           "chunks": [{"id": "fixed", "role": "reuse", "start": 0, "end": F},
+                      {"id": "q", "role": "recompute", "start": F, "end": F + 64}]}
+    plan = RequestPlan.parse(doc, list(range(F + 64)))
+    L = 8
+    busy = torch.randn(8192, 8192, device=device, dtype=torch.bfloat16)
+    work = lambda: [busy @ busy for _ in range(8)]             # per-layer compute stand-in
+
+    def per_layer(loop):
+        loop()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        loop()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / L * 1e3
+
+    with tempfile.TemporaryDirectory() as root:
+        store = TieredPageStore(root + "/pages", cpu_budget_bytes=(L + 1) * len(data),
+                                disk_budget_bytes=(L + 1) * len(data))
+        key = lambda layer: plan.cache_key("bench", layer) + "/kv"
+        for layer in range(L):
+            store.put(key(layer), data)
+        ms_store = wall(lambda: store.read(key(0)))
+
+        def compute_only():
+            for _ in range(L):
+                work()
+
+        def reference_flow():
+            # runtime.py:531-536 on the compute thread: _read (decode) then
+            # _prefetch (a resident page is checksummed inside submit_load)
+            future = store.submit_load(key(0))
+            for layer in range(L):
+                future.result()
+                reference()
+                if layer + 1 < L:
+                    future = store.submit_load(key(layer + 1))
+                work()
+
+        def our_flow(depth):
+            snaps = LayerSnapshots(store, plan, "bench", device, layers=L, kv_heads=HKV, head_dim=D,
+                                   hidden_size=4096, prefetch_depth=depth)
+
+            def loop():
+                snaps.prefetch(0, torch.bfloat16)
+                for layer in range(L):
+                    snaps.read(layer, "kv", torch.bfloat16)
+                    snaps.prefetch(layer + 1, torch.bfloat16)
+                    work()
+            return snaps, loop
+
+        ms_compute = per_layer(compute_only)
+        ms_ref_loop = per_layer(reference_flow)
+        loops = {}
+        for depth in (1, 4):
+            snaps, loop = our_flow(depth)
+            loops[depth] = per_layer(loop)
+            snaps.uploader.close()
+        store.close()
+    uploader.close()
+    return {
+        "workload": "layer K/V snapshot page: 13926 fixed tokens x 8 kv heads x 128 x (K, V), bf16, "
+                    f"{region / 1e6:.1f} MB data region, page bytes in host memory",
+        "decode_ms_per_page": round(ms_ours, 3),
+        "decode_GBs": round(region / (ms_ours * 1e-3) / 1e9, 2),
+        "reference_decode_ms_per_page": round(ms_ref, 3),
+        "speedup_vs_reference_steps": round(ms_ref / ms_ours, 2),
+        "h2d_dma_GBs": round(region / (ms_dma * 1e-3) / 1e9, 2),
+        "pcie_frac": round(region / (ms_dma * 1e-3) / 64e9, 3),
+        "store_read_ms_per_page": round(ms_store, 3),
+        "layer_loop": {
+            "layers": L,
+            "compute_only_ms_per_layer": round(ms_compute, 3),
+            "reference_flow_ms_per_layer": round(ms_ref_loop, 3),
+            "prefetch_depth1_ms_per_layer": round(loops[1], 3),
+            "prefetch_depth4_ms_per_layer": round(loops[4], 3),
+        },
+        "checked": ok,
+        "note": "wall clock; the reference steps run here on the same bytes (safetensors load, "
+                "CPU isfinite, .to(device)); every read includes the store's sha256 check of the "
+                "page; PCIe 5.0 x16 is 64 GB/s per direction",
+    }
+
+
 def copy_calibration(device, nbytes: int, steps: int) -> dict:
     """A plain device copy of a known size, for scaling HBM counters
     (FETCH_SIZE / WRITE_SIZE) read under rocprofv3 --pmc."""
@@ -467,6 +626,7 @@ def main() -> int:
     ap.add_argument("--slide-layers", type=int, default=32)
     ap.add_argument("--no-wca", action="store_true")
     ap.add_argument("--no-rows", action="store_true")
+    ap.add_argument("--no-snapshot", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -537,6 +697,10 @@ def main() -> int:
         record["rows"] = rows_measure(device)
         note(f"rows: remap {record['rows']['remap_us_per_call']} us, "
              f"scatter {record['rows']['scatter_us_per_call']} us")
+    if not args.no_snapshot:
+        record["snapshot"] = snapshot_measure(device)
+        note(f"snapshot: decode {record['snapshot']['decode_ms_per_page']} ms/page, "
+             f"layer loop {record['snapshot']['layer_loop']}")
     if not args.no_cpu_baseline:
         record["cpu_baseline"] = cpu_baseline(host, shape, args.cpu_heads)
     print(json.dumps(record), flush=True)

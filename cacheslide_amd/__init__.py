@@ -4,7 +4,9 @@ Drop-in counterparts of the reference's cacheslide_vllm modules for CCPE
 attention (position, attention), WCA (wca, policy) and SLIDE slot management
 (slide, paged), computing on hand-written gfx950 kernels in
 _lib/libcacheslide_hip.so; plus fused paged-cache entry points (ccpe),
-batched relocation (relocate) and the CCPE profile artifacts (profiles).
+batched relocation (relocate), the CCPE profile artifacts (profiles), and
+the layer snapshot pages between the RAM/SSD page store and HBM (storage,
+snapshot).
 """
 
 from .attention import CanonicalPositionPolicy, SelectedAssociationPolicy
@@ -21,7 +23,8 @@ from .position import (
     validate_contextual_path,
 )
 from .slide import LayerSlotMap, SlotWrite, coalesce_slot_writes
-from .storage import CacheCapacityError, CacheIntegrityError, StaleCompletionError
+from .snapshot import LayerSnapshots, SnapshotUploader, encode_snapshot, parse_snapshot
+from .storage import CacheCapacityError, CacheIntegrityError, StaleCompletionError, TieredPageStore
 from .wca import (
     WCANumericalError,
     WCAState,
@@ -36,8 +39,9 @@ __version__ = "0.1.0"
 __all__ = [
     "CCPEPositionError", "CCPEProfile", "CacheCapacityError", "CacheIntegrityError",
     "CanonicalPositionPolicy", "ChunkIdentity", "CoPE",
-    "CoPEPositionTrace", "LayerSlotMap", "NativePagedKV", "RequestPlan",
-    "SelectedAssociationPolicy", "SlotWrite", "StaleCompletionError", "WCAConfig",
+    "CoPEPositionTrace", "LayerSlotMap", "LayerSnapshots", "NativePagedKV", "RequestPlan",
+    "SelectedAssociationPolicy", "SlotWrite", "SnapshotUploader", "StaleCompletionError",
+    "TieredPageStore", "WCAConfig",
     "WCANumericalError", "WCAState", "WCAUpdate", "adaptation_weight", "coalesce_slot_writes",
-    "cope_attention", "mean_head_cosine", "squared_deviation", "validate_contextual_path",
+    "cope_attention", "encode_snapshot", "mean_head_cosine", "parse_snapshot", "squared_deviation", "validate_contextual_path",
 ]

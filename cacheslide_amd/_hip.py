@@ -39,6 +39,7 @@ FLAG_PATH_GAP = 1 << 19
 FLAG_ROW_LOST = 1 << 20
 FLAG_ROWS_UNSORTED = 1 << 21
 FLAG_ROW_INDEX = 1 << 22
+COPY_H2D, COPY_D2H, COPY_D2D = range(3)
 
 _DTYPE_CODES = {
     torch.float32: CS_F32,
@@ -152,6 +153,8 @@ SIGNATURES = {
     "cs_rows_missing": (_I32, [_P, _I64, _P, _I64, _P, _P]),
     "cs_rows_scatter": (_I32, [_VP, _P, _I64, _VP, _P, _P]),
     "cs_rows_gather": (_I32, [_VP, _P, _I64, _VP, _P, _P]),
+    "cs_copy_async": (_I32, [_P, _P, _I64, _I32, _P]),
+    "cs_snapshot_convert": (_I32, [_VP, _VP, _I32, _P, _P]),
     "cs_freelist_acquire": (_I32, [_P, _I64, _I64, _P, _P, _P]),
     "cs_wca_score": (_I32, [_VP, _P, _VP, _P, _P, _P, _P]),
     "cs_wca_alpha": (_I32, [_P, _P, _I64, ctypes.c_double, _I32, _P, _P, _P]),

@@ -390,6 +390,26 @@ int cs_rows_scatter(const cs_view* rows, const int64_t* tokens, int64_t m, cs_vi
 int cs_rows_gather(const cs_view* src, const int64_t* idx, int64_t m, cs_view* out,
                    int32_t* flags, void* stream);
 
+/* ------------------------------------------------------------------------ *
+ * Layer snapshots between host memory and HBM (runtime.py:192-256).
+ * ------------------------------------------------------------------------ */
+enum cs_copy_kind { CS_COPY_H2D = 0, CS_COPY_D2H = 1, CS_COPY_D2D = 2 };
+
+/* hipMemcpyAsync of `bytes` on `stream`.  Replaces the host<->device moves of a
+ * snapshot: `tensor.to(device=..., dtype=...)` after safetensors decoding in
+ * `_read` (runtime.py:227-229) and `tensor.detach().contiguous().cpu()` in
+ * `_put` (runtime.py:238-243).  The host side should be pinned memory for an
+ * asynchronous DMA. */
+int cs_copy_async(void* dst, const void* src, int64_t bytes, int32_t kind, void* stream);
+
+/* The finite check and dtype conversion of a decoded snapshot tensor
+ * (runtime.py:224-229: `torch.isfinite(tensor).all()` then
+ * `tensor.to(dtype=dtype)`): raises `bit` in flags when src holds a non-finite
+ * value and writes dst = src converted with torch's rounding.  dst absent (or
+ * equal to src) checks only.  Both views contiguous, floating point. */
+int cs_snapshot_convert(const cs_view* src, const cs_view* dst, int32_t bit, int32_t* flags,
+                        void* stream);
+
 #ifdef __cplusplus
 }
 #endif
