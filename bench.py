@@ -350,14 +350,17 @@ def wca_measure(device, layers: int = 31) -> dict:
         for st, (n_k, n_v, o_k, o_v, _, _) in zip(states, reqs):
             idx = st.active_indices
             rk, rv = n_k.index_select(0, idx), n_v.index_select(0, idx)
+            computed = idx.clone()  # the caller's row positions (runtime.py:535-537)
             torch.cuda.synchronize()
             t0 = time.perf_counter()
-            st.update(layer, o_k, o_v, rk, rv)
+            st.update(layer, o_k, o_v, rk, rv, computed_indices=computed)
             torch.cuda.synchronize()
             upd_s += time.perf_counter() - t0
             a = idx.numel()
             rows += a
-            upd_bytes += 6 * a * H * D * 2  # old and new K, V rows read; fused K, V written
+            # finite checks of the whole cached K and V, then old and new K, V rows
+            # read and fused K, V written
+            upd_bytes += 2 * T * H * D * 2 + 6 * a * H * D * 2
     n_upd = layers * R
     return {
         "workload": "wca: 4 requests x 8 chunks x 2048 tokens, 8 kv heads x 128, bf16, "
@@ -368,7 +371,8 @@ def wca_measure(device, layers: int = 31) -> dict:
         "active_rows_per_update": round(rows / n_upd, 1),
         "update_GBs": round(upd_bytes / upd_s / 1e9, 1),
         "note": "wall-clock per call, host validation and the one status readback per call "
-                "included (transactional API)",
+                "included (transactional API); update bytes = finite checks of the cached K/V "
+                "plus 6 row passes",
     }
 
 
