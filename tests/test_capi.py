@@ -51,3 +51,25 @@ def test_argument_errors_need_no_device():
     # per split: gate total and carry (f64), accumulator (128 f32), max, sum,
     # fixup-queue entry; plus the queue counter
     assert lib.cs_ccpe_decode_workspace_bytes(2, 4, 1000, 256) == 2 * 4 * 4 * (8 + 8 + 4 * 128 + 4 + 4 + 4) + 16
+
+
+def test_snapshot_entry_points_check_arguments_without_a_device():
+    lib = _hip.load()
+    buf = ctypes.create_string_buffer(16)
+    assert lib.cs_copy_async(None, None, 0, _hip.COPY_H2D, None) == _hip.CS_OK   # nothing to move
+    assert lib.cs_copy_async(buf, buf, -1, _hip.COPY_H2D, None) == _hip.CS_EINVAL
+    assert lib.cs_copy_async(None, buf, 16, _hip.COPY_H2D, None) == _hip.CS_EINVAL
+    assert lib.cs_copy_async(buf, buf, 16, 7, None) == _hip.CS_EINVAL
+    assert b"copy kind" in lib.cs_last_error()
+    flags = ctypes.c_int32(0)
+    assert lib.cs_snapshot_convert(None, None, 1, ctypes.byref(flags), None) == _hip.CS_EINVAL
+    ints = _hip.CsView()
+    ints.data, ints.dtype, ints.ndim = ctypes.addressof(buf), _hip.CS_I32, 1
+    ints.shape[0], ints.stride[0] = 4, 1
+    assert lib.cs_snapshot_convert(ctypes.byref(ints), None, 1, ctypes.byref(flags), None) == _hip.CS_EINVAL
+    assert b"floating point" in lib.cs_last_error()
+    strided = _hip.CsView()
+    strided.data, strided.dtype, strided.ndim = ctypes.addressof(buf), _hip.CS_BF16, 1
+    strided.shape[0], strided.stride[0] = 4, 2
+    assert lib.cs_snapshot_convert(ctypes.byref(strided), None, 1, ctypes.byref(flags), None) == _hip.CS_EINVAL
+    assert b"contiguous" in lib.cs_last_error()
