@@ -1,8 +1,9 @@
 """Snapshot page codec on the CPU, against the safetensors library (runtime.py:192-256).
 
 The reference writes snapshot pages with ``safetensors.torch.save`` and reads
-them with ``safetensors.torch.load`` (runtime.py:17-18).  The library is
-installed here, so it is the known answer: the page header and layout built
+them with ``safetensors.torch.load`` (runtime.py:17-18), pinned at
+safetensors==0.8.0 (constraints/cpu-tests.txt:4).  That version is installed
+here, so it is the known answer: the page header and layout built
 by ``snapshot_header`` must reproduce its bytes exactly, and ``parse_snapshot``
 must accept what it loads and reject what it refuses.
 """
