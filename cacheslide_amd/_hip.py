@@ -63,6 +63,27 @@ class CsView(ctypes.Structure):
     ]
 
 
+class CsWcaUpdateArgs(ctypes.Structure):
+    """cs_wca_update_args: one WCAState.update in one library call."""
+
+    _fields_ = [
+        ("cached_k", CsView), ("cached_v", CsView), ("recomputed_k", CsView),
+        ("recomputed_v", CsView), ("fused_k", CsView), ("fused_v", CsView),
+        ("rows", ctypes.c_void_p), ("computed", ctypes.c_void_p),
+        ("a", ctypes.c_int64), ("n", ctypes.c_int64), ("budget", ctypes.c_int64),
+        ("alpha", ctypes.c_void_p), ("deviation", ctypes.c_void_p),
+        ("selected", ctypes.c_void_p), ("candidate", ctypes.c_void_p),
+        ("removed_mask", ctypes.c_void_p), ("mandatory", ctypes.c_void_p),
+        ("err", ctypes.c_void_p), ("norm", ctypes.c_void_p), ("next_alpha", ctypes.c_void_p),
+        ("cosine", ctypes.c_void_p), ("used", ctypes.c_void_p), ("removed", ctypes.c_void_p),
+        ("promoted", ctypes.c_void_p), ("scratch", ctypes.c_void_p), ("active", ctypes.c_void_p),
+        ("flags", ctypes.c_void_p), ("counts", ctypes.c_void_p),
+        ("epsilon", ctypes.c_double), ("threshold", ctypes.c_double),
+        ("clamp", ctypes.c_int32), ("previous_layer", ctypes.c_int32), ("gate", ctypes.c_int32),
+        ("distance_mode", ctypes.c_int32), ("abort_mask", ctypes.c_int32),
+    ]
+
+
 class CsCcpeArgs(ctypes.Structure):
     _fields_ = [
         ("q", CsView),
@@ -154,6 +175,7 @@ SIGNATURES = {
     "cs_rows_scatter": (_I32, [_VP, _P, _I64, _VP, _P, _P]),
     "cs_rows_gather": (_I32, [_VP, _P, _I64, _VP, _P, _P]),
     "cs_copy_async": (_I32, [_P, _P, _I64, _I32, _P]),
+    "cs_wca_update": (_I32, [ctypes.POINTER(CsWcaUpdateArgs), _P]),
     "cs_snapshot_convert": (_I32, [_VP, _VP, _I32, _P, _P]),
     "cs_freelist_acquire": (_I32, [_P, _I64, _I64, _P, _P, _P]),
     "cs_wca_score": (_I32, [_VP, _P, _VP, _P, _P, _P, _P]),

@@ -980,3 +980,39 @@ extern "C" int cs_wca_head_cosine(const cs_view* a, const cs_view* b, const int6
   CS_LAUNCH_CHECK("wca_head_cosine");
   return CS_OK;
 }
+
+extern "C" int cs_wca_update(const cs_wca_update_args* u, void* stream) {
+  CS_REQUIRE(u && u->flags && u->counts, "null arguments");
+  int32_t* f = u->flags;
+  int st;
+#define CS_STEP(expr) \
+  do {                \
+    st = (expr);      \
+    if (st != CS_OK) return st; \
+  } while (0)
+  CS_STEP(cs_check_finite(&u->cached_k, 1 << 20, f, stream));
+  CS_STEP(cs_check_finite(&u->cached_v, 1 << 22, f, stream));
+  if (u->computed) CS_STEP(cs_wca_same_rows(u->computed, u->rows, u->a, 64, f, stream));
+  CS_STEP(cs_check_finite(&u->recomputed_k, 1 << 21, f, stream));
+  CS_STEP(cs_check_finite(&u->recomputed_v, 1 << 23, f, stream));
+  CS_STEP(cs_wca_score(&u->cached_k, u->rows, &u->recomputed_k, u->err, u->norm, f, stream));
+  CS_STEP(cs_wca_alpha(u->err, u->norm, u->a, u->epsilon, u->clamp, u->next_alpha, f, stream));
+  CS_STEP(cs_wca_used_alpha(u->alpha, u->next_alpha, u->rows, u->mandatory, u->a, u->previous_layer,
+                            u->used, stream));
+  cs_view fk = u->fused_k, fv = u->fused_v;
+  CS_STEP(cs_wca_blend(&u->cached_k, &u->cached_v, u->rows, &u->recomputed_k, &u->recomputed_v, u->used,
+                       nullptr, &fk, &fv, f, stream));
+  if (u->gate) {
+    CS_STEP(cs_wca_head_cosine(&u->recomputed_k, &u->cached_k, u->rows, u->epsilon, u->cosine, stream));
+    CS_STEP(cs_wca_gate(u->cosine, u->rows, u->selected, u->a, u->distance_mode, u->threshold, u->removed,
+                        u->counts, stream));
+  }
+  CS_STEP(cs_wca_commit(u->alpha, u->next_alpha, u->rows, u->a, u->gate ? u->removed : nullptr,
+                        u->gate ? u->counts : nullptr, u->selected, u->candidate, u->removed_mask, f,
+                        u->abort_mask, stream));
+  CS_STEP(cs_wca_promote(u->deviation, u->candidate, u->removed_mask, u->selected, u->n, u->budget,
+                         u->scratch, u->promoted, u->counts + 1, f, u->abort_mask, stream));
+  CS_STEP(cs_mask_nonzero(u->selected, u->mandatory, u->n, u->active, u->counts + 2, stream));
+#undef CS_STEP
+  return CS_OK;
+}

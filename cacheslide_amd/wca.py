@@ -87,7 +87,25 @@ def _kv(name: str, tensor: Tensor, fl: _Flags, view=None) -> None:
         fl.finish(ValueError(f"{name} must have nonempty heads/dimension"))
     bit = _NONFINITE_BIT[name]
     call("cs_check_finite", view if view is not None else vref(tensor), bit, fl.ptr, fl.stream)
-    fl.step(bit, WCANumericalError, f"{name} must have finite values")
+    _finite_step(name, fl)
+
+
+def _raw(tensor: Tensor | None):
+    """Address for a struct field, None (NULL) for an absent or empty tensor, as ``ptr``."""
+    return tensor.data_ptr() if tensor is not None and tensor.numel() else None
+
+
+def _finite_step(name: str, fl: _Flags) -> None:
+    fl.step(_NONFINITE_BIT[name], WCANumericalError, f"{name} must have finite values")
+
+
+def _alpha_steps(fl: _Flags) -> None:
+    fl.step(2 | 16, WCANumericalError, "adaptation weight overflowed float64")
+    fl.step(4, WCANumericalError, "adaptation weight overflowed; inspect the K magnitudes")
+
+
+_COMPUTED_MESSAGE = "computed_indices must equal sorted active_indices"
+_BLEND_MESSAGE = "weighted K/V overflowed the cache dtype"
 
 
 def _matching(name: str, tensor: Tensor, reference_shape, reference: Tensor, fl: _Flags,
@@ -140,8 +158,7 @@ def _alpha(err, norm, epsilon, clamp, fl: _Flags, out: Tensor | None = None) -> 
     alpha = torch.empty_like(err) if out is None else out
     call("cs_wca_alpha", ptr(err), ptr(norm), err.numel(), float(epsilon), 1 if clamp else 0,
          ptr(alpha), fl.ptr, fl.stream)
-    fl.step(2 | 16, WCANumericalError, "adaptation weight overflowed float64")
-    fl.step(4, WCANumericalError, "adaptation weight overflowed; inspect the K magnitudes")
+    _alpha_steps(fl)
     return alpha
 
 
@@ -237,6 +254,7 @@ class WCAState:
     # and cosine rows; the int64 promotion scratch
     _work_f64: Tensor | None = field(default=None, repr=False, compare=False)
     _work_i64: Tensor | None = field(default=None, repr=False, compare=False)
+    _update_args: object = field(default=None, repr=False, compare=False)
 
     @classmethod
     def initialize(
@@ -344,10 +362,116 @@ class WCAState:
         recomputed_v: Tensor,
         computed_indices: Tensor | None = None,
     ) -> WCAUpdate:
-        """Fuse sparse recomputed rows against the full current-layer cache (wca.py:217-304)."""
+        """Fuse sparse recomputed rows against the full current-layer cache (wca.py:217-304).
+
+        When every host-side check passes, the device work is one library call
+        (``cs_wca_update``); otherwise the checked path below raises in the
+        reference's order of checks.
+        """
         if layer_index != self.last_layer + 1:
             raise ValueError("layers must update consecutively after full layer one")
         device = _hip.require_device(cached_k)
+        if self._inputs_pass(cached_k, cached_v, recomputed_k, recomputed_v, computed_indices):
+            return self._update_device(layer_index, device, cached_k, cached_v, recomputed_k,
+                                       recomputed_v, computed_indices)
+        return self._update_checked(layer_index, device, cached_k, cached_v, recomputed_k,
+                                    recomputed_v, computed_indices)
+
+    def _inputs_pass(self, cached_k, cached_v, recomputed_k, recomputed_v, computed) -> bool:
+        """True when none of update's host-side checks (_kv, _matching, counts) would raise."""
+        if not all(isinstance(t, Tensor) for t in (cached_k, cached_v, recomputed_k, recomputed_v)):
+            return False
+        if cached_k.ndim != 3 or not cached_k.is_floating_point() or min(cached_k.shape[1:]) < 1:
+            return False
+        if (cached_v.shape, cached_v.dtype, cached_v.device) != (cached_k.shape, cached_k.dtype,
+                                                                 cached_k.device):
+            return False
+        if cached_k.shape[0] != self.reused_mask.numel() or cached_k.device != self.reused_mask.device:
+            return False
+        indices = self.active_indices
+        if computed is not None and (
+            not isinstance(computed, Tensor)
+            or computed.dtype != torch.long
+            or computed.device != indices.device
+            or computed.shape != indices.shape
+        ):
+            return False
+        rows_shape = (indices.numel(), *cached_k.shape[1:])
+        return all((t.shape, t.dtype, t.device) == (rows_shape, ref.dtype, ref.device)
+                   for t, ref in ((recomputed_k, cached_k), (recomputed_v, cached_v)))
+
+    def _update_device(self, layer_index, device, cached_k, cached_v, recomputed_k, recomputed_v,
+                       computed_indices) -> WCAUpdate:
+        """The launches of _update_checked in one cs_wca_update call, with its checks registered."""
+        indices = self.active_indices
+        a, n = indices.numel(), self.selected_mask.numel()
+        fl = _Flags(device, 3)
+        work, scratch = self._workspace()
+        rows_shape = (a, *cached_k.shape[1:])
+        used = torch.empty(a, dtype=torch.float64, device=device)
+        fused_k = torch.empty(rows_shape, dtype=cached_k.dtype, device=device)
+        fused_v = torch.empty(rows_shape, dtype=cached_v.dtype, device=device)
+        gate = layer_index % self.config.gate_interval == 0 and a > 0
+        removed_buf = torch.empty(a, dtype=torch.long, device=device) if gate else None
+        promoted_buf = torch.empty(max(n, 1), dtype=torch.long, device=device)
+        active_buf = torch.empty(max(n, 1), dtype=torch.long, device=device)
+        computed = computed_indices.contiguous() if computed_indices is not None else None
+        # the checks in the order the launches make them (the reference's order)
+        _finite_step("cached_k", fl)
+        _finite_step("cached_v", fl)
+        if computed is not None:
+            fl.step(64, ValueError, _COMPUTED_MESSAGE)
+        _finite_step("recomputed_k", fl)
+        _finite_step("recomputed_v", fl)
+        _alpha_steps(fl)
+        fl.step(8, WCANumericalError, _BLEND_MESSAGE)
+        u = self._update_args
+        if u is None:
+            u = self._update_args = _hip.CsWcaUpdateArgs()
+        u.cached_k, u.cached_v = _hip.view(cached_k), _hip.view(cached_v)
+        u.recomputed_k, u.recomputed_v = _hip.view(recomputed_k), _hip.view(recomputed_v)
+        u.fused_k, u.fused_v = _hip.view(fused_k), _hip.view(fused_v)
+        u.rows, u.computed = _raw(indices), _raw(computed)
+        u.a, u.n, u.budget = a, n, self.budget
+        u.alpha, u.deviation = _raw(self.alpha), _raw(self.initial_deviation)
+        u.selected, u.candidate = _raw(self.selected_mask), _raw(self.candidate_mask)
+        u.removed_mask, u.mandatory = _raw(self.removed_mask), _raw(self.mandatory_mask)
+        base = work.data_ptr()
+        u.err, u.norm, u.next_alpha, u.cosine = base, base + 8 * n, base + 16 * n, base + 24 * n
+        u.used, u.removed = _raw(used), _raw(removed_buf)
+        u.promoted, u.scratch, u.active = _raw(promoted_buf), _raw(scratch), _raw(active_buf)
+        u.flags, u.counts = fl.block.data_ptr(), fl.block.data_ptr() + 8
+        u.epsilon, u.threshold = float(self.config.epsilon), float(self.config.convergence_threshold)
+        u.clamp = 1 if self.config.clamp_alpha else 0
+        u.previous_layer = 1 if self.config.weight_update == "previous_layer" else 0
+        u.gate = 1 if gate else 0
+        u.distance_mode = 1 if self.config.convergence_mode == "distance_lt" else 0
+        u.abort_mask = fl.abort_mask
+        call("cs_wca_update", ctypes.byref(u), fl.stream)
+        fl.finish(read=True)
+        return self._finish_update(layer_index, fl, indices, fused_k, fused_v, used, gate, removed_buf,
+                                   promoted_buf, active_buf)
+
+    def _finish_update(self, layer_index, fl, indices, fused_k, fused_v, used, gate, removed_buf,
+                       promoted_buf, active_buf) -> WCAUpdate:
+        n_removed, n_promoted, n_active = fl.counts
+        removed = removed_buf[:n_removed] if gate else indices[:0]
+        promoted = promoted_buf[:n_promoted]
+        next_indices = self._cache_active(active_buf, n_active)
+        self.last_layer = layer_index
+        return WCAUpdate(
+            indices=indices,
+            fused_k=fused_k,
+            fused_v=fused_v,
+            alpha=used,
+            removed_indices=removed,
+            promoted_indices=promoted,
+            next_indices=next_indices,
+        )
+
+    def _update_checked(self, layer_index, device, cached_k, cached_v, recomputed_k, recomputed_v,
+                        computed_indices) -> WCAUpdate:
+        """One library call per step, each host check in the reference's place (wca.py:217-304)."""
         # counters: removed, promoted, next active
         fl = _Flags(device, 3)
         # each tensor's view is built once for all the calls below
@@ -367,11 +491,11 @@ class WCAState:
                 or computed_indices.device != indices.device
                 or computed_indices.shape != indices.shape
             ):
-                fl.finish(ValueError("computed_indices must equal sorted active_indices"))
+                fl.finish(ValueError(_COMPUTED_MESSAGE))
             # element equality on the device, raised in this place of the check order
             call("cs_wca_same_rows", ptr(computed_indices.contiguous()), ptr(indices), a, 64, fl.ptr,
                  fl.stream)
-            fl.step(64, ValueError, "computed_indices must equal sorted active_indices")
+            fl.step(64, ValueError, _COMPUTED_MESSAGE)
         rows_shape = (a, *cached_k.shape[1:])
         rk = ctypes.byref(_hip.view(recomputed_k)) if isinstance(recomputed_k, Tensor) else None
         rv = ctypes.byref(_hip.view(recomputed_v)) if isinstance(recomputed_v, Tensor) else None
@@ -391,7 +515,7 @@ class WCAState:
         fused_v = torch.empty(rows_shape, dtype=cached_v.dtype, device=device)
         call("cs_wca_blend", ck, cv, ptr(indices), rk, rv, ptr(used), ptr(None), vref(fused_k),
              vref(fused_v), fl.ptr, fl.stream)
-        fl.step(8, WCANumericalError, "weighted K/V overflowed the cache dtype")
+        fl.step(8, WCANumericalError, _BLEND_MESSAGE)
 
         gate = layer_index % self.config.gate_interval == 0 and a > 0
         removed_buf = None
@@ -415,17 +539,5 @@ class WCAState:
         call("cs_mask_nonzero", ptr(self.selected_mask), ptr(self.mandatory_mask), n, ptr(active_buf),
              fl.counter(2), fl.stream)
         fl.finish(read=True)
-        n_removed, n_promoted, n_active = fl.counts
-        removed = removed_buf[:n_removed] if gate else indices[:0]
-        promoted = promoted_buf[:n_promoted]
-        next_indices = self._cache_active(active_buf, n_active)
-        self.last_layer = layer_index
-        return WCAUpdate(
-            indices=indices,
-            fused_k=fused_k,
-            fused_v=fused_v,
-            alpha=used,
-            removed_indices=removed,
-            promoted_indices=promoted,
-            next_indices=next_indices,
-        )
+        return self._finish_update(layer_index, fl, indices, fused_k, fused_v, used, gate, removed_buf,
+                                   promoted_buf, active_buf)

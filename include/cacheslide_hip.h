@@ -353,6 +353,45 @@ int cs_wca_commit(double* alpha, const double* next, const int64_t* rows, int64_
                   uint8_t* candidate, uint8_t* removed_mask, const int32_t* abort_flags,
                   int32_t abort_mask, void* stream);
 
+/* One WCAState.update (wca.py:217-304) in a single call, for callers that
+ * have already made the host-side checks: the calls of the entry points above
+ * in the order WCAState.update makes them, with the same flag bits --
+ * cs_check_finite of cached K (1<<20) and V (1<<22), cs_wca_same_rows of
+ * computed (64, skipped when NULL), cs_check_finite of recomputed K (1<<21)
+ * and V (1<<23), cs_wca_score, cs_wca_alpha, cs_wca_used_alpha, cs_wca_blend
+ * (2, 4, 16, 8), then on gate layers cs_wca_head_cosine and cs_wca_gate, then
+ * cs_wca_commit, cs_wca_promote and cs_mask_nonzero of selected | mandatory.
+ * The commit and the promotion do nothing when a bit of abort_mask fired.
+ * counts: removed (gate), promoted, active.  The first failing call's status
+ * is returned; no call after it is made. */
+typedef struct cs_wca_update_args {
+  cs_view cached_k, cached_v, recomputed_k, recomputed_v, fused_k, fused_v;
+  const int64_t* rows;      /* active rows, ascending [a] */
+  const int64_t* computed;  /* the caller's rows [a], or NULL */
+  int64_t a, n, budget;
+  double* alpha;            /* committed weights [n] */
+  const double* deviation;  /* initial deviation [n], the promotion key */
+  uint8_t* selected;
+  uint8_t* candidate;
+  uint8_t* removed_mask;
+  const uint8_t* mandatory;
+  double* err;              /* work [a] */
+  double* norm;             /* work [a] */
+  double* next_alpha;       /* work [a] */
+  double* cosine;           /* work [a], gate layers */
+  double* used;             /* out [a] */
+  int64_t* removed;         /* out [a], gate layers */
+  int64_t* promoted;        /* out [n] */
+  int64_t* scratch;         /* work [2n] */
+  int64_t* active;          /* out [n] */
+  int32_t* flags;           /* status word */
+  int64_t* counts;          /* [3] */
+  double epsilon, threshold;
+  int32_t clamp, previous_layer, gate, distance_mode, abort_mask;
+} cs_wca_update_args;
+
+int cs_wca_update(const cs_wca_update_args* u, void* stream);
+
 /* ------------------------------------------------------------------------ *
  * Row bookkeeping of the selective prefill (runtime.py:408-456).  Row views
  * are [rows, H] with contiguous H; rows move bit for bit (any dtype).  Token

@@ -298,3 +298,45 @@ def test_finite_check_vector_path(device, dtype):
         y[where] = bad
         with pytest.raises(WCANumericalError, match="cached_k must have finite values"):
             squared_deviation(y, x)
+
+
+@pytest.mark.parametrize("weight_update, mode, dtype", [
+    ("previous_layer", "paper_cosine_lt", torch.bfloat16),
+    ("same_layer", "distance_lt", torch.float32),
+])
+def test_single_call_update_equals_checked_update(device, weight_update, mode, dtype):
+    """update() makes its device work one cs_wca_update call when the host checks
+    pass; it must equal the step-by-step checked path bit for bit."""
+    gen = torch.Generator().manual_seed(77)
+    T, H, D = 600, 2, 64
+    fresh = torch.randn(T, H, D, generator=gen)
+    cached = (fresh + 0.05 * torch.randn(T, H, D, generator=gen)).to(dtype).to(device)
+    fresh = fresh.to(dtype).to(device)
+    reused = torch.ones(T, dtype=torch.bool, device=device)
+    reused[-3:] = False
+    config = WCAConfig(weight_update=weight_update, convergence_mode=mode, gate_interval=2,
+                       convergence_threshold=0.999 if mode == "paper_cosine_lt" else 0.001)
+    fast = WCAState.initialize(cached, fresh, reused, ~reused, config)
+    slow = WCAState.initialize(cached, fresh, reused, ~reused, config)
+    for layer in range(2, 8):
+        layer_fresh = fresh * (1 + 0.01 * layer)
+        rows = fast.active_indices
+        assert torch.equal(rows, slow.active_indices)
+        rk, rv = layer_fresh[rows], (2 * layer_fresh)[rows]
+        a = fast.update(layer, cached, cached * 0.5, rk, rv, computed_indices=rows.clone())
+        b = slow._update_checked(layer, device, cached, cached * 0.5, rk, rv, rows.clone())
+        for name in ("indices", "fused_k", "fused_v", "alpha", "removed_indices", "promoted_indices",
+                     "next_indices"):
+            x, y = getattr(a, name), getattr(b, name)
+            assert x.dtype == y.dtype and torch.equal(x, y), (layer, name)
+        for name in ("alpha", "selected_mask", "candidate_mask", "removed_mask"):
+            assert torch.equal(getattr(fast, name), getattr(slow, name)), (layer, name)
+    # a failing device check still rolls the single call back: nothing is committed
+    rows = fast.active_indices
+    before = (fast.alpha.clone(), fast.selected_mask.clone(), fast.last_layer)
+    bad = fresh[rows].clone()
+    bad[0, 0, 0] = float("nan")
+    with pytest.raises(WCANumericalError, match="recomputed_k must have finite values"):
+        fast.update(fast.last_layer + 1, cached, cached, bad, fresh[rows])
+    assert torch.equal(fast.alpha, before[0]) and torch.equal(fast.selected_mask, before[1])
+    assert fast.last_layer == before[2]
