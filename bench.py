@@ -456,10 +456,10 @@ def snapshot_measure(device, reps: int = 5) -> dict:
     * store_read: TieredPageStore.read of a resident page (its sha256 check),
       the same cost in both implementations;
     * h2d_GBs: the bare pinned-to-HBM DMA of the data region, HIP events on its stream;
-    * layer_loop: 8 layers of (read this layer's page, prefetch the next, a GPU
+    * layer_loop: 32 layers of (read this layer's page, prefetch the next, a GPU
       compute stand-in), wall clock per layer: compute alone, the reference's
       flow (decode and the next page's checksum on the compute thread), and
-      LayerSnapshots at prefetch depth 1 (the reference's policy) and 4.
+      LayerSnapshots at prefetch depth 1 (the reference's policy), 4 and 8.
     """
     import ctypes
     import tempfile
@@ -523,7 +523,7 @@ def snapshot_measure(device, reps: int = 5) -> dict:
            "chunks": [{"id": "fixed", "role": "reuse", "start": 0, "end": F},
                       {"id": "q", "role": "recompute", "start": F, "end": F + 64}]}
     plan = RequestPlan.parse(doc, list(range(F + 64)))
-    L = 8
+    L = 32  # Mistral-7B's layer count
     busy = torch.randn(8192, 8192, device=device, dtype=torch.bfloat16)
     work = lambda: [busy @ busy for _ in range(8)]             # per-layer compute stand-in
 
@@ -573,7 +573,7 @@ def snapshot_measure(device, reps: int = 5) -> dict:
         ms_compute = per_layer(compute_only)
         ms_ref_loop = per_layer(reference_flow)
         loops = {}
-        for depth in (1, 4):
+        for depth in (1, 4, 8):
             snaps, loop = our_flow(depth)
             loops[depth] = per_layer(loop)
             snaps.uploader.close()
@@ -595,6 +595,7 @@ def snapshot_measure(device, reps: int = 5) -> dict:
             "reference_flow_ms_per_layer": round(ms_ref_loop, 3),
             "prefetch_depth1_ms_per_layer": round(loops[1], 3),
             "prefetch_depth4_ms_per_layer": round(loops[4], 3),
+            "prefetch_depth8_ms_per_layer": round(loops[8], 3),
         },
         "checked": ok,
         "note": "wall clock; the reference steps run here on the same bytes (safetensors load, "
