@@ -206,3 +206,42 @@ def test_prefetch_depth_keeps_layers_in_flight(device, tmp_path):
     reader.uploader.close()
     snaps.uploader.close()
     store.close()
+
+
+def _hand_page(entries, body, pad=True, metadata=None):
+    import json
+    import struct
+    header = dict(entries)
+    if metadata is not None:
+        header = {"__metadata__": metadata, **header}
+    text = json.dumps(header, separators=(",", ":")).encode()
+    if pad:
+        text += b" " * (-len(text) % 8)
+    return struct.pack("<Q", len(text)) + text + body
+
+
+@pytest.mark.parametrize("layout", ["reversed_entries", "unpadded_metadata", "odd_offsets"])
+def test_unusual_valid_pages_decode_like_safetensors(device, layout):
+    g = torch.Generator().manual_seed(3)
+    k = torch.randn(5, 2, 3, generator=g).to(torch.bfloat16)
+    v = torch.randn(5, 2, 3, generator=g).to(torch.float32)
+    kb, vb = k.view(torch.uint8).numpy().tobytes(), v.view(torch.uint8).numpy().tobytes()
+    ek = {"dtype": "BF16", "shape": [5, 2, 3]}
+    ev = {"dtype": "F32", "shape": [5, 2, 3]}
+    if layout == "reversed_entries":    # v first in the data region, entries listed k first
+        page = _hand_page({"k": {**ek, "data_offsets": [len(vb), len(vb) + len(kb)]},
+                           "v": {**ev, "data_offsets": [0, len(vb)]}}, vb + kb)
+    elif layout == "unpadded_metadata":
+        page = _hand_page({"k": {**ek, "data_offsets": [0, len(kb)]},
+                           "v": {**ev, "data_offsets": [len(kb), len(kb) + len(vb)]}}, kb + vb,
+                          pad=False, metadata={"format": "pt"})
+    else:                               # k (60 bytes) first: v starts 4-byte aligned only
+        page = _hand_page({"k": {**ek, "data_offsets": [0, 60]},
+                           "v": {**ev, "data_offsets": [60, 60 + len(vb)]}}, kb + vb)
+    want = st_load(page)
+    uploader = SnapshotUploader(device)
+    for dtype in (torch.bfloat16, torch.float32):
+        got = SnapshotUploader.take(uploader.submit(lambda: page, {"k": (5, 2, 3), "v": (5, 2, 3)}, dtype))
+        for name in ("k", "v"):
+            assert torch.equal(bits(got[name]), bits(want[name].to(dtype))), (layout, dtype, name)
+    uploader.close()
