@@ -382,25 +382,6 @@ __global__ void check_finite_kernel(dview v, int64_t numel, int32_t bit, int32_t
 // words (all-ones exponent = inf or NaN), four words in flight per thread.
 // KIND: 0 bf16, 1 f16, 2 f32, 3 f64.
 template <int KIND>
-__device__ inline bool word_nonfinite(uint4 v) {
-  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-  bool bad = false;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    if constexpr (KIND == 0) {
-      bad |= ((w[q] & 0x7f80u) == 0x7f80u) || ((w[q] & 0x7f800000u) == 0x7f800000u);
-    } else if constexpr (KIND == 1) {
-      bad |= ((w[q] & 0x7c00u) == 0x7c00u) || ((w[q] & 0x7c000000u) == 0x7c000000u);
-    } else if constexpr (KIND == 2) {
-      bad |= (w[q] & 0x7f800000u) == 0x7f800000u;
-    } else {
-      if (q & 1) bad |= (w[q] & 0x7ff00000u) == 0x7ff00000u;
-    }
-  }
-  return bad;
-}
-
-template <int KIND>
 __global__ void __launch_bounds__(256) check_finite_vec_kernel(const uint4* p, int64_t words,
                                                                int32_t bit, int32_t* flags) {
   bool bad = false;

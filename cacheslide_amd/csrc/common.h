@@ -95,6 +95,27 @@ __device__ inline uint16_t float_to_f16(float f) {
 __device__ inline uint16_t double_to_bf16(double d) { return float_to_bf16(static_cast<float>(d)); }
 __device__ inline uint16_t double_to_f16(double d) { return float_to_f16(static_cast<float>(d)); }
 
+// Any non-finite element in a 16-byte word of KIND 0 bf16, 1 f16, 2 f32, 3 f64
+// (exponent field all ones).
+template <int KIND>
+__device__ inline bool word_nonfinite(uint4 v) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  bool bad = false;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    if constexpr (KIND == 0) {
+      bad |= ((w[q] & 0x7f80u) == 0x7f80u) || ((w[q] & 0x7f800000u) == 0x7f800000u);
+    } else if constexpr (KIND == 1) {
+      bad |= ((w[q] & 0x7c00u) == 0x7c00u) || ((w[q] & 0x7c000000u) == 0x7c000000u);
+    } else if constexpr (KIND == 2) {
+      bad |= (w[q] & 0x7f800000u) == 0x7f800000u;
+    } else {
+      if (q & 1) bad |= (w[q] & 0x7ff00000u) == 0x7ff00000u;
+    }
+  }
+  return bad;
+}
+
 // Dynamic-dtype scalar loads/stores (small tensors only: tables, positions).
 __device__ inline double load_as_double(const void* p, int dt, int64_t i) {
   switch (dt) {

@@ -981,8 +981,92 @@ extern "C" int cs_wca_head_cosine(const cs_view* a, const cs_view* b, const int6
   return CS_OK;
 }
 
+namespace cs {
+namespace {
+// The checks that open an update, in one launch: the finite checks of four
+// contiguous, 16-byte aligned tensors (segments 0..3) and the row-list
+// equality (segment 4).  Each workgroup serves one segment; the flag bits are
+// those of the separate launches.
+struct update_checks {
+  const uint4* p[4];
+  int64_t words[4];
+  int32_t kind[4];
+  int32_t bit[4];
+  int64_t first[6];  // first workgroup of each segment; first[5] = grid
+  const int64_t* ra;
+  const int64_t* rb;
+  int64_t rn;
+};
+
+template <int KIND>
+__device__ inline bool words_nonfinite(const uint4* p, int64_t words, int64_t i, int64_t step) {
+  bool bad = false;
+  for (; i + 3 * step < words; i += 4 * step) {
+    uint4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = p[i + u * step];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) bad |= word_nonfinite<KIND>(v[u]);
+  }
+  for (; i < words; i += step) bad |= word_nonfinite<KIND>(p[i]);
+  return bad;
+}
+
+__global__ void __launch_bounds__(256) update_checks_kernel(update_checks c, int32_t* flags) {
+  const int64_t b = blockIdx.x;
+  int seg = 0;
+  while (seg < 5 && b >= c.first[seg + 1]) ++seg;
+  const int64_t step = (c.first[seg + 1] - c.first[seg]) * 256;
+  const int64_t i = (b - c.first[seg]) * 256 + threadIdx.x;
+  bool bad = false;
+  int32_t bit = 64;
+  if (seg < 4) {
+    bit = c.bit[seg];
+    switch (c.kind[seg]) {
+      case 0: bad = words_nonfinite<0>(c.p[seg], c.words[seg], i, step); break;
+      case 1: bad = words_nonfinite<1>(c.p[seg], c.words[seg], i, step); break;
+      case 2: bad = words_nonfinite<2>(c.p[seg], c.words[seg], i, step); break;
+      default: bad = words_nonfinite<3>(c.p[seg], c.words[seg], i, step); break;
+    }
+  } else {
+    for (int64_t j = i; j < c.rn; j += step) bad |= c.ra[j] != c.rb[j];
+  }
+  if (__any(bad) && (threadIdx.x & 63) == 0) atomicOr(flags, bit);
+}
+
+// Fills one check segment when v is contiguous, 16-byte aligned and floating;
+// false leaves the separate launch to the caller.  An absent or empty view
+// takes no workgroups.
+bool check_segment(const cs_view* v, int32_t bit, update_checks& c, int seg, int64_t& blocks) {
+  c.p[seg] = nullptr;
+  c.words[seg] = 0;
+  c.bit[seg] = bit;
+  c.kind[seg] = 0;
+  c.first[seg] = blocks;
+  if (!v->data) return true;
+  int64_t numel = 1, expect = 1;
+  bool contiguous = true;
+  for (int d = 0; d < v->ndim; ++d) numel *= v->shape[d];
+  for (int d = v->ndim - 1; d >= 0; --d) {
+    if (v->shape[d] != 1 && v->stride[d] != expect) contiguous = false;
+    expect *= v->shape[d];
+  }
+  if (numel == 0) return true;
+  const int64_t bytes = numel * dtype_size(v->dtype);
+  if (!is_float_dtype(v->dtype) || !contiguous || (reinterpret_cast<uintptr_t>(v->data) & 15) || bytes % 16)
+    return false;
+  c.p[seg] = static_cast<const uint4*>(v->data);
+  c.words[seg] = bytes / 16;
+  c.kind[seg] = v->dtype == CS_BF16 ? 0 : v->dtype == CS_F16 ? 1 : v->dtype == CS_F32 ? 2 : 3;
+  blocks += std::min<int64_t>(ceil_div(c.words[seg], 256 * 4), 4096);
+  return true;
+}
+}  // namespace
+}  // namespace cs
+
 extern "C" int cs_wca_update(const cs_wca_update_args* u, void* stream) {
   CS_REQUIRE(u && u->flags && u->counts, "null arguments");
+  CS_REQUIRE(u->a >= 0 && (!u->computed || u->a == 0 || u->rows), "null arguments");
   int32_t* f = u->flags;
   int st;
 #define CS_STEP(expr) \
@@ -990,11 +1074,33 @@ extern "C" int cs_wca_update(const cs_wca_update_args* u, void* stream) {
     st = (expr);      \
     if (st != CS_OK) return st; \
   } while (0)
-  CS_STEP(cs_check_finite(&u->cached_k, 1 << 20, f, stream));
-  CS_STEP(cs_check_finite(&u->cached_v, 1 << 22, f, stream));
-  if (u->computed) CS_STEP(cs_wca_same_rows(u->computed, u->rows, u->a, 64, f, stream));
-  CS_STEP(cs_check_finite(&u->recomputed_k, 1 << 21, f, stream));
-  CS_STEP(cs_check_finite(&u->recomputed_v, 1 << 23, f, stream));
+  update_checks c{};
+  int64_t blocks = 0;
+  const bool fused = check_segment(&u->cached_k, 1 << 20, c, 0, blocks) &&
+                     check_segment(&u->cached_v, 1 << 22, c, 1, blocks) &&
+                     check_segment(&u->recomputed_k, 1 << 21, c, 2, blocks) &&
+                     check_segment(&u->recomputed_v, 1 << 23, c, 3, blocks);
+  if (fused) {
+    c.first[4] = blocks;
+    if (u->computed && u->a > 0) {
+      c.ra = u->computed;
+      c.rb = u->rows;
+      c.rn = u->a;
+      blocks += std::min<int64_t>(ceil_div(u->a, 256), 1024);
+    }
+    c.first[5] = blocks;
+    if (blocks > 0) {
+      hipLaunchKernelGGL(update_checks_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                         as_stream(stream), c, f);
+      CS_LAUNCH_CHECK("update_checks");
+    }
+  } else {
+    CS_STEP(cs_check_finite(&u->cached_k, 1 << 20, f, stream));
+    CS_STEP(cs_check_finite(&u->cached_v, 1 << 22, f, stream));
+    if (u->computed) CS_STEP(cs_wca_same_rows(u->computed, u->rows, u->a, 64, f, stream));
+    CS_STEP(cs_check_finite(&u->recomputed_k, 1 << 21, f, stream));
+    CS_STEP(cs_check_finite(&u->recomputed_v, 1 << 23, f, stream));
+  }
   CS_STEP(cs_wca_score(&u->cached_k, u->rows, &u->recomputed_k, u->err, u->norm, f, stream));
   CS_STEP(cs_wca_alpha(u->err, u->norm, u->a, u->epsilon, u->clamp, u->next_alpha, f, stream));
   CS_STEP(cs_wca_used_alpha(u->alpha, u->next_alpha, u->rows, u->mandatory, u->a, u->previous_layer,

@@ -362,8 +362,10 @@ int cs_wca_commit(double* alpha, const double* next, const int64_t* rows, int64_
  * (2, 4, 16, 8), then on gate layers cs_wca_head_cosine and cs_wca_gate, then
  * cs_wca_commit, cs_wca_promote and cs_mask_nonzero of selected | mandatory.
  * The commit and the promotion do nothing when a bit of abort_mask fired.
- * counts: removed (gate), promoted, active.  The first failing call's status
- * is returned; no call after it is made. */
+ * counts: removed (gate), promoted, active.  When the four K/V views are
+ * contiguous and 16-byte aligned, their finite checks and the row-list
+ * equality run as one launch with the same bits.  The first failing call's
+ * status is returned; no call after it is made. */
 typedef struct cs_wca_update_args {
   cs_view cached_k, cached_v, recomputed_k, recomputed_v, fused_k, fused_v;
   const int64_t* rows;      /* active rows, ascending [a] */

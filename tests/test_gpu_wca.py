@@ -340,3 +340,48 @@ def test_single_call_update_equals_checked_update(device, weight_update, mode, d
         fast.update(fast.last_layer + 1, cached, cached, bad, fresh[rows])
     assert torch.equal(fast.alpha, before[0]) and torch.equal(fast.selected_mask, before[1])
     assert fast.last_layer == before[2]
+
+
+def test_fused_update_checks_raise_in_reference_order(device):
+    """The single-launch checks of cached K/V, the computed rows and recomputed
+    K/V raise their own errors, the first in the reference's order when several
+    fire, and commit nothing."""
+    gen = torch.Generator().manual_seed(5)
+    cached = torch.randn(300, 2, 16, generator=gen).to(torch.bfloat16).to(device)
+    fresh = (cached.float() + 0.1).to(torch.bfloat16)
+    reused = torch.ones(300, dtype=torch.bool, device=device)
+    reused[-1] = False
+    state = WCAState.initialize(cached, fresh, reused, ~reused)
+    rows = state.active_indices
+    rk, rv = fresh[rows], fresh[rows]
+    bad_rows = rows.clone()
+    bad_rows[3] += 1
+
+    def nan(t, at):
+        t = t.clone()
+        t.view(-1)[at] = float("nan")
+        return t
+
+    cases = [
+        (dict(cached_k=nan(cached, 7)), WCANumericalError, "cached_k must have finite values"),
+        (dict(cached_v=nan(cached, 9000)), WCANumericalError, "cached_v must have finite values"),
+        (dict(computed=bad_rows), ValueError, "computed_indices must equal"),
+        (dict(rk=nan(rk, 1)), WCANumericalError, "recomputed_k must have finite values"),
+        (dict(rv=nan(rv, rv.numel() - 1)), WCANumericalError, "recomputed_v must have finite values"),
+        # several at once: the first check in the reference's order wins
+        (dict(cached_v=nan(cached, 5), computed=bad_rows, rk=nan(rk, 0)), WCANumericalError,
+         "cached_v must have finite values"),
+        (dict(computed=bad_rows, rv=nan(rv, 2)), ValueError, "computed_indices must equal"),
+    ]
+    alpha, selected = state.alpha.clone(), state.selected_mask.clone()
+    for overrides, exc, message in cases:
+        args = dict(cached_k=cached, cached_v=cached, rk=rk, rv=rv, computed=rows.clone())
+        args.update(overrides)
+        assert state._inputs_pass(args["cached_k"], args["cached_v"], args["rk"], args["rv"], args["computed"])
+        with pytest.raises(exc, match=message):
+            state.update(2, args["cached_k"], args["cached_v"], args["rk"], args["rv"],
+                         computed_indices=args["computed"])
+        assert torch.equal(state.alpha, alpha) and torch.equal(state.selected_mask, selected)
+        assert state.last_layer == 1
+    result = state.update(2, cached, cached, rk, rv, computed_indices=rows.clone())
+    assert result.fused_k.shape == rk.shape and state.last_layer == 2
