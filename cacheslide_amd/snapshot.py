@@ -330,6 +330,11 @@ class SnapshotUploader:
             tensor.record_stream(current)
         return upload.tensors
 
+    @staticmethod
+    def drain(future: Future) -> None:
+        """Wait for an upload without taking its tensors (a dropped prefetch)."""
+        future.result().done.synchronize()
+
     def close(self) -> None:
         self._fetch.shutdown(wait=True)
         self._pool.shutdown(wait=True)
@@ -429,10 +434,10 @@ class LayerSnapshots:
         try:
             if kind == "kv" and layer in self._pending:
                 future, made_for = self._pending.pop(layer)
-                tensors = SnapshotUploader.take(future)
+                tensors = self.uploader.take(future)
                 return tensors if made_for == dtype else _convert(tensors, dtype)
             future = self.uploader.submit(lambda: self.store.read(key), self._shapes(layer, kind), dtype)
-            return SnapshotUploader.take(future)
+            return self.uploader.take(future)
         except (ValueError, KeyError, OSError, RuntimeError) as exc:
             raise ReuseFailure(f"invalid {kind} snapshot at layer {layer}") from exc
 
@@ -474,6 +479,6 @@ class LayerSnapshots:
         pending, self._pending = self._pending, {}
         for future, _ in pending.values():
             try:
-                future.result().done.synchronize()
+                self.uploader.drain(future)
             except Exception:
                 pass
