@@ -237,7 +237,8 @@ class SnapshotUploader:
     non-finite page, and orders the caller's current stream after the upload.
     """
 
-    _CHUNK = 4 << 20
+    _CHUNK = 8 << 20   # a DMA is issued per staged chunk of a tensor
+    _PIECE = 1 << 20   # the least a staging thread copies
 
     def __init__(self, device, *, slots: int = 2, fetchers: int = 1, copy_threads: int = 4):
         self.device = torch.device(device)
@@ -263,9 +264,9 @@ class SnapshotUploader:
         return self._pool.submit(self._upload, fetched, dict(shapes), dtype)
 
     def _stage(self, dst: np.ndarray, src: np.ndarray) -> None:
-        """Copy into pinned memory in parallel chunks (numpy releases the GIL for the copies)."""
+        """Copy into pinned memory in parallel pieces (numpy releases the GIL for the copies)."""
         n = len(src)
-        pieces = min(self._copy_threads, max(1, n // self._CHUNK))
+        pieces = min(self._copy_threads, max(1, n // self._PIECE))
         if pieces == 1:
             np.copyto(dst, src)
             return
@@ -282,17 +283,23 @@ class SnapshotUploader:
         slot = self._slots[self._next]
         self._next = (self._next + 1) % len(self._slots)
         staging = slot.reserve(nbytes)
-        if nbytes:
-            self._stage(staging.numpy()[:nbytes], np.frombuffer(data, dtype=np.uint8, count=nbytes, offset=start))
         stream = ctypes.c_void_p(self.stream.cuda_stream)
         host = staging.data_ptr()
         with torch.cuda.device(self.device), torch.cuda.stream(self.stream):
-            # one DMA per tensor, each into its own allocation (aligned whatever the page's offsets)
-            raw = {}
-            for t in tensors:
-                raw[t.name] = torch.empty(t.shape, dtype=t.torch_dtype, device=self.device)
-                call("cs_copy_async", _hip.ptr(raw[t.name]), ctypes.c_void_p(host + t.begin),
-                     t.end - t.begin, _hip.COPY_H2D, stream)
+            # each tensor into its own allocation (aligned whatever the page's
+            # offsets); its bytes are staged chunk by chunk, and each chunk's DMA
+            # runs while the next chunk is copied into pinned memory
+            raw = {t.name: torch.empty(t.shape, dtype=t.torch_dtype, device=self.device) for t in tensors}
+            if nbytes:
+                src = np.frombuffer(data, dtype=np.uint8, count=nbytes, offset=start)
+                dst = staging.numpy()
+                for t in tensors:
+                    base = raw[t.name].data_ptr()
+                    for lo in range(t.begin, t.end, self._CHUNK):
+                        hi = min(lo + self._CHUNK, t.end)
+                        self._stage(dst[lo:hi], src[lo:hi])
+                        call("cs_copy_async", ctypes.c_void_p(base + lo - t.begin), ctypes.c_void_p(host + lo),
+                             hi - lo, _hip.COPY_H2D, stream)
             slot.event = torch.cuda.Event()
             slot.event.record(self.stream)
             flags = _hip.new_flags(self.device)
