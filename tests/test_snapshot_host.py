@@ -167,3 +167,63 @@ def test_runtime_schema():
     # float8 pages are floating point for the reference but have no device check here
     with pytest.raises(ValueError, match="not supported"):
         check_schema(page(k=ok, v=torch.zeros(2, 1, 4, dtype=torch.float8_e4m3fn)), shapes)
+
+
+from hypothesis import HealthCheck, given, settings  # noqa: E402
+from hypothesis import strategies as hst  # noqa: E402
+
+_FUZZ_DTYPES = [torch.float32, torch.bfloat16, torch.float16, torch.float64, torch.int32, torch.uint8]
+
+
+@hst.composite
+def mutated_pages(draw):
+    names = draw(hst.lists(hst.sampled_from(["k", "v", "hidden", "residual", "x"]), min_size=1, max_size=3,
+                           unique=True))
+    tensors = {}
+    for name in names:
+        dtype = draw(hst.sampled_from(_FUZZ_DTYPES))
+        shape = tuple(draw(hst.lists(hst.integers(0, 3), min_size=0, max_size=3)))
+        tensors[name] = torch.arange(math_prod(shape), dtype=torch.float64).reshape(shape).to(dtype)
+    page = bytearray(st_save(tensors))
+    kind = draw(hst.sampled_from(["flip", "truncate", "append", "digit", "none"]))
+    if kind == "flip":
+        at = draw(hst.integers(0, len(page) - 1))
+        page[at] ^= draw(hst.integers(1, 255))
+    elif kind == "truncate":
+        page = page[:draw(hst.integers(0, len(page) - 1))]
+    elif kind == "append":
+        page += bytes(draw(hst.integers(1, 9)))
+    elif kind == "digit":
+        header_end = 8 + int.from_bytes(page[:8], "little")
+        digits = [i for i in range(8, min(header_end, len(page))) if chr(page[i]).isdigit()]
+        if digits:
+            at = draw(hst.sampled_from(digits))
+            page[at] = ord(str((int(chr(page[at])) + draw(hst.integers(1, 9))) % 10))
+    return bytes(page)
+
+
+def math_prod(shape):
+    out = 1
+    for s in shape:
+        out *= s
+    return out
+
+
+@settings(max_examples=300, deadline=None, suppress_health_check=[HealthCheck.too_slow])
+@given(mutated_pages())
+def test_parse_accepts_exactly_what_safetensors_loads(page):
+    try:
+        loaded = st_load(page)
+    except Exception:
+        loaded = None
+    try:
+        tensors, start = parse_snapshot(page)
+    except ValueError:
+        tensors = None
+    assert (loaded is None) == (tensors is None)
+    if loaded is not None:
+        assert {t.name for t in tensors} == set(loaded)
+        for t in tensors:
+            assert t.torch_dtype == loaded[t.name].dtype and t.shape == tuple(loaded[t.name].shape)
+            assert page[start + t.begin:start + t.end] == loaded[t.name].contiguous().view(-1).view(
+                torch.uint8).numpy().tobytes()
