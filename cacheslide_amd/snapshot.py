@@ -415,6 +415,7 @@ class LayerSnapshots:
         self.layers, self.reuse, self.write_cache = layers, reuse, write_cache
         self.depth = prefetch_depth
         self.geometry = {"kv_heads": kv_heads, "head_dim": head_dim, "hidden_size": hidden_size}
+        self._owns_uploader = uploader is None
         self.uploader = uploader if uploader is not None else SnapshotUploader(device, fetchers=prefetch_depth)
         self._pending: dict[int, tuple[Future, torch.dtype]] = {}
         self.created_keys: list[str] = []
@@ -480,6 +481,18 @@ class LayerSnapshots:
             future = self.uploader.submit(lambda key=key: self.store.submit_load(key).result(),
                                           self._shapes(target, "kv"), dtype)
             self._pending[target] = (future, dtype)
+
+    def close(self) -> None:
+        """release(), then shut down the uploader when this object created it."""
+        self.release()
+        if self._owns_uploader:
+            self.uploader.close()
+
+    def __enter__(self) -> LayerSnapshots:
+        return self
+
+    def __exit__(self, *exc: object) -> None:
+        self.close()
 
     def release(self) -> None:
         """Drain pending prefetches before the request's pages may change (runtime.py:162-171)."""

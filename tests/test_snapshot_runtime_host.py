@@ -158,3 +158,23 @@ def test_prefetch_window(env):
     assert s._pending == {}
     with pytest.raises(ValueError):
         snapshots(env, prefetch_depth=0)
+
+
+def test_close_drains_and_closes_only_an_owned_uploader(env):
+    w = snapshots(env, write_cache=True)
+    w.put(0, "kv", kv(0))
+
+    class Owned(HostUploader):
+        closed = False
+
+        def close(self):
+            self.closed = True
+
+    shared = Owned()
+    with snapshots(env, uploader=shared) as s:
+        s.prefetch(0, torch.float32)
+    assert s.kv_future is None and shared.drained == 1 and not shared.closed
+    owned = snapshots(env)
+    owned._owns_uploader, owned.uploader = True, Owned()
+    owned.close()
+    assert owned.uploader.closed
