@@ -73,3 +73,12 @@ def test_snapshot_entry_points_check_arguments_without_a_device():
     strided.shape[0], strided.stride[0] = 4, 2
     assert lib.cs_snapshot_convert(ctypes.byref(strided), None, 1, ctypes.byref(flags), None) == _hip.CS_EINVAL
     assert b"contiguous" in lib.cs_last_error()
+
+
+def test_wca_update_checks_arguments_without_a_device():
+    lib = _hip.load()
+    assert lib.cs_wca_update(None, None) == _hip.CS_EINVAL
+    assert b"null" in lib.cs_last_error()
+    args = _hip.CsWcaUpdateArgs()          # no status block
+    assert lib.cs_wca_update(ctypes.byref(args), None) == _hip.CS_EINVAL
+    assert ctypes.sizeof(_hip.CsWcaUpdateArgs) == 888   # the C struct's size on x86-64
