@@ -90,7 +90,8 @@ enum cs_flag {
 /* Nonfinite scan of a floating view; ORs `bit` into *flags. */
 int cs_check_finite(const cs_view* x, int32_t bit, int32_t* flags, void* stream);
 
-/* int64 positions [n]: negative, duplicate and (keys only) not strictly
+/* The coordinate checks of cope_attention (position.py:127-137, 178-179):
+ * int64 positions [n]: negative, duplicate and (keys only) not strictly
  * increasing.  The quadratic duplicate scan runs only when the order check
  * found a descent.  Bits are the query or key variants selected by `is_key`;
  * bit 24 is used internally for query order. */
@@ -174,7 +175,8 @@ int cs_selected_visibility(const int64_t* queries, int64_t nq, const int64_t* ke
                            const int64_t* selected, int64_t nselected, uint8_t* out,
                            void* stream);
 
-/* out[i] = values[i] is in set[0..m) (torch.isin). */
+/* out[i] = values[i] is in set[0..m) (the torch.isin of
+ * SelectedAssociationPolicy, attention.py:60-72). */
 int cs_isin(const int64_t* values, int64_t n, const int64_t* set, int64_t m, uint8_t* out,
             void* stream);
 
@@ -218,7 +220,9 @@ int cs_ccpe_prefill_bf16(const void* q, int64_t q_s_batch, int64_t q_s_tok, int6
                          const float* e, int32_t max_positions, void* out, int32_t* flags,
                          void* stream);
 
-/* Decode (q = 1 row per request at position nk[b]-1) with speculative
+/* cope_attention for one query row per request (position.py:404-560 as the
+ * decode step calls it, runtime.py:600-609 over the paged.py:433-472 gather).
+ * Decode (q = 1 row per request at position nk[b]-1) with speculative
  * split-K: splits are aligned to the last key; a split whose right-hand gate
  * mass is below P-1 is recomputed exactly.  workspace must hold
  * cs_ccpe_decode_workspace_bytes(batch, hq, max_nk, split) bytes.
@@ -240,32 +244,41 @@ int cs_ccpe_decode_bf16(const void* q, int64_t q_s_batch, int64_t q_s_head, int3
 int cs_slot_scatter(const cs_view* cache, const cs_view* side_k, const cs_view* side_v,
                     const int64_t* slots, const int64_t* rows, int64_t n,
                     const cs_view* key, const cs_view* value, void* stream);
+/* NativePagedKV.gather (paged.py:433-472): key/value rows of slots, in order. */
 int cs_slot_gather(const cs_view* cache, const cs_view* side_k, const cs_view* side_v,
                    const int64_t* slots, const int64_t* rows, int64_t n,
                    cs_view* key, cs_view* value, void* stream);
 
-/* Relocation on a stacked cache [L, blocks, H, bs, 2D]: copy whole token
- * records (all layers, heads, K and V) from src_slots[i] to dst_slots[i].
+/* The copy-on-write moves of LayerSlotMap.promote_selected over all layers
+ * (slide.py:283-360).  Relocation on a stacked cache [L, blocks, H, bs, 2D]:
+ * copy whole token records (all layers, heads, K and V) from src_slots[i] to
+ * dst_slots[i].
  * Source and destination sets must be disjoint. */
 int cs_slot_copy(const cs_view* cache, const int64_t* src_slots, const int64_t* dst_slots,
                  int64_t n, void* stream);
-/* Whole-page copy on a stacked cache [L, blocks, H, bs, 2D]. */
+/* Whole-page copy on a stacked cache [L, blocks, H, bs, 2D] (the same moves
+ * when a chunk covers whole blocks, slide.py:283-360). */
 int cs_page_copy(const cs_view* cache, const int64_t* src_blocks, const int64_t* dst_blocks,
                  int64_t n, void* stream);
 
-/* Token -> slot maps (int64): map[tokens[i]] = slots[i]; out[i] = map[tokens[i]]. */
+/* Token -> slot maps (int64), LayerSlotMap's lookups and updates in bulk
+ * (slide.py:54-520): map[tokens[i]] = slots[i]; out[i] = map[tokens[i]]. */
 int cs_mapping_scatter(int64_t* map, int64_t map_len, const int64_t* tokens,
                        const int64_t* slots, int64_t n, void* stream);
+/* the lookup half, out[i] = map[tokens[i]]: pinned_mapping and the source
+ * slots of promote_selected (slide.py:175-192, 264-270) */
 int cs_mapping_gather(const int64_t* map, int64_t map_len, const int64_t* tokens,
                       int64_t* out, int64_t n, void* stream);
 
-/* Free-slot bitmap (bit set = free), nbits slots in ceil(nbits/32) words.
+/* LayerSlotMap's free-slot order (slide.py:103-112) as a bitmap.
+ * Free-slot bitmap (bit set = free), nbits slots in ceil(nbits/32) words.
  * release: set bits of slots[0..n).  acquire: take the `count` lowest free
  * slots in ascending order (LayerSlotMap._fresh_slot order), clear them and
  * write them to out; if fewer than count are free nothing changes and
  * *status_out = CS_ECAPACITY (device int32). */
 int cs_freelist_release(uint32_t* bitmap, int64_t nbits, const int64_t* slots, int64_t n,
                         void* stream);
+/* _fresh_slot, count at a time (slide.py:103-112) */
 int cs_freelist_acquire(uint32_t* bitmap, int64_t nbits, int64_t count, int64_t* out,
                         int32_t* status_out, void* stream);
 
@@ -281,7 +294,8 @@ int cs_freelist_acquire(uint32_t* bitmap, int64_t nbits, int64_t count, int64_t*
 int cs_wca_score(const cs_view* old_rows_src, const int64_t* old_rows, const cs_view* fresh,
                  double* err, double* norm, int32_t* flags, void* stream);
 
-/* alpha = err / (norm + eps), optionally clamped to [0, 1]; ORs 2 into *flags
+/* adaptation_weight (wca.py:65-93): alpha = err / (norm + eps), optionally
+ * clamped to [0, 1]; ORs 2 into *flags
  * when err or norm + eps is nonfinite and 4 when the quotient is nonfinite. */
 int cs_wca_alpha(const double* err, const double* norm, int64_t n, double eps, int32_t clamp,
                  double* alpha, int32_t* flags, void* stream);
@@ -310,7 +324,8 @@ int cs_mask_nonzero(const uint8_t* a, const uint8_t* b, int64_t n, int64_t* out,
 int cs_wca_same_rows(const int64_t* a, const int64_t* b, int64_t n, int32_t bit, int32_t* flags,
                      void* stream);
 
-/* fused = w * new + (1 - w) * old in fp64 (no contraction), stored in the
+/* The blend of WCAState.update (wca.py:266-276):
+ * fused = w * new + (1 - w) * old in fp64 (no contraction), stored in the
  * cache dtype (fp64 -> fp32 -> 16-bit, as torch converts); w = 1 where
  * mandatory[i].  rows [a] index old (NULL = identity); fused_k/v [a,H,D].
  * ORs 8 into *flags when a fused value is nonfinite in the cache dtype. */
