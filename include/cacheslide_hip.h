@@ -229,6 +229,7 @@ int cs_ccpe_prefill_bf16(const void* q, int64_t q_s_batch, int64_t q_s_tok, int6
  *   q [B, Hq, 128] bf16 (q_s_batch, q_s_head), out [B, Hq, 128] bf16. */
 int64_t cs_ccpe_decode_workspace_bytes(int32_t batch, int32_t hq, int32_t max_nk,
                                        int32_t split);
+/* the decode step itself: cope_attention at one query row (position.py:404-560) */
 int cs_ccpe_decode_bf16(const void* q, int64_t q_s_batch, int64_t q_s_head, int32_t batch,
                         int32_t hq, int32_t hkv, const int32_t* nk, int32_t max_nk,
                         const cs_kv_source* kv, const float* e, int32_t max_positions,
