@@ -15,6 +15,13 @@ Modules:
             (paged.py, slide.py)
   rows   -- the selective prefill's row bookkeeping (runtime.py)
 
+The layer snapshot pages (runtime.py:192-256) have no restatement here: their
+codec is the reference's own dependency, safetensors==0.8.0
+(constraints/cpu-tests.txt:4), which is installed and is itself the checker
+(tests/test_snapshot_host.py); the page store's file format is pinned by known
+answers (sha256 of known payloads, hand-written page files) in
+tests/test_storage_host.py.
+
 Pinning: every function is checked in tests/test_oracle.py against the
 reference's own closed-form test vectors (tests/test_position.py,
 test_attention_policies.py, test_wca.py, test_slide.py, test_paged.py), against
