@@ -602,3 +602,49 @@ def test_decode_unsaturated_splits_are_recomputed(device):
     assert p.max() < 63  # never saturated: the fixup path is exercised
     expected = orc.cope_attention(acc_np(qq), acc_np(keys[0]), acc_np(vals[0]), e.numpy(), np.array([n - 1]))
     assert_close_bf16(out, expected)
+
+
+@pytest.mark.parametrize("hq, hkv, bs", [(4, 4, 16), (8, 4, 32), (16, 2, 64), (32, 1, 16)])
+def test_paged_prefill_group_and_block_sizes(device, hq, hkv, bs):
+    """GQA groups 1, 2, 8 and 32 over block sizes 16-64, every row causal."""
+    lens = [150, 520]
+    nb, table, rows = paged_layout(lens, hkv, bs, 128, seed=hq + bs)
+    cache = seeded((nb, hkv, bs, 256), 150 + hq, dtype=torch.bfloat16)
+    keys = [seeded((n, hkv, 128), 160 + i + hq, dtype=torch.bfloat16) for i, n in enumerate(lens)]
+    vals = [seeded((n, hkv, 128), 170 + i + hq, dtype=torch.bfloat16) for i, n in enumerate(lens)]
+    fill_paged(cache, rows, keys, vals)
+    e = seeded((128, 64), 180 + bs, scale=0.02)
+    nq = 48
+    qs = seeded((len(lens), nq, hq, 128), 181 + hq, dtype=torch.bfloat16)
+    gen = np.random.default_rng(hq * 100 + bs)
+    qpos = np.stack([np.sort(gen.choice(n, nq, replace=False)) for n in lens]).astype(np.int64)
+    cope = cope_on(device, 128, 64, table=e)
+    out = ccpe_prefill_paged(qs.to(device), cache.to(device), table.to(device),
+                             torch.tensor(lens, dtype=torch.int32, device=device), cope,
+                             torch.from_numpy(qpos).to(device))
+    for b in range(len(lens)):
+        expected = np.concatenate([
+            orc.cope_attention(acc_np(qs[b, r:r + 1]), acc_np(keys[b]), acc_np(vals[b]), e.numpy(),
+                               qpos[b, r:r + 1])
+            for r in range(nq)], axis=0)
+        assert_close_bf16(out[b], expected)
+
+
+@pytest.mark.parametrize("hq, hkv, bs, split", [(4, 4, 16, 1024), (32, 8, 32, 1024), (64, 8, 64, 256)])
+def test_decode_group_and_block_sizes(device, hq, hkv, bs, split):
+    """GQA groups 1, 4 and 8 over block sizes 16-64, the default split included."""
+    lens = [5, 1100, 2600]
+    nb, table, rows = paged_layout(lens, hkv, bs, 128, seed=hq + split)
+    cache = seeded((nb, hkv, bs, 256), 250 + hq, dtype=torch.bfloat16)
+    keys = [seeded((n, hkv, 128), 260 + i + hq, dtype=torch.bfloat16) for i, n in enumerate(lens)]
+    vals = [seeded((n, hkv, 128), 270 + i + hq, dtype=torch.bfloat16) for i, n in enumerate(lens)]
+    fill_paged(cache, rows, keys, vals)
+    e = seeded((128, 64), 280 + bs, scale=0.02)
+    q = seeded((len(lens), hq, 128), 283 + hq, dtype=torch.bfloat16)
+    cope = cope_on(device, 128, 64, table=e)
+    out = ccpe_decode_paged(q.to(device), cache.to(device), table.to(device),
+                            torch.tensor(lens, dtype=torch.int32, device=device), cope, split=split)
+    for b, n in enumerate(lens):
+        expected = orc.cope_attention(acc_np(q[b:b + 1]), acc_np(keys[b]), acc_np(vals[b]), e.numpy(),
+                                      np.array([n - 1]))
+        assert_close_bf16(out[b:b + 1], expected)
