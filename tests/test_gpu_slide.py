@@ -241,3 +241,30 @@ def test_bf16_arena_round_trip_bit_exact(device):
     expect_k[sel], expect_v[sel] = newk, newv
     np.testing.assert_array_equal(bits(gk), bits(expect_k))
     np.testing.assert_array_equal(bits(gv), bits(expect_v))
+
+
+@pytest.mark.parametrize("layers, blocks, heads, bs, d, dtype", [
+    (2, 64, 8, 16, 128, torch.bfloat16),
+    (1, 100, 1, 8, 64, torch.float32),
+    (4, 50, 4, 32, 32, torch.float16),
+])
+def test_relocation_random_geometry_bit_exact(device, layers, blocks, heads, bs, d, dtype):
+    gen = torch.Generator().manual_seed(blocks + heads)
+    cache_cpu = torch.randn((layers, blocks, heads, bs, 2 * d), generator=gen, dtype=torch.float64).to(dtype)
+    ref = bits(cache_cpu).copy()
+    cache = cache_cpu.to(device)
+    perm = torch.randperm(blocks, generator=gen).tolist()
+    q = blocks // 4
+    src_b, dst_b = perm[:q], perm[q:2 * q]                                   # disjoint block sets
+    orc.page_copy(ref, src_b, dst_b)
+    relocate.copy_pages(cache, torch.tensor(src_b, device=device), torch.tensor(dst_b, device=device))
+    # slots inside the untouched blocks, disjoint sources and destinations
+    rest = perm[2 * q:]
+    slots = [blk * bs + off for blk in rest for off in range(bs)]
+    order = torch.randperm(len(slots), generator=gen).tolist()
+    k = min(40, len(slots) // 2)
+    src_s = [slots[i] for i in order[:k]]
+    dst_s = [slots[i] for i in order[k:2 * k]]
+    orc.slot_copy(ref, src_s, dst_s)
+    relocate.copy_slots(cache, torch.tensor(src_s, device=device), torch.tensor(dst_s, device=device))
+    np.testing.assert_array_equal(bits(cache), ref)
