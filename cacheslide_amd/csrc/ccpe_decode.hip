@@ -645,12 +645,17 @@ __global__ void __launch_bounds__(kPlanThreads) decode_plan_kernel(decode_params
   for (int base = 0; base < splits; base += kPlanThreads) {
     const int r = base + tid;
     bool need = false;
+    // all heads' totals are loaded before the first carry store: tot and carry
+    // may alias as far as the compiler knows, so it would not hoist them itself
+    double v[kMaxGroup];
+#pragma unroll
+    for (int h = 0; h < kMaxGroup; ++h)
+      v[h] = (h < G && r < splits) ? p.tot[ws_index(p, b, h0 + h, r)] : 0.0;
 #pragma unroll
     for (int h = 0; h < kMaxGroup; ++h) {
       if (h >= G) continue;
       const int64_t wi = ws_index(p, b, h0 + h, r < splits ? r : 0);
-      const double v = r < splits ? p.tot[wi] : 0.0;
-      double x = v;  // inclusive scan within the wave
+      double x = v[h];  // inclusive scan within the wave
 #pragma unroll
       for (int off = 1; off < 64; off <<= 1) {
         const double y = __shfl_up(x, off, 64);
@@ -710,8 +715,14 @@ __global__ void __launch_bounds__(kD) decode_combine_kernel(decode_params p) {
   int splits = (nk + p.split - 1) / p.split;
   if (splits > p.smax) splits = p.smax;
   const int64_t w0 = ws_index(p, b, h, 0);
-  float M = -INFINITY;
-  for (int r = d; r < splits; r += kD) M = fmaxf(M, p.mx[w0 + r]);
+  // the first 128 splits' max and sum stay in registers for the weights below
+  float m_first = -INFINITY, l_first = 0.f;
+  if (d < splits) {
+    m_first = p.mx[w0 + d];
+    l_first = p.sm[w0 + d];
+  }
+  float M = m_first;
+  for (int r = d + kD; r < splits; r += kD) M = fmaxf(M, p.mx[w0 + r]);
   M = wave_max(M);
   if (lane == 0) red[wave] = M;
   __syncthreads();
@@ -722,15 +733,26 @@ __global__ void __launch_bounds__(kD) decode_combine_kernel(decode_params p) {
     const int r = base + d;
     float f = 0.f;
     if (r < splits) {
-      const float m = p.mx[w0 + r];
+      const float m = base == 0 ? m_first : p.mx[w0 + r];
+      const float l = base == 0 ? l_first : p.sm[w0 + r];
       f = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
-      L += p.sm[w0 + r] * f;
+      L += l * f;
     }
     wgt[d] = f;
     __syncthreads();
     const int n = splits - base < kD ? splits - base : kD;
     const float* acc = p.acc + (w0 + base) * kD + d;
     int i = 0;
+    // 16 partials in flight per thread: the merge is bound by load latency
+    for (; i + 16 <= n; i += 16) {
+      float a[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) a[j] = acc[(i + j) * kD];
+#pragma unroll
+      for (int j = 0; j < 16; j += 4)
+        O += wgt[i + j] * a[j] + wgt[i + j + 1] * a[j + 1] + wgt[i + j + 2] * a[j + 2] +
+             wgt[i + j + 3] * a[j + 3];
+    }
     for (; i + 4 <= n; i += 4) {
       const float a0 = acc[(i + 0) * kD], a1 = acc[(i + 1) * kD];
       const float a2 = acc[(i + 2) * kD], a3 = acc[(i + 3) * kD];
