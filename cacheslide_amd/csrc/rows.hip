@@ -236,6 +236,9 @@ extern "C" int cs_rows_remap(const cs_view* hidden_in, const cs_view* residual_i
   const int64_t width = hidden_in->shape[1];
   const int es = dtype_size(hidden_in->dtype);
   CS_REQUIRE(es > 0, "unknown dtype");
+  // no active rows: nothing is read or written, and empty outputs have no data
+  // pointer, so the views below would read as absent
+  if (n_active == 0) return CS_OK;
   rows2 hi, ri, sh, sr, ho, ro;
   int st;
   if ((st = row_view(hidden_in, width, es, "hidden", &hi, false))) return st;
@@ -251,7 +254,7 @@ extern "C" int cs_rows_remap(const cs_view* hidden_in, const cs_view* residual_i
   CS_REQUIRE(!sr.base || sr.n_rows >= sh.n_rows, "snapshot residual has fewer rows");
   if (ri.base && sh.base) CS_REQUIRE(sr.base != nullptr, "the snapshot needs residual rows too");
   hipStream_t s = as_stream(stream);
-  if (n_active == 0 || width == 0) return CS_OK;  // nothing to move (and nothing to look up)
+  if (width == 0) return CS_OK;  // nothing to move
   const int64_t row_bytes = width * es;
   const int w = pick_word(row_bytes, {&hi, &ri, &sh, &sr, &ho, &ro});
   CS_ROWS_DISPATCH(w, rows_remap_kernel, row_grid(n_active), s, hi, ri, sh, sr, ho, ro, previous, n_prev,
@@ -280,7 +283,8 @@ extern "C" int cs_rows_scatter(const cs_view* rows, const int64_t* tokens, int64
   CS_REQUIRE(es > 0, "unknown dtype");
   rows2 src, dst;
   int st;
-  if ((st = row_view(rows, width, es, "rows", &src, false))) return st;
+  // no tokens: the rows are never read (and an empty tensor has no data pointer)
+  if ((st = row_view(rows, width, es, "rows", &src, m == 0))) return st;
   if ((st = row_view(out, width, es, "out", &dst, false))) return st;
   CS_REQUIRE(src.n_rows >= m, "fewer rows than tokens");
   hipStream_t s = as_stream(stream);
@@ -303,8 +307,9 @@ extern "C" int cs_rows_gather(const cs_view* src, const int64_t* idx, int64_t m,
   CS_REQUIRE(es > 0, "unknown dtype");
   rows2 a, b;
   int st;
-  if ((st = row_view(src, width, es, "src", &a, false))) return st;
-  if ((st = row_view(out, width, es, "out", &b, false))) return st;
+  // no indices: nothing is read or written (an empty tensor has no data pointer)
+  if ((st = row_view(src, width, es, "src", &a, m == 0))) return st;
+  if ((st = row_view(out, width, es, "out", &b, m == 0))) return st;
   CS_REQUIRE(b.n_rows >= m, "fewer out rows than indices");
   if (m == 0 || width == 0) return CS_OK;
   const int64_t row_bytes = width * es;

@@ -132,3 +132,53 @@ def test_scatter_and_gather_rows(device, dtype, width):
         scatter_rows(rows.to(device), torch.from_numpy(tokens), int(tokens[-1]))
     with pytest.raises(ValueError, match="ascending and distinct"):
         scatter_rows(rows.to(device), torch.from_numpy(tokens[::-1].copy()), 500)
+
+
+def test_layer_chain_at_bench_size(device):
+    """Four layers of a 16384-token prompt, hidden 4096 bf16, 90% fixed tokens:
+    each layer's active set is the dynamic tokens plus a fresh 15% draw of the
+    fixed ones, so every layer both keeps and restores rows."""
+    n, width = 16384, 4096
+    rng = np.random.default_rng(16384)
+    fixed = np.sort(rng.choice(n, n * 9 // 10, replace=False))
+    dynamic = np.setdiff1d(np.arange(n), fixed)
+    gen = torch.Generator().manual_seed(16384)
+    snap_h = random_rows(len(fixed), width, torch.bfloat16, gen)
+    snap_r = random_rows(len(fixed), width, torch.bfloat16, gen)
+    snap = {"hidden": snap_h.to(device), "residual": snap_r.to(device)}
+    previous = np.sort(np.concatenate([dynamic, rng.choice(fixed, len(fixed) * 15 // 100, replace=False)]))
+    hidden_bits = bits(random_rows(len(previous), width, torch.bfloat16, gen))
+    residual_bits = bits(random_rows(len(previous), width, torch.bfloat16, gen))
+    hidden = torch.from_numpy(hidden_bits).view(torch.bfloat16).to(device)
+    residual = torch.from_numpy(residual_bits).view(torch.bfloat16).to(device)
+    for layer in range(4):
+        active = np.sort(np.concatenate([dynamic, rng.choice(fixed, len(fixed) * 15 // 100, replace=False)]))
+        want_h, want_r, want_n = orc.next_layer_rows(hidden_bits, residual_bits, previous, active, fixed,
+                                                     bits(snap_h), bits(snap_r), n)
+        got = next_layer_rows(hidden, residual, torch.from_numpy(previous), torch.from_numpy(active),
+                              torch.from_numpy(fixed), snap)
+        np.testing.assert_array_equal(bits(got.hidden), want_h, err_msg=f"layer {layer}")
+        np.testing.assert_array_equal(bits(got.residual), want_r, err_msg=f"layer {layer}")
+        assert int(got.restored.item()) == want_n > 0
+        previous, hidden, residual, hidden_bits, residual_bits = active, got.hidden, got.residual, want_h, want_r
+    full = scatter_rows(hidden, torch.from_numpy(previous), n)
+    np.testing.assert_array_equal(bits(full), orc.scatter_rows(hidden_bits, previous, n))
+    # gather(scatter(rows)) is the rows again
+    np.testing.assert_array_equal(bits(gather_rows(full, torch.from_numpy(previous))), hidden_bits)
+
+
+def test_empty_active_list(device):
+    fixed, previous, _ = case(2)
+    hidden = torch.randn(len(previous), 8, device=device)
+    empty = torch.zeros(0, dtype=torch.long)
+    got = next_layer_rows(hidden, hidden.clone(), torch.from_numpy(previous), empty, torch.from_numpy(fixed),
+                          {"hidden": torch.randn(len(fixed), 8, device=device),
+                           "residual": torch.randn(len(fixed), 8, device=device)})
+    assert got.hidden.shape == (0, 8) and got.residual.shape == (0, 8) and int(got.restored.item()) == 0
+    assert scatter_rows(got.hidden, empty, 300).abs().sum().item() == 0
+    assert gather_rows(got.hidden, empty).shape == (0, 8)
+    # every active token restored from the snapshot: no previous rows at all
+    fixed_t = torch.from_numpy(fixed)
+    snap = {"hidden": torch.randn(len(fixed), 8, device=device)}
+    only = next_layer_rows(snap["hidden"][:3], None, fixed_t[:3], fixed_t[:5], fixed_t, snap)
+    assert torch.equal(only.hidden, snap["hidden"][:5]) and int(only.restored.item()) == 2
