@@ -268,3 +268,23 @@ def test_relocation_random_geometry_bit_exact(device, layers, blocks, heads, bs,
     orc.slot_copy(ref, src_s, dst_s)
     relocate.copy_slots(cache, torch.tensor(src_s, device=device), torch.tensor(dst_s, device=device))
     np.testing.assert_array_equal(bits(cache), ref)
+
+
+def test_empty_moves_leave_the_cache_alone(device):
+    cache = random_bf16((2, 6, 2, 4, 16), 3).to(device)
+    before = bits(cache).copy()
+    empty = torch.zeros(0, dtype=torch.long, device=device)
+    relocate.copy_pages(cache, empty, empty)
+    relocate.copy_slots(cache, empty, empty)
+    mapping = torch.arange(10, dtype=torch.long, device=device)
+    relocate.scatter_mapping(mapping, empty, empty)
+    assert relocate.gather_mapping(mapping, empty).shape == (0,)
+    from cacheslide_amd.paged import HipSlotMover
+
+    layer = cache[0]
+    kv = torch.zeros((0, 2, 8), dtype=torch.bfloat16, device=device)
+    HipSlotMover().scatter(layer, None, None, [], kv, kv)
+    HipSlotMover().gather(layer, None, None, [], kv, kv)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(bits(cache), before)
+    assert torch.equal(mapping.cpu(), torch.arange(10))
