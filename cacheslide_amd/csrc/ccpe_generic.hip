@@ -655,8 +655,11 @@ using namespace cs;
 extern "C" int cs_ccpe_attention(const cs_ccpe_args* a, void* stream) {
   CS_REQUIRE(a != nullptr, "null arguments");
   const cs_view &q = a->q, &k = a->k, &v = a->v, &e = a->e;
-  CS_REQUIRE(q.data && k.data && v.data && e.data, "q, k, v and e are required");
   CS_REQUIRE(q.ndim == 3 && k.ndim == 3 && v.ndim == 3 && e.ndim == 2, "q/k/v must be 3-d, e 2-d");
+  // zero query tokens is a valid call with an empty result (position.py:117-150
+  // asks for one key, not one query); empty tensors carry no data pointer
+  const bool no_queries = q.shape[0] == 0;
+  CS_REQUIRE((q.data || no_queries) && k.data && v.data && e.data, "q, k, v and e are required");
   CS_REQUIRE(q.dtype == k.dtype && k.dtype == v.dtype && is_float_dtype(q.dtype),
              "q, k, v must share a float dtype");
   const int64_t nq = q.shape[0], hq = q.shape[1], d = q.shape[2];
@@ -664,7 +667,7 @@ extern "C" int cs_ccpe_attention(const cs_ccpe_args* a, void* stream) {
   CS_REQUIRE(k.shape[2] == d && v.shape[0] == nk && v.shape[1] == hkv && hkv > 0 && hq % hkv == 0,
              "inconsistent q/k/v shapes");
   CS_REQUIRE(e.shape[0] == d && e.shape[1] >= 2 && is_float_dtype(e.dtype), "e must be [D, P]");
-  CS_REQUIRE(a->qpos && a->kpos && a->flags, "positions and flags are required");
+  CS_REQUIRE((a->qpos || no_queries) && a->kpos && a->flags, "positions and flags are required");
   CS_REQUIRE(dv <= 64 * kMaxDvChunks, "value head dim %lld exceeds %d", (long long)dv,
              64 * kMaxDvChunks);
   const int64_t npos = e.shape[1];

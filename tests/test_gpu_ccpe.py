@@ -648,3 +648,13 @@ def test_decode_group_and_block_sizes(device, hq, hkv, bs, split):
         expected = orc.cope_attention(acc_np(q[b:b + 1]), acc_np(keys[b]), acc_np(vals[b]), e.numpy(),
                                       np.array([n - 1]))
         assert_close_bf16(out[b:b + 1], expected)
+
+
+def test_zero_query_tokens_give_an_empty_result(device):
+    # position.py:117-150 requires one key and one head, not one query token
+    cope = CoPE(16, 8, device=device)
+    q = torch.zeros((0, 4, 16), device=device)
+    k = torch.randn((5, 2, 16), device=device)
+    v = torch.randn((5, 2, 16), device=device)
+    out = cope_attention(q, k, v, cope, torch.zeros(0, dtype=torch.long, device=device))
+    assert out.shape == (0, 4, 16)
