@@ -205,7 +205,7 @@ def decode_measure(device, steps: int, warmup: int):
     lib = _hip.load()
     e = cope.position_embeddings.detach()
     args = (_hip.ptr(q), q.stride(0), q.stride(1), B, HQ, HKV, _hip.ptr(nk), CTX, src, _hip.ptr(e), P,
-            SPLIT, _hip.ptr(ws), _hip.ptr(out), _hip.ptr(flags), _hip.stream_of(device))
+            SPLIT, _hip.ptr(ws), ws.numel(), _hip.ptr(out), _hip.ptr(flags), _hip.stream_of(device))
 
     def step():
         status = lib.cs_ccpe_decode_bf16(*args)
@@ -280,8 +280,8 @@ def slide_measure(device, steps: int, layers: int = 32) -> dict:
     src_slots = dev((np.repeat(src_blk, BS) * BS + np.tile(np.arange(BS), need)).tolist())
 
     def step():
-        relocate.copy_pages(cache, fs, fd)
-        relocate.copy_slots(cache, ps, pd)
+        relocate.copy_pages(cache, fs, fd, check=False)  # disjoint by construction (two halves of one permutation)
+        relocate.copy_slots(cache, ps, pd, check=False)
         relocate.scatter_mapping(mapping, tokens, slots)
         relocate.gather_mapping(mapping, tokens)
         free.release(src_slots)

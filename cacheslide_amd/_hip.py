@@ -32,6 +32,8 @@ FLAG_SCORE_NONFINITE = 1 << 10
 FLAG_E_NONFINITE = 1 << 11
 FLAG_POS_NONFINITE = 1 << 12
 FLAG_BLOCK_INVALID = 1 << 13
+FLAG_NO_KEY = 1 << 14
+FLAG_CONTEXT_RANGE = 1 << 15
 FLAG_PATH_NEGATIVE = 1 << 16
 FLAG_PATH_AVAILABLE = 1 << 17
 FLAG_PATH_INCREASING = 1 << 18
@@ -128,6 +130,13 @@ class CsKvSource(ctypes.Structure):
         ("v_s_batch", ctypes.c_int64),
         ("v_s_tok", ctypes.c_int64),
         ("v_s_head", ctypes.c_int64),
+        ("slots", ctypes.c_void_p),
+        ("slots_stride", ctypes.c_int64),
+        ("side_k", ctypes.c_void_p),
+        ("side_v", ctypes.c_void_p),
+        ("side_s_row", ctypes.c_int64),
+        ("side_s_head", ctypes.c_int64),
+        ("side_rows", ctypes.c_int64),
     ]
 
 
@@ -160,7 +169,7 @@ SIGNATURES = {
     "cs_ccpe_decode_bf16": (
         _I32,
         [_P, _I64, _I64, _I32, _I32, _I32, _P, _I32, ctypes.POINTER(CsKvSource), _P,
-         _I32, _I32, _P, _P, _P, _P],
+         _I32, _I32, _P, _I64, _P, _P, _P],
     ),
     "cs_slot_scatter": (_I32, [_VP, _VP, _VP, _P, _P, _I64, _VP, _VP, _P]),
     "cs_slot_gather": (_I32, [_VP, _VP, _VP, _P, _P, _I64, _VP, _VP, _P]),

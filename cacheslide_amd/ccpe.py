@@ -1,11 +1,20 @@
 """Fused CCPE attention over the paged KV cache (bf16, head dim 128).
 
 These entry points read K and V straight from the vLLM-layout paged cache
-[blocks, kv_heads, block_size, 2 * 128] through a block table, instead of
-first materialising the logical K/V with ``NativePagedKV.gather``
-(src/cacheslide_vllm/runtime.py:573 and :505-507 followed by
-position.py:404-560).  Results equal ``cope_attention`` on the gathered K/V
-with default key positions 0..nk-1, within the bf16 tolerance.
+[blocks, kv_heads, block_size, 2 * 128] instead of first materialising the
+logical K/V with ``NativePagedKV.gather`` (src/cacheslide_vllm/runtime.py:
+499-507 and :573, followed by position.py:404-560), with default key
+positions 0..nk-1.  Key j of a request is addressed either
+
+* through a block table, at its canonical slot ``table[j // bs] * bs + j % bs``
+  (paged.py:146-151) -- what a vLLM block table names; or
+* through a per-token slot map -- the slot ``NativePagedKV.gather`` reads for
+  token j, native or sidecar (paged.py:433-472).  After SLIDE relocation and
+  decode hole reuse the canonical slot of a selected token may hold a decode
+  token's K/V and the token itself lives in the sidecar (paged.py:474-524,
+  slide.py:401-459), so only this form equals ``gather`` + ``cope_attention``
+  on such an arena.  ``ccpe_decode_arena`` / ``ccpe_prefill_arena`` take the map
+  from a ``NativePagedKV`` under the same pins ``gather`` takes.
 
 * ``ccpe_prefill_paged``: many query rows per request (MFMA kernel).
 * ``ccpe_decode_paged``: one new row per request at position nk-1 (split-K
@@ -32,24 +41,66 @@ def _check_e(cope, device, max_positions: int = 256) -> Tensor:
     return e
 
 
-def _paged_source(cache: Tensor, block_table: Tensor) -> _hip.CsKvSource:
+def _cache_source(cache: Tensor) -> _hip.CsKvSource:
     if cache.ndim != 4 or cache.dtype != torch.bfloat16 or cache.shape[3] != 256:
         raise ValueError("cache must be bf16 [blocks, kv_heads, block_size, 256]")
     if cache.stride(3) != 1:
         raise ValueError("cache records must be contiguous in the last dimension")
-    if block_table.ndim != 2 or block_table.dtype != torch.int32:
-        raise ValueError("block_table must be int32 [batch, max_blocks]")
     src = _hip.CsKvSource()
     src.cache = cache.data_ptr()
     src.s_block, src.s_head, src.s_offset = cache.stride(0), cache.stride(1), cache.stride(2)
     src.block_size = cache.shape[2]
     src.num_blocks = cache.shape[0]
+    return src
+
+
+def _paged_source(cache: Tensor, block_table: Tensor) -> _hip.CsKvSource:
+    src = _cache_source(cache)
+    if block_table.ndim != 2 or block_table.dtype != torch.int32:
+        raise ValueError("block_table must be int32 [batch, max_blocks]")
+    if block_table.stride(1) != 1:
+        raise ValueError("block_table rows must be contiguous")
     src.block_table = block_table.data_ptr()
     src.bt_stride = block_table.stride(0)
     src.bt_cols = block_table.shape[1]
-    if block_table.stride(1) != 1:
-        raise ValueError("block_table rows must be contiguous")
     return src
+
+
+def _slot_source(cache: Tensor, slots: Tensor, side_k: Tensor | None,
+                 side_v: Tensor | None) -> _hip.CsKvSource:
+    """Per-token slot map [B, >= nk] int64; slots past the native pool name sidecar rows."""
+    src = _cache_source(cache)
+    if slots.ndim != 2 or slots.dtype != torch.long or slots.stride(1) != 1:
+        raise ValueError("slots must be int64 [batch, tokens] with contiguous rows")
+    src.slots = slots.data_ptr()
+    src.slots_stride = slots.stride(0)
+    if (side_k is None) != (side_v is None):
+        raise ValueError("side_k and side_v go together")
+    if side_k is not None:
+        for side in (side_k, side_v):
+            if (side.ndim != 3 or side.dtype != torch.bfloat16 or side.shape[1:] != (cache.shape[1], 128)
+                    or side.stride(2) != 1 or side.device != cache.device):
+                raise ValueError("sidecar must be bf16 [rows, kv_heads, 128] on the cache device")
+        if side_k.shape != side_v.shape or side_k.stride() != side_v.stride():
+            raise ValueError("side_k and side_v must share shape and strides")
+        if side_k.shape[0]:
+            src.side_k, src.side_v = side_k.data_ptr(), side_v.data_ptr()
+            src.side_s_row, src.side_s_head = side_k.stride(0), side_k.stride(1)
+            src.side_rows = side_k.shape[0]
+    return src
+
+
+def _kv_source(cache: Tensor, block_table: Tensor | None, slots: Tensor | None,
+               side_k: Tensor | None, side_v: Tensor | None) -> _hip.CsKvSource:
+    if slots is not None:
+        if block_table is not None:
+            raise ValueError("give either block_table or slots, not both")
+        return _slot_source(cache, slots, side_k, side_v)
+    if block_table is None:
+        raise ValueError("block_table or slots is required")
+    if side_k is not None or side_v is not None:
+        raise ValueError("sidecar rows are addressed through slots only")
+    return _paged_source(cache, block_table)
 
 
 def _prefill_dense(query: Tensor, key: Tensor, value: Tensor, e: Tensor,
@@ -78,22 +129,27 @@ def _prefill_dense(query: Tensor, key: Tensor, value: Tensor, e: Tensor,
 def ccpe_prefill_paged(
     query: Tensor,
     cache: Tensor,
-    block_table: Tensor,
+    block_table: Tensor | None,
     context_lens: Tensor,
     cope,
     query_positions: Tensor,
     *,
+    slots: Tensor | None = None,
+    side_k: Tensor | None = None,
+    side_v: Tensor | None = None,
     check: bool = True,
 ) -> Tensor:
     """Batched CCPE prefill over the paged cache.
 
-    query [B, nq, Hq, 128] bf16; cache bf16 [blocks, Hkv, bs, 256];
-    block_table int32 [B, max_blocks]; context_lens int32 [B] (keys 0..n-1 of
-    request b live at block_table[b, j // bs], offset j % bs);
-    query_positions int64 [B, nq].  Returns [B, nq, Hq, 128] bf16.
-    With ``check`` the nonfinite / invalid-block flags are read back (one sync).
+    query [B, nq, Hq, 128] bf16; cache bf16 [blocks, Hkv, bs, 256]; keys
+    0..n-1 of request b (n = context_lens[b], int32 [B]) come through
+    ``block_table`` (int32 [B, max_blocks]: block table[b, j // bs], offset
+    j % bs) or through ``slots`` (int64 [B, >= n]: native slots and rows of
+    ``side_k`` / ``side_v``); query_positions int64 [B, nq].  Returns
+    [B, nq, Hq, 128] bf16.  With ``check`` the invalid-block flag is read back
+    (one sync).
     """
-    device = _hip.require_device(query, cache, block_table, context_lens, query_positions)
+    device = _hip.require_device(query, cache, context_lens, query_positions, block_table, slots)
     if query.ndim != 4 or query.dtype != torch.bfloat16 or query.shape[3] != 128 or query.stride(3) != 1:
         raise ValueError("query must be bf16 [batch, rows, heads, 128] with contiguous rows")
     b, nq, hq = query.shape[0], query.shape[1], query.shape[2]
@@ -104,8 +160,10 @@ def ccpe_prefill_paged(
         raise ValueError("context_lens must be int32 [batch]")
     if query_positions.shape != (b, nq) or query_positions.dtype != torch.long or query_positions.stride(1) != 1:
         raise ValueError("query_positions must be int64 [batch, rows]")
+    if slots is not None and slots.shape[0] != b:
+        raise ValueError("slots must have one row per request")
     e = _check_e(cope, device, max_positions=128)
-    src = _paged_source(cache, block_table)
+    src = _kv_source(cache, block_table, slots, side_k, side_v)
     flags = _hip.new_flags(device)
     out = torch.empty((b, nq, hq, 128), dtype=torch.bfloat16, device=device)
     call(
@@ -118,18 +176,43 @@ def ccpe_prefill_paged(
     return out
 
 
+def ccpe_prefill_arena(query: Tensor, arena, cope, query_positions: Tensor, *,
+                       check: bool = True) -> Tensor:
+    """``cope_attention(query, *arena.gather(range(n)), cope, query_positions)``
+    for one request's arena (runtime.py:571-573 without policies), fused: the
+    kernel reads the n logical tokens in place through the arena's slot map.
+
+    query [nq, Hq, 128] bf16, query_positions int64 [nq] (< n); returns
+    [nq, Hq, 128] bf16.
+    """
+    n = arena.logical_length()
+    with arena.device_slots(range(n)) as (slots, side_k, side_v):
+        lens = torch.full((1,), n, dtype=torch.int32, device=query.device)
+        out = ccpe_prefill_paged(query.unsqueeze(0), arena.cache, None, lens, cope,
+                                 query_positions.reshape(1, -1).contiguous(), slots=slots.unsqueeze(0),
+                                 side_k=side_k, side_v=side_v, check=check)
+    return out[0]
+
+
+def decode_workspace_bytes(batch: int, heads: int, max_context: int, split: int) -> int:
+    return int(_hip.load().cs_ccpe_decode_workspace_bytes(batch, heads, max_context, split))
+
+
 def decode_workspace(batch: int, heads: int, max_context: int, split: int, device) -> Tensor:
-    nbytes = int(_hip.load().cs_ccpe_decode_workspace_bytes(batch, heads, max_context, split))
+    nbytes = decode_workspace_bytes(batch, heads, max_context, split)
     return torch.empty(max(nbytes, 16), dtype=torch.uint8, device=device)
 
 
 def ccpe_decode_paged(
     query: Tensor,
     cache: Tensor,
-    block_table: Tensor,
+    block_table: Tensor | None,
     context_lens: Tensor,
     cope,
     *,
+    slots: Tensor | None = None,
+    side_k: Tensor | None = None,
+    side_v: Tensor | None = None,
     max_context: int | None = None,
     split: int = 1024,
     workspace: Tensor | None = None,
@@ -137,11 +220,16 @@ def ccpe_decode_paged(
 ) -> Tensor:
     """Batched CCPE decode: row b attends keys 0..context_lens[b]-1 at position context_lens[b]-1.
 
-    query [B, Hq, 128] bf16; returns [B, Hq, 128] bf16.  ``max_context`` bounds
-    context_lens (read back from the device when omitted); ``split`` is the
-    number of keys per split-K work item (multiple of 64, <= 1024).
+    query [B, Hq, 128] bf16; returns [B, Hq, 128] bf16.  Keys come through
+    ``block_table`` (int32 [B, max_blocks]) or through ``slots`` (int64
+    [B, >= max_context], native slots and rows of ``side_k`` / ``side_v``).
+    ``max_context`` bounds context_lens (read back from the device when
+    omitted); a larger context raises ValueError, as does an empty one
+    (position.py:149-150).  ``split`` is the number of keys per split-K work
+    item (multiple of 64, <= 1024).  ``workspace`` (uint8, device) must hold
+    ``decode_workspace_bytes(B, Hq, max_context, split)`` bytes.
     """
-    device = _hip.require_device(query, cache, block_table, context_lens)
+    device = _hip.require_device(query, cache, context_lens, block_table, slots)
     if query.ndim != 3 or query.dtype != torch.bfloat16 or query.shape[2] != 128 or query.stride(2) != 1:
         raise ValueError("query must be bf16 [batch, heads, 128] with contiguous rows")
     b, hq = query.shape[0], query.shape[1]
@@ -151,24 +239,57 @@ def ccpe_decode_paged(
     if context_lens.shape != (b,) or context_lens.dtype != torch.int32:
         raise ValueError("context_lens must be int32 [batch]")
     e = _check_e(cope, device)
-    src = _paged_source(cache, block_table)
+    src = _kv_source(cache, block_table, slots, side_k, side_v)
     if max_context is None:
-        max_context = int(context_lens.max().item()) if b else 1
+        max_context = max(int(context_lens.max().item()), 1) if b else 1
+    if type(max_context) is not int or max_context < 1:
+        raise ValueError("max_context must be a positive integer")
+    if slots is not None and slots.shape[0] != b:
+        raise ValueError("slots must have one row per request")
+    if slots is not None and slots.shape[1] < max_context:
+        raise ValueError("slots must cover max_context tokens per request")
+    need = decode_workspace_bytes(b, hq, max_context, split)
     if workspace is None:
         workspace = decode_workspace(b, hq, max_context, split, device)
+    elif workspace.device != device or not workspace.is_contiguous():
+        raise ValueError("workspace must be a contiguous tensor on the query device")
+    have = workspace.numel() * workspace.element_size()
+    if have < need:
+        raise ValueError(f"decode workspace holds {have} bytes, the call needs {need}")
     flags = _hip.new_flags(device)
     out = torch.empty((b, hq, 128), dtype=torch.bfloat16, device=device)
     call(
         "cs_ccpe_decode_bf16", ptr(query), query.stride(0), query.stride(1), b, hq, hkv,
         ptr(context_lens), max_context, src, ptr(e), cope.max_positions, split, ptr(workspace),
-        ptr(out), ptr(flags), _hip.stream_of(device),
+        have, ptr(out), ptr(flags), _hip.stream_of(device),
     )
     if check:
         _raise_flags(flags)
     return out
 
 
+def ccpe_decode_arena(query: Tensor, arena, cope, *, split: int = 1024, check: bool = True) -> Tensor:
+    """The decode step of runtime.py:489-508 on one request's arena, fused:
+    ``cope_attention(query, *arena.gather(range(n)), cope, [n - 1])`` with n the
+    arena's logical length, read in place through the arena's slot map.
+
+    query [Hq, 128] (or [1, Hq, 128]) bf16; returns [1, Hq, 128] bf16.
+    """
+    if query.ndim == 2:
+        query = query.unsqueeze(0)
+    n = arena.logical_length()
+    with arena.device_slots(range(n)) as (slots, side_k, side_v):
+        lens = torch.full((1,), n, dtype=torch.int32, device=query.device)
+        return ccpe_decode_paged(query, arena.cache, None, lens, cope, slots=slots.unsqueeze(0),
+                                 side_k=side_k, side_v=side_v, max_context=max(n, 1), split=split,
+                                 check=check)
+
+
 def _raise_flags(flags: Tensor) -> None:
     value = _hip.read_flags(flags)[0]
+    if value & _hip.FLAG_NO_KEY:
+        raise ValueError("attention requires at least one key")
+    if value & _hip.FLAG_CONTEXT_RANGE:
+        raise ValueError("context_lens exceeds max_context")
     if value & _hip.FLAG_BLOCK_INVALID:
-        raise ValueError("block_table names a block outside the cache")
+        raise ValueError("a block-table entry or slot names a record outside the cache")

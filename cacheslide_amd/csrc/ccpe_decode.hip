@@ -25,8 +25,8 @@
 //   keys 4g .. 4g+3, dims 8x .. 8x+7, and the probabilities of head h reach it
 //   from lane (g, h) through a DPP row broadcast.
 // The next tile's K/V loads are issued before the current tile is consumed.
-// Record offsets of the split's keys are resolved through the block table
-// once, into LDS.
+// Record offsets of the split's keys are resolved once, into LDS, through the
+// block table or the per-token slot map (native slot or sidecar row).
 
 #include "common.h"
 
@@ -53,6 +53,11 @@ constexpr float kLog2e = 1.4426950408889634f;
 // exactly (a load under a branch makes it wait for all of them).
 __device__ __attribute__((aligned(16))) uint32_t g_zero_record[kD] = {};
 
+// A key's record offset in LDS: an element offset from the cache base, or,
+// with kSideBit set, from the sidecar bases (K and V share the offset); -1
+// when the key's block or slot is invalid.
+constexpr int64_t kSideBit = int64_t(1) << 62;
+
 struct kv_addr {
   const uint16_t* cache;
   int64_t s_block, s_head, s_offset;
@@ -63,6 +68,12 @@ struct kv_addr {
   const uint16_t* k;
   const uint16_t* v;
   int64_t k_sb, k_st, k_sh, v_sb, v_st, v_sh;
+  const int64_t* slots;  // per-token slot map (replaces the block table)
+  int64_t slots_stride;
+  int64_t native_slots;  // num_blocks * block_size
+  const uint16_t* side_k;
+  const uint16_t* side_v;
+  int64_t side_sr, side_sh, side_rows;
 };
 
 struct decode_params {
@@ -70,6 +81,7 @@ struct decode_params {
   int64_t q_sb, q_sh;
   int32_t batch, hq, hkv, group;
   const int32_t* nk;
+  int32_t max_nk;
   kv_addr kv;
   const float* e;
   int32_t npos;
@@ -166,11 +178,35 @@ __device__ inline const uint16_t* zero_record() {
 
 __device__ inline uint4 ld16(const uint16_t* ptr) { return *reinterpret_cast<const uint4*>(ptr); }
 
-// Resolve the record offsets of keys [lo, hi) through the block table.
+// Element offset of the record of native slot `slot` (block slot / bs, offset
+// slot % bs) for KV head kvh.
+__device__ inline int64_t native_record(const kv_addr& kv, int64_t blk, int64_t o, int kvh) {
+  return blk * kv.s_block + kvh * kv.s_head + o * kv.s_offset;
+}
+
+// Resolve the record offsets of keys [lo, hi) through the block table or the
+// slot map.
 template <int G>
 __device__ void load_offsets(const decode_params& p, smem_t<G>& s, const split_ctx& c, bool& bad) {
-  if (!p.kv.block_table) return;
   const int n = static_cast<int>(c.hi - c.lo);
+  if (p.kv.slots) {
+    const int64_t* row = p.kv.slots + c.b * p.kv.slots_stride;
+    for (int i = threadIdx.x; i < n; i += kThreads) {
+      const int64_t slot = row[c.lo + i];
+      int64_t off = -1;
+      if (slot >= 0 && slot < p.kv.native_slots) {
+        const int64_t blk = p.kv.bs_shift >= 0 ? (slot >> p.kv.bs_shift) : slot / p.kv.block_size;
+        const int64_t o = slot - blk * p.kv.block_size;
+        off = native_record(p.kv, blk, o, c.kvh);
+      } else if (slot >= p.kv.native_slots && slot - p.kv.native_slots < p.kv.side_rows) {
+        off = kSideBit | ((slot - p.kv.native_slots) * p.kv.side_sr + c.kvh * p.kv.side_sh);
+      }
+      if (off < 0) bad = true;
+      s.koff[i] = off;
+    }
+    return;
+  }
+  if (!p.kv.block_table) return;
   for (int i = threadIdx.x; i < n; i += kThreads) {
     const int64_t j = c.lo + i;
     const int64_t bi = p.kv.bs_shift >= 0 ? (j >> p.kv.bs_shift) : j / p.kv.block_size;
@@ -180,7 +216,7 @@ __device__ void load_offsets(const decode_params& p, smem_t<G>& s, const split_c
       if (blk >= 0 && blk < p.kv.num_blocks) {
         const int64_t o =
             p.kv.bs_shift >= 0 ? (j & ((int64_t(1) << p.kv.bs_shift) - 1)) : j % p.kv.block_size;
-        off = blk * p.kv.s_block + c.kvh * p.kv.s_head + o * p.kv.s_offset;
+        off = native_record(p.kv, blk, o, c.kvh);
       }
     }
     if (off < 0) bad = true;
@@ -195,7 +231,8 @@ __device__ inline const uint16_t* k_row(const decode_params& p, const smem_t<G>&
                                         const split_ctx& c, int64_t j, bool valid) {
   if constexpr (PAGED) {
     const int64_t o = s.koff[valid ? j - c.lo : 0];
-    return valid && o >= 0 ? p.kv.cache + o : zero_record();
+    if (!valid || o < 0) return zero_record();
+    return (o & kSideBit) ? p.kv.side_k + (o ^ kSideBit) : p.kv.cache + o;
   } else {
     return valid ? p.kv.k + c.b * p.kv.k_sb + j * p.kv.k_st + c.kvh * p.kv.k_sh : zero_record();
   }
@@ -206,7 +243,8 @@ __device__ inline const uint16_t* v_row(const decode_params& p, const smem_t<G>&
                                         const split_ctx& c, int64_t j, bool valid) {
   if constexpr (PAGED) {
     const int64_t o = s.koff[valid ? j - c.lo : 0];
-    return valid && o >= 0 ? p.kv.cache + o + kD : zero_record() + kD;
+    if (!valid || o < 0) return zero_record() + kD;
+    return (o & kSideBit) ? p.kv.side_v + (o ^ kSideBit) : p.kv.cache + o + kD;
   } else {
     return valid ? p.kv.v + c.b * p.kv.v_sb + j * p.kv.v_st + c.kvh * p.kv.v_sh : zero_record() + kD;
   }
@@ -613,6 +651,11 @@ __global__ void __launch_bounds__(kThreads) decode_main_kernel(decode_params p) 
   const int r = id / per_r, rem = id % per_r;
   const int b = rem / p.hkv, kvh = rem % p.hkv;
   if (id == 0 && threadIdx.x == 0) *p.work_count = 0;
+  if (r == 0 && kvh == 0 && threadIdx.x == 0) {
+    const int nk = p.nk[b];
+    if (nk < 1) atomicOr(p.flags, CS_FLAG_NO_KEY);
+    if (nk > p.max_nk) atomicOr(p.flags, CS_FLAG_CONTEXT_RANGE);
+  }
   split_ctx c;
   if (!make_ctx(p, b, kvh, r, c)) return;
   bool bad = false;
@@ -785,7 +828,7 @@ void launch_split_kernels(const decode_params& p, hipStream_t s) {
 
 template <int G>
 void launch_group(const decode_params& p, hipStream_t s) {
-  if (p.kv.block_table)
+  if (p.kv.block_table || p.kv.slots)
     launch_split_kernels<G, true>(p, s);
   else
     launch_split_kernels<G, false>(p, s);
@@ -805,12 +848,15 @@ extern "C" int64_t cs_ccpe_decode_workspace_bytes(int32_t batch, int32_t hq, int
   return n * (8 + 8 + 4 * kD + 4 + 4 + 4) + 16;
 }
 
-extern "C" int cs_ccpe_decode_bf16(const void* q, int64_t q_s_batch, int64_t q_s_head,
-                                   int32_t batch, int32_t hq, int32_t hkv, const int32_t* nk,
-                                   int32_t max_nk, const cs_kv_source* kv, const float* e,
-                                   int32_t max_positions, int32_t split, void* workspace,
-                                   void* out, int32_t* flags, void* stream) {
-  CS_REQUIRE(q && nk && kv && e && out && flags && workspace, "null arguments");
+namespace {
+
+// Validate the arguments of a decode call and fill its parameters; the
+// workspace pointers are set by the caller.
+int prepare_decode(const void* q, int64_t q_s_batch, int64_t q_s_head, int32_t batch, int32_t hq,
+                   int32_t hkv, const int32_t* nk, int32_t max_nk, const cs_kv_source* kv,
+                   const float* e, int32_t max_positions, int32_t split, void* out, int32_t* flags,
+                   decode_params* pp) {
+  CS_REQUIRE(q && nk && kv && e && out && flags, "null arguments");
   CS_REQUIRE(hq > 0 && hkv > 0 && hq % hkv == 0 && hq / hkv <= kMaxGroup,
              "GQA group must be at most %d", kMaxGroup);
   CS_REQUIRE(max_positions >= 2 && max_positions <= kMaxPos, "max_positions must be in [2, %d]",
@@ -819,7 +865,6 @@ extern "C" int cs_ccpe_decode_bf16(const void* q, int64_t q_s_batch, int64_t q_s
              "split must be a multiple of 64 in [64, %d]", kMaxSplit);
   CS_REQUIRE(max_nk >= 1, "max_nk must be positive");
   CS_REQUIRE(batch >= 0, "batch must be non-negative");
-  CS_REQUIRE((reinterpret_cast<uintptr_t>(workspace) % 16) == 0, "workspace must be aligned");
   CS_REQUIRE((reinterpret_cast<uintptr_t>(q) % 16) == 0 && q_s_batch % 8 == 0 && q_s_head % 8 == 0,
              "query rows must be 16-byte aligned");
   const int64_t smax = (static_cast<int64_t>(max_nk) + split - 1) / split;
@@ -833,9 +878,11 @@ extern "C" int cs_ccpe_decode_bf16(const void* q, int64_t q_s_batch, int64_t q_s
   p.hkv = hkv;
   p.group = hq / hkv;
   p.nk = nk;
-  if (kv->block_table) {
-    CS_REQUIRE(kv->cache && kv->block_size > 0 && (reinterpret_cast<uintptr_t>(kv->cache) % 16) == 0 &&
-                   kv->s_block % 8 == 0 && kv->s_head % 8 == 0 && kv->s_offset % 8 == 0,
+  p.max_nk = max_nk;
+  if (kv->block_table || kv->slots) {
+    CS_REQUIRE(kv->cache && kv->block_size > 0 && kv->num_blocks >= 0 &&
+                   (reinterpret_cast<uintptr_t>(kv->cache) % 16) == 0 && kv->s_block % 8 == 0 &&
+                   kv->s_head % 8 == 0 && kv->s_offset % 8 == 0,
                "paged cache rows must be 16-byte aligned");
     p.kv.cache = static_cast<const uint16_t*>(kv->cache);
     p.kv.s_block = kv->s_block;
@@ -843,13 +890,32 @@ extern "C" int cs_ccpe_decode_bf16(const void* q, int64_t q_s_batch, int64_t q_s
     p.kv.s_offset = kv->s_offset;
     p.kv.block_size = kv->block_size;
     p.kv.num_blocks = kv->num_blocks;
-    p.kv.block_table = kv->block_table;
-    p.kv.bt_stride = kv->bt_stride;
-    p.kv.bt_cols = kv->bt_cols;
     p.kv.bs_shift = -1;
     for (int sh = 0; sh < 31; ++sh)
       if ((1 << sh) == kv->block_size) p.kv.bs_shift = sh;
-    CS_REQUIRE(p.kv.bt_cols > 0, "block table needs at least one column");
+    if (kv->slots) {
+      CS_REQUIRE(kv->slots_stride >= 0, "slot map stride must be non-negative");
+      CS_REQUIRE(kv->side_rows >= 0, "side_rows must be non-negative");
+      if (kv->side_rows > 0)
+        CS_REQUIRE(kv->side_k && kv->side_v && (reinterpret_cast<uintptr_t>(kv->side_k) % 16) == 0 &&
+                       (reinterpret_cast<uintptr_t>(kv->side_v) % 16) == 0 &&
+                       kv->side_s_row % 8 == 0 && kv->side_s_head % 8 == 0 &&
+                       kv->side_s_row >= 0 && kv->side_s_head >= 0,
+                   "sidecar rows must be 16-byte aligned");
+      p.kv.slots = kv->slots;
+      p.kv.slots_stride = kv->slots_stride;
+      p.kv.native_slots = kv->num_blocks * kv->block_size;
+      p.kv.side_k = static_cast<const uint16_t*>(kv->side_k);
+      p.kv.side_v = static_cast<const uint16_t*>(kv->side_v);
+      p.kv.side_sr = kv->side_s_row;
+      p.kv.side_sh = kv->side_s_head;
+      p.kv.side_rows = kv->side_rows;
+    } else {
+      p.kv.block_table = kv->block_table;
+      p.kv.bt_stride = kv->bt_stride;
+      p.kv.bt_cols = kv->bt_cols;
+      CS_REQUIRE(p.kv.bt_cols > 0, "block table needs at least one column");
+    }
   } else {
     CS_REQUIRE(kv->k && kv->v && (reinterpret_cast<uintptr_t>(kv->k) % 16) == 0 &&
                    (reinterpret_cast<uintptr_t>(kv->v) % 16) == 0 && kv->k_s_tok % 8 == 0 &&
@@ -869,7 +935,15 @@ extern "C" int cs_ccpe_decode_bf16(const void* q, int64_t q_s_batch, int64_t q_s
   p.npos = max_positions;
   p.split = split;
   p.smax = static_cast<int32_t>(smax);
-  const int64_t n = static_cast<int64_t>(batch) * hq * p.smax;
+  p.out = static_cast<uint16_t*>(out);
+  p.flags = flags;
+  *pp = p;
+  return CS_OK;
+}
+
+// Carve the workspace of a prepared call and launch its kernels.
+int launch_decode(decode_params& p, void* workspace, void* stream) {
+  const int64_t n = static_cast<int64_t>(p.batch) * p.hq * p.smax;
   char* ws = static_cast<char*>(workspace);
   p.tot = reinterpret_cast<double*>(ws);
   p.carry = p.tot + n;
@@ -878,9 +952,7 @@ extern "C" int cs_ccpe_decode_bf16(const void* q, int64_t q_s_batch, int64_t q_s
   p.sm = p.mx + n;
   p.work = reinterpret_cast<int32_t*>(p.sm + n);
   p.work_count = p.work + n;
-  p.out = static_cast<uint16_t*>(out);
-  p.flags = flags;
-  if (batch == 0) return CS_OK;
+  if (p.batch == 0) return CS_OK;
   hipStream_t s = as_stream(stream);
   switch (p.group) {
     case 1: launch_group<1>(p, s); break;
@@ -892,7 +964,27 @@ extern "C" int cs_ccpe_decode_bf16(const void* q, int64_t q_s_batch, int64_t q_s
     case 7: launch_group<7>(p, s); break;
     default: launch_group<8>(p, s); break;
   }
-  hipLaunchKernelGGL(decode_combine_kernel, dim3(batch * hq), dim3(kD), 0, s, p);
+  hipLaunchKernelGGL(decode_combine_kernel, dim3(p.batch * p.hq), dim3(kD), 0, s, p);
   CS_LAUNCH_CHECK("ccpe_decode");
   return CS_OK;
+}
+
+}  // namespace
+
+extern "C" int cs_ccpe_decode_bf16(const void* q, int64_t q_s_batch, int64_t q_s_head,
+                                   int32_t batch, int32_t hq, int32_t hkv, const int32_t* nk,
+                                   int32_t max_nk, const cs_kv_source* kv, const float* e,
+                                   int32_t max_positions, int32_t split, void* workspace,
+                                   int64_t workspace_bytes, void* out, int32_t* flags,
+                                   void* stream) {
+  decode_params p{};
+  const int st = prepare_decode(q, q_s_batch, q_s_head, batch, hq, hkv, nk, max_nk, kv, e,
+                                max_positions, split, out, flags, &p);
+  if (st) return st;
+  const int64_t need = cs_ccpe_decode_workspace_bytes(batch, hq, max_nk, split);
+  CS_REQUIRE(workspace != nullptr || batch == 0, "null workspace");
+  CS_REQUIRE(workspace_bytes >= need, "decode workspace holds %lld bytes, the call needs %lld",
+             static_cast<long long>(workspace_bytes), static_cast<long long>(need));
+  CS_REQUIRE((reinterpret_cast<uintptr_t>(workspace) % 16) == 0, "workspace must be aligned");
+  return launch_decode(p, workspace, stream);
 }

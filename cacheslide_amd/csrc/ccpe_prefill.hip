@@ -46,6 +46,13 @@
 // so one direct load (64 lanes x 16 bytes = slots 64 j .. 64 j + 63) covers the
 // same four keys 4j .. 4j+3 in K and in V, and each lane loads key 4j + lane % 4
 // of both: the record address of a key is computed once for K and V.
+//
+// K/V sources (MODE): dense K/V rows (0); the paged cache through a block table
+// (1); the paged cache through a per-token slot map whose slots past the native
+// pool name sidecar rows (2).  Modes 1 and 2 keep a window of the table (block
+// ids, or one entry per key) in LDS, and a load whose four keys share one block
+// in consecutive offsets takes the scalar-base form; other loads address each
+// lane's record.
 
 #include "common.h"
 
@@ -66,7 +73,7 @@ constexpr int kChunks = 16;              // 16-byte chunks of a 256-byte K or V 
 constexpr int kStageSlots = kTileN * kChunks;  // uint4 slots of one K (or V) stage
 constexpr int kMaxPos = 128;
 constexpr int kPosChunk = 64;  // E^T positions staged per pass (bf16 hi and lo, 16 KB each)
-constexpr int kBtWindow = 1024;  // block-table entries held in LDS at a time
+constexpr int kBtWindow = 1024;  // block-table (or slot-map) entries held in LDS at a time
 constexpr int kStages = 3;
 constexpr size_t kStaticLds = kStages * 2 * kStageSlots * 16 + 4 * kBtWindow + 16;
 constexpr size_t kLdsLimit = 160 * 1024;
@@ -106,7 +113,18 @@ struct kv_addr {
   const uint16_t* k;
   const uint16_t* v;
   int64_t k_sb, k_st, k_sh, v_sb, v_st, v_sh;
+  const int64_t* slots;  // per-token slot map (mode 2)
+  int64_t slots_stride;
+  int64_t native_slots;  // num_blocks * block_size (< 2^31)
+  const uint16_t* side_k;
+  const uint16_t* side_v;
+  int64_t side_sr, side_sh, side_rows;
 };
+
+// Slot-map window entries (mode 2): a native slot (< 2^31), kSideTag | sidecar
+// row, or kNoSlot for an invalid slot.
+constexpr uint32_t kSideTag = 0x80000000u;
+constexpr uint32_t kNoSlot = 0xFFFFFFFFu;
 
 struct prefill_params {
   const uint16_t* q;
@@ -173,14 +191,18 @@ struct stage_t {
 };
 
 // WAVES wavefronts of 32 columns each; two wavefronts per SIMD
-template <bool PAGED, int WAVES>
+template <int MODE, int WAVES>
 __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(prefill_params p) {
+  constexpr bool PAGED = MODE != 0;
+  constexpr bool SLOTS = MODE == 2;
   constexpr int kThreads = 64 * WAVES;
   constexpr int kInstr = 8 / WAVES;  // 64-slot loads per wave for each of K and V
   __shared__ __align__(16) stage_t st0;
   __shared__ __align__(16) stage_t st1;
   __shared__ __align__(16) stage_t st2;
-  __shared__ int32_t bt_lds[kBtWindow];  // block ids of blocks [bt_lo, bt_lo + kBtWindow)
+  // block ids of blocks [bt_lo, bt_lo + kBtWindow), or (slot map) the entries
+  // of keys [bt_lo, bt_lo + kBtWindow)
+  __shared__ int32_t bt_lds[kBtWindow];
   __shared__ int64_t wg_max_pos;
   // [32 WAVES columns][tab_stride] QE log2(e), fp16 (the table only enters
   // bias differences of unsaturated keys; 2^-11 relative precision)
@@ -306,12 +328,30 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
   // before the window's tile loop, so that loop issues no vector-memory
   // operation other than the tile loads themselves.
   int64_t bt_lo = 0;
-  auto load_window = [&](int tlo, int thi) {  // blocks of keys [32 tlo, 32 thi)
-    const int64_t blo = (static_cast<int64_t>(tlo) * kTileN) >> p.kv.bs_shift;
-    const int64_t bhi = (static_cast<int64_t>(thi) * kTileN - 1) >> p.kv.bs_shift;
-    for (int64_t i = tid; i <= bhi - blo; i += kThreads)
-      bt_lds[i] = blo + i < p.kv.bt_cols ? p.kv.block_table[b * p.kv.bt_stride + blo + i] : -1;
-    bt_lo = blo;
+  auto load_window = [&](int tlo, int thi) {  // blocks (or slots) of keys [32 tlo, 32 thi)
+    if constexpr (SLOTS) {
+      const int klo = tlo * kTileN, n_win = (thi - tlo) * kTileN;
+      const int64_t* srow = p.kv.slots + b * p.kv.slots_stride;
+      for (int i = tid; i < n_win; i += kThreads) {
+        const int key = klo + i;
+        uint32_t ent = kNoSlot;
+        if (key < kend) {
+          const int64_t slot = srow[key];
+          if (slot >= 0 && slot < p.kv.native_slots)
+            ent = static_cast<uint32_t>(slot);
+          else if (slot >= p.kv.native_slots && slot - p.kv.native_slots < p.kv.side_rows)
+            ent = kSideTag | static_cast<uint32_t>(slot - p.kv.native_slots);
+        }
+        bt_lds[i] = static_cast<int32_t>(ent);
+      }
+      bt_lo = klo;
+    } else {
+      const int64_t blo = (static_cast<int64_t>(tlo) * kTileN) >> p.kv.bs_shift;
+      const int64_t bhi = (static_cast<int64_t>(thi) * kTileN - 1) >> p.kv.bs_shift;
+      for (int64_t i = tid; i <= bhi - blo; i += kThreads)
+        bt_lds[i] = blo + i < p.kv.bt_cols ? p.kv.block_table[b * p.kv.bt_stride + blo + i] : -1;
+      bt_lo = blo;
+    }
   };
 
   // ---- tile loads.  Load j (0..7) of a stage fills slots [64 j, 64 j + 64) of
@@ -359,11 +399,26 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
     for (int i = 0; i < kInstr; ++i) {
       const int key0 = tl * kTileN + 4 * (kInstr * wave + i);
       bool ok = tl >= win_lo && key0 + 3 < kend32 && p.kv.bs_shift >= 2;
-      const int idx = ok ? (key0 >> p.kv.bs_shift) - static_cast<int>(bt_lo) : 0;
-      const int blk = bt_lds[idx];
-      ok = ok && blk >= 0 && blk < nblocks;
+      int blk;
+      uint32_t offs;
+      if constexpr (SLOTS) {
+        // the four keys' slots are native, consecutive and in one block
+        const int idx = ok ? key0 - static_cast<int>(bt_lo) : 0;
+        const uint32_t s0 = static_cast<uint32_t>(bt_lds[idx]);
+        ok = ok && (s0 & kSideTag) == 0u && (s0 & off_mask) + 3u <= off_mask &&
+             static_cast<uint32_t>(bt_lds[idx + 1]) == s0 + 1u &&
+             static_cast<uint32_t>(bt_lds[idx + 2]) == s0 + 2u &&
+             static_cast<uint32_t>(bt_lds[idx + 3]) == s0 + 3u;
+        blk = static_cast<int>(s0 >> p.kv.bs_shift);
+        offs = s0 & off_mask;
+      } else {
+        const int idx = ok ? (key0 >> p.kv.bs_shift) - static_cast<int>(bt_lo) : 0;
+        blk = bt_lds[idx];
+        ok = ok && blk >= 0 && blk < nblocks;
+        offs = static_cast<uint32_t>(key0) & off_mask;
+      }
       const uint64_t off = 2ull * (static_cast<uint64_t>(static_cast<uint32_t>(blk)) * s_blk +
-                                   static_cast<uint64_t>(static_cast<uint32_t>(key0) & off_mask) * s_off);
+                                   static_cast<uint64_t>(offs) * s_off);
       fo_lo[i] = ok ? static_cast<uint32_t>(off) : 0u;
       fo_hi[i] = ok ? static_cast<uint32_t>(off >> 32) : 0xFFFFFFFFu;
     }
@@ -403,7 +458,21 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
         const bool in = key < kend32;
         const uint16_t* kr;
         const uint16_t* vr;
-        if constexpr (PAGED) {
+        if constexpr (SLOTS) {
+          const uint32_t ent = in ? static_cast<uint32_t>(bt_lds[key - static_cast<int>(bt_lo)]) : kNoSlot;
+          const bool ok = ent != kNoSlot;
+          bad_block |= in && !ok;
+          if (ok && (ent & kSideTag)) {
+            const int64_t so = static_cast<int64_t>(ent & ~kSideTag) * p.kv.side_sr + kvh * p.kv.side_sh;
+            kr = p.kv.side_k + so;
+            vr = p.kv.side_v + so;
+          } else {
+            const uint64_t off = static_cast<uint64_t>(ent >> p.kv.bs_shift) * s_blk +
+                                 static_cast<uint64_t>(ent & off_mask) * s_off;
+            kr = ok ? rec_base + off : zrec;
+            vr = kr + kD;
+          }
+        } else if constexpr (PAGED) {
           const int blk = bt_lds[(key >> p.kv.bs_shift) - static_cast<int>(bt_lo)];
           const bool ok = in && blk >= 0 && blk < nblocks;
           bad_block |= in && !ok;
@@ -614,7 +683,9 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
   // compiler keeps a full vector-memory wait inside the tile loop for them.
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   int tiles_per_window = ntiles;
-  if constexpr (PAGED)
+  if constexpr (SLOTS)
+    tiles_per_window = kBtWindow / kTileN;
+  else if constexpr (PAGED)
     tiles_per_window = static_cast<int>(((static_cast<int64_t>(kBtWindow) - 1) << p.kv.bs_shift) / kTileN);
   if (tiles_per_window < 1) tiles_per_window = 1;
   for (int thi = ntiles; thi > 0;) {
@@ -674,7 +745,7 @@ namespace {
 int fill_kv(const cs_kv_source* kv, cs::kv_addr* a) {
   CS_REQUIRE(kv != nullptr, "null kv source");
   cs::kv_addr r{};
-  if (kv->block_table) {
+  if (kv->block_table || kv->slots) {
     CS_REQUIRE(kv->cache && kv->block_size > 0 && kv->num_blocks > 0, "paged kv needs a cache");
     CS_REQUIRE(kv->s_block % 8 == 0 && kv->s_head % 8 == 0 && kv->s_offset % 8 == 0 &&
                    (reinterpret_cast<uintptr_t>(kv->cache) % 16) == 0,
@@ -688,10 +759,30 @@ int fill_kv(const cs_kv_source* kv, cs::kv_addr* a) {
     for (int s = 0; s < 31; ++s)
       if ((1 << s) == kv->block_size) r.bs_shift = s;
     r.num_blocks = kv->num_blocks;
-    r.block_table = kv->block_table;
-    r.bt_stride = kv->bt_stride;
-    r.bt_cols = kv->bt_cols;
-    CS_REQUIRE(r.bt_cols > 0, "block table needs at least one column");
+    if (kv->slots) {
+      CS_REQUIRE(kv->slots_stride >= 0 && kv->side_rows >= 0, "bad slot map");
+      CS_REQUIRE(kv->num_blocks * kv->block_size < (int64_t(1) << 31) && kv->side_rows < (int64_t(1) << 31),
+                 "the slot-map prefill needs fewer than 2^31 native slots and sidecar rows");
+      if (kv->side_rows > 0)
+        CS_REQUIRE(kv->side_k && kv->side_v && (reinterpret_cast<uintptr_t>(kv->side_k) % 16) == 0 &&
+                       (reinterpret_cast<uintptr_t>(kv->side_v) % 16) == 0 &&
+                       kv->side_s_row % 8 == 0 && kv->side_s_head % 8 == 0 &&
+                       kv->side_s_row >= 0 && kv->side_s_head >= 0,
+                   "sidecar rows must be 16-byte aligned");
+      r.slots = kv->slots;
+      r.slots_stride = kv->slots_stride;
+      r.native_slots = kv->num_blocks * kv->block_size;
+      r.side_k = static_cast<const uint16_t*>(kv->side_k);
+      r.side_v = static_cast<const uint16_t*>(kv->side_v);
+      r.side_sr = kv->side_s_row;
+      r.side_sh = kv->side_s_head;
+      r.side_rows = kv->side_rows;
+    } else {
+      r.block_table = kv->block_table;
+      r.bt_stride = kv->bt_stride;
+      r.bt_cols = kv->bt_cols;
+      CS_REQUIRE(r.bt_cols > 0, "block table needs at least one column");
+    }
   } else {
     CS_REQUIRE(kv->k && kv->v, "dense kv needs k and v");
     CS_REQUIRE(kv->k_s_tok % 8 == 0 && kv->k_s_head % 8 == 0 && kv->v_s_tok % 8 == 0 &&
@@ -735,14 +826,15 @@ extern "C" int cs_ccpe_prefill_bf16(const void* q, int64_t q_s_batch, int64_t q_
   cs::prefill_params p{};
   int st = fill_kv(kv, &p.kv);
   if (st) return st;
-  if (p.kv.block_table ? (p.kv.s_block >= (1ll << 31) || p.kv.s_offset >= (1ll << 31) || p.kv.s_block < 0 ||
+  const bool paged = p.kv.block_table || p.kv.slots;
+  if (paged ? (p.kv.s_block >= (1ll << 31) || p.kv.s_offset >= (1ll << 31) || p.kv.s_block < 0 ||
                           p.kv.s_offset < 0)
                        : (p.kv.k_st >= (1ll << 31) || p.kv.v_st >= (1ll << 31) || p.kv.k_st < 0 ||
                           p.kv.v_st < 0)) {
     set_error("the MFMA prefill kernel needs non-negative block / token strides below 2^31");
     return CS_EUNSUPPORTED;
   }
-  if (p.kv.block_table && p.kv.bs_shift < 0) {
+  if (paged && p.kv.bs_shift < 0) {
     set_error("the MFMA prefill kernel needs a power-of-two block size (got %d)", kv->block_size);
     return CS_EUNSUPPORTED;
   }
@@ -786,14 +878,19 @@ extern "C" int cs_ccpe_prefill_bf16(const void* q, int64_t q_s_batch, int64_t q_
   }
   const dim3 grid(p.total_wg), block(64 * waves);
   hipStream_t s = as_stream(stream);
-  if (p.kv.block_table && waves == 8)
-    hipLaunchKernelGGL((ccpe_prefill_kernel<true, 8>), grid, block, smem, s, p);
-  else if (p.kv.block_table)
-    hipLaunchKernelGGL((ccpe_prefill_kernel<true, 4>), grid, block, smem, s, p);
+  const int mode = p.kv.slots ? 2 : (p.kv.block_table ? 1 : 0);
+  if (mode == 2 && waves == 8)
+    hipLaunchKernelGGL((ccpe_prefill_kernel<2, 8>), grid, block, smem, s, p);
+  else if (mode == 2)
+    hipLaunchKernelGGL((ccpe_prefill_kernel<2, 4>), grid, block, smem, s, p);
+  else if (mode == 1 && waves == 8)
+    hipLaunchKernelGGL((ccpe_prefill_kernel<1, 8>), grid, block, smem, s, p);
+  else if (mode == 1)
+    hipLaunchKernelGGL((ccpe_prefill_kernel<1, 4>), grid, block, smem, s, p);
   else if (waves == 8)
-    hipLaunchKernelGGL((ccpe_prefill_kernel<false, 8>), grid, block, smem, s, p);
+    hipLaunchKernelGGL((ccpe_prefill_kernel<0, 8>), grid, block, smem, s, p);
   else
-    hipLaunchKernelGGL((ccpe_prefill_kernel<false, 4>), grid, block, smem, s, p);
+    hipLaunchKernelGGL((ccpe_prefill_kernel<0, 4>), grid, block, smem, s, p);
   CS_LAUNCH_CHECK("ccpe_prefill");
   return CS_OK;
 }

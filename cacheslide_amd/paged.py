@@ -28,6 +28,7 @@ import queue
 import threading
 from collections.abc import Iterable, Sequence
 from concurrent.futures import Future
+from contextlib import contextmanager
 
 import numpy as np
 import torch
@@ -407,6 +408,29 @@ class NativePagedKV:
                                    key, value)
             _wait_device(self.cache.device)  # the pins hold until the reads have executed
             return key, value
+
+    def logical_length(self) -> int:
+        """Number of logical tokens (prompt plus decoded), i.e. the next decode token."""
+        with self._mutex:
+            return len(self._canonical)
+
+    @contextmanager
+    def device_slots(self, logical_positions):
+        """The slots ``gather`` would read for the positions, for a kernel that
+        reads the arena in place: yields (int64 device slots, sidecar K, sidecar V)
+        -- the sidecar tensors are None before first use -- under pins of those
+        slots, held until the reads enqueued inside the block have executed
+        (the read half of paged.py:433-472)."""
+        positions = _indices(logical_positions, "logical_positions")
+        with self._mutex, self.slot_map.pinned_mapping(positions) as current:
+            self._settled_loads(pending_ok=True)
+            slots = torch.tensor([current[t] for t in positions], dtype=torch.long,
+                                 device=self.cache.device)
+            side_k, side_v = self._side if self._side is not None else (None, None)
+            try:
+                yield slots, side_k, side_v
+            finally:
+                _wait_device(self.cache.device)  # the pins hold until the reads have executed
 
     def decode(self, token: int, key: torch.Tensor, value: torch.Tensor,
                canonical_slot: int | None = None) -> int:

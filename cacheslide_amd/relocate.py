@@ -8,7 +8,8 @@ paged.py:205-240); these entry points run it for every layer and chunk of a
 step in a handful of launches.  All moves are byte copies (bit-exact).
 
 Cache views are [L, blocks, H, bs, 2D] (or a single layer [blocks, H, bs, 2D]).
-Sources and destinations of one call must be disjoint.
+Sources and destinations of one call must be disjoint (checked unless the
+caller passes ``check=False``).
 """
 
 from __future__ import annotations
@@ -27,27 +28,46 @@ def _long(t: Tensor, device) -> Tensor:
     return t
 
 
-def copy_pages(cache: Tensor, src_blocks: Tensor, dst_blocks: Tensor) -> None:
-    """cache[..., dst_blocks[i], :, :, :] = cache[..., src_blocks[i], :, :, :] for every layer."""
+def _disjoint(src: Tensor, dst: Tensor, what: str) -> None:
+    """Sources and destinations of one launch must be disjoint and the
+    destinations distinct: the moves run concurrently, so an overlap races."""
+    if src.numel() == 0:
+        return
+    if bool(torch.isin(dst, src).any()) or torch.unique(dst).numel() != dst.numel():
+        raise ValueError(f"{what}: destinations must be distinct and disjoint from the sources")
+
+
+def copy_pages(cache: Tensor, src_blocks: Tensor, dst_blocks: Tensor, *, check: bool = True) -> None:
+    """cache[..., dst_blocks[i], :, :, :] = cache[..., src_blocks[i], :, :, :] for every layer.
+
+    With ``check`` the index vectors are checked for overlap first (one
+    readback); callers that build them from disjoint pools may skip it.
+    """
     device = _hip.require_device(cache)
     if src_blocks.shape != dst_blocks.shape or src_blocks.ndim != 1:
         raise ValueError("src_blocks and dst_blocks must be matching vectors")
-    call("cs_page_copy", vref(cache), ptr(_long(src_blocks, device)), ptr(_long(dst_blocks, device)),
-         src_blocks.numel(), _hip.stream_of(device))
+    src, dst = _long(src_blocks, device), _long(dst_blocks, device)
+    if check:
+        _disjoint(src, dst, "copy_pages")
+    call("cs_page_copy", vref(cache), ptr(src), ptr(dst), src.numel(), _hip.stream_of(device))
 
 
-def copy_slots(cache: Tensor, src_slots: Tensor, dst_slots: Tensor) -> None:
+def copy_slots(cache: Tensor, src_slots: Tensor, dst_slots: Tensor, *, check: bool = True) -> None:
     """Copy token records (all layers, heads, K and V) from src_slots[i] to dst_slots[i]."""
     device = _hip.require_device(cache)
     if src_slots.shape != dst_slots.shape or src_slots.ndim != 1:
         raise ValueError("src_slots and dst_slots must be matching vectors")
-    call("cs_slot_copy", vref(cache), ptr(_long(src_slots, device)), ptr(_long(dst_slots, device)),
-         src_slots.numel(), _hip.stream_of(device))
+    src, dst = _long(src_slots, device), _long(dst_slots, device)
+    if check:
+        _disjoint(src, dst, "copy_slots")
+    call("cs_slot_copy", vref(cache), ptr(src), ptr(dst), src.numel(), _hip.stream_of(device))
 
 
 def scatter_mapping(mapping: Tensor, tokens: Tensor, slots: Tensor) -> None:
     """mapping[tokens[i]] = slots[i] (tokens outside the map are ignored)."""
     device = _hip.require_device(mapping)
+    if tokens.numel() != slots.numel():
+        raise ValueError("tokens and slots must have the same length")
     call("cs_mapping_scatter", ptr(_long(mapping, device)), mapping.numel(),
          ptr(_long(tokens, device)), ptr(_long(slots, device)), tokens.numel(),
          _hip.stream_of(device))
@@ -87,12 +107,20 @@ class SlotFreeList:
         self._status = torch.zeros(1, dtype=torch.int32, device=self.device)
 
     def release(self, slots: Tensor) -> None:
+        if slots.ndim != 1:
+            raise ValueError("slots must be a vector")
         call("cs_freelist_release", ptr(self.bitmap), self.nbits, ptr(_long(slots, self.device)),
              slots.numel(), _hip.stream_of(self.device))
 
     def acquire(self, count: int, out: Tensor | None = None, *, check: bool = True) -> Tensor:
+        if type(count) is not int or count < 0:
+            raise ValueError("count must be a nonnegative integer")
         if out is None:
             out = torch.empty(max(count, 1), dtype=torch.long, device=self.device)
+        else:
+            out = _long(out, self.device)
+            if out.numel() < count:
+                raise ValueError(f"out holds {out.numel()} slots, acquire needs {count}")
         call("cs_freelist_acquire", ptr(self.bitmap), self.nbits, count, ptr(out), ptr(self._status),
              _hip.stream_of(self.device))
         if check and int(self._status.item()) == _hip.CS_ECAPACITY:

@@ -71,7 +71,11 @@ enum cs_flag {
   CS_FLAG_SCORE_NONFINITE = 1 << 10,  /* position.py:519-520 */
   CS_FLAG_E_NONFINITE = 1 << 11,
   CS_FLAG_POS_NONFINITE = 1 << 12,    /* validate: positions not finite */
-  CS_FLAG_BLOCK_INVALID = 1 << 13,    /* a block-table entry outside the cache */
+  CS_FLAG_BLOCK_INVALID = 1 << 13,    /* a block-table entry or slot outside the cache */
+  CS_FLAG_NO_KEY = 1 << 14,           /* decode: a context length < 1 (position.py:149-150
+                                         "attention requires at least one key") */
+  CS_FLAG_CONTEXT_RANGE = 1 << 15,    /* decode: a context length above the max_nk the
+                                         workspace was sized for */
   /* strict contextual-path checks, position.py:99-114, in the reference's order */
   CS_FLAG_PATH_NEGATIVE = 1 << 16,
   CS_FLAG_PATH_AVAILABLE = 1 << 17,
@@ -189,12 +193,22 @@ int cs_canonical_substitute(cs_view* result, const cs_view* canonical,
 
 /* ------------------------------------------------------------------------ *
  * CCPE fast paths: bf16, D = Dv = 128, key positions 0..nk-1, no masks.
- * K/V are read either from dense [nk, Hkv, 128] views or from the paged
- * cache [blocks, Hkv, block_size, 256] (K = [..., :128], V = [..., 128:]) via
- * an int32 block table [B, max_blocks].
+ * K/V of key j of request b are read from one of three sources:
+ *   dense  (block_table == NULL, slots == NULL): k, v [B][nk, Hkv, 128];
+ *   blocks (block_table != NULL): the paged cache [blocks, Hkv, block_size, 256]
+ *          (K = [..., :128], V = [..., 128:]) at block block_table[b, j / bs],
+ *          offset j % bs -- the canonical slot of paged.py:146-151;
+ *   slots  (slots != NULL): the per-token slot map of a SLIDE arena,
+ *          s = slots[b * slots_stride + j] (the slot NativePagedKV.gather reads
+ *          for token j, paged.py:433-472 over slide.py:264-270).  A slot below
+ *          num_blocks * block_size is native (block s / bs, offset s % bs); slot
+ *          num_blocks * block_size + i is sidecar row i of side_k / side_v
+ *          [side_rows, Hkv, 128] (paged.py:205-240), which holds selected rows
+ *          displaced by decode hole reuse (paged.py:474-524, slide.py:401-459).
+ *          A slot outside both sets CS_FLAG_BLOCK_INVALID and reads zeros.
  * ------------------------------------------------------------------------ */
 typedef struct cs_kv_source {
-  /* paged form (block_table != NULL) */
+  /* paged forms */
   const void* cache;          /* bf16 base of [blocks, Hkv, block_size, 2*128] */
   int64_t s_block, s_head, s_offset; /* element strides; dim stride must be 1 */
   int32_t block_size;
@@ -207,12 +221,21 @@ typedef struct cs_kv_source {
   const void* v;
   int64_t k_s_batch, k_s_tok, k_s_head;
   int64_t v_s_batch, v_s_tok, v_s_head;
+  /* slot form (slots != NULL; cache, strides, block_size and num_blocks as above, the
+   * block table is not read): int64 slots [B, >= nk] */
+  const int64_t* slots;
+  int64_t slots_stride;       /* elements between requests of slots */
+  const void* side_k;         /* bf16 [side_rows, Hkv, 128] or NULL */
+  const void* side_v;
+  int64_t side_s_row, side_s_head; /* element strides shared by side_k and side_v */
+  int64_t side_rows;
 } cs_kv_source;
 
 /* Prefill (position.py:404-560 for q >> 1) on MFMA.
  *   q [B, nq, Hq, 128] bf16 (strides q_s_batch/q_s_tok/q_s_head, dim stride 1)
  *   qpos [B, nq] int64 (any order, each < nk_b is not required: keys 0..min(qpos,nk-1))
- *   nk [B] int32 key counts; e [128, P] fp32 contiguous (P <= 256)
+ *   nk [B] int32 key counts; e [128, P] fp32 contiguous (P <= 128: the QE table
+ *   of a workgroup lives in LDS; larger tables take cs_ccpe_attention)
  *   out [B, nq, Hq, 128] bf16 contiguous */
 int cs_ccpe_prefill_bf16(const void* q, int64_t q_s_batch, int64_t q_s_tok, int64_t q_s_head,
                          const int64_t* qpos, int64_t qpos_s_batch, int32_t batch, int32_t nq,
@@ -221,11 +244,14 @@ int cs_ccpe_prefill_bf16(const void* q, int64_t q_s_batch, int64_t q_s_tok, int6
                          void* stream);
 
 /* cope_attention for one query row per request (position.py:404-560 as the
- * decode step calls it, runtime.py:600-609 over the paged.py:433-472 gather).
+ * decode step calls it, runtime.py:489-508 over the paged.py:433-472 gather).
  * Decode (q = 1 row per request at position nk[b]-1) with speculative
  * split-K: splits are aligned to the last key; a split whose right-hand gate
  * mass is below P-1 is recomputed exactly.  workspace must hold
- * cs_ccpe_decode_workspace_bytes(batch, hq, max_nk, split) bytes.
+ * cs_ccpe_decode_workspace_bytes(batch, hq, max_nk, split) bytes; the call
+ * refuses a smaller workspace_bytes.  A request with nk[b] < 1 sets
+ * CS_FLAG_NO_KEY and one with nk[b] > max_nk sets CS_FLAG_CONTEXT_RANGE; the
+ * output rows of such requests are not valid.
  *   q [B, Hq, 128] bf16 (q_s_batch, q_s_head), out [B, Hq, 128] bf16. */
 int64_t cs_ccpe_decode_workspace_bytes(int32_t batch, int32_t hq, int32_t max_nk,
                                        int32_t split);
@@ -233,8 +259,8 @@ int64_t cs_ccpe_decode_workspace_bytes(int32_t batch, int32_t hq, int32_t max_nk
 int cs_ccpe_decode_bf16(const void* q, int64_t q_s_batch, int64_t q_s_head, int32_t batch,
                         int32_t hq, int32_t hkv, const int32_t* nk, int32_t max_nk,
                         const cs_kv_source* kv, const float* e, int32_t max_positions,
-                        int32_t split, void* workspace, void* out, int32_t* flags,
-                        void* stream);
+                        int32_t split, void* workspace, int64_t workspace_bytes, void* out,
+                        int32_t* flags, void* stream);
 
 /* ------------------------------------------------------------------------ *
  * SLIDE slot kernels (paged.py:205-240, 433-472; slide.py:103-112).

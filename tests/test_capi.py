@@ -82,3 +82,30 @@ def test_wca_update_checks_arguments_without_a_device():
     args = _hip.CsWcaUpdateArgs()          # no status block
     assert lib.cs_wca_update(ctypes.byref(args), None) == _hip.CS_EINVAL
     assert ctypes.sizeof(_hip.CsWcaUpdateArgs) == 888   # the C struct's size on x86-64
+
+
+def test_decode_refuses_a_small_workspace_without_a_device():
+    """cs_ccpe_decode_bf16 checks workspace_bytes against the size its
+    max_nk / split / batch / heads need before any launch (host pointers stand
+    in for device buffers: nothing is dereferenced)."""
+    lib = _hip.load()
+    buf = ctypes.create_string_buffer(4096 + 16)
+    base = (ctypes.addressof(buf) + 15) // 16 * 16
+    src = _hip.CsKvSource()
+    src.cache, src.block_table = base, base
+    src.s_block, src.s_head, src.s_offset, src.block_size = 4096, 4096, 256, 16
+    src.num_blocks, src.bt_stride, src.bt_cols = 1, 1, 1
+    need = lib.cs_ccpe_decode_workspace_bytes(2, 4, 1000, 256)
+    args = [base, 512, 128, 2, 4, 1, base, 1000, ctypes.byref(src), base, 64, 256, base]
+    tail = [base, base, None]
+    assert lib.cs_ccpe_decode_bf16(*args, need - 1, *tail) == _hip.CS_EINVAL
+    assert b"workspace holds" in lib.cs_last_error()
+    # the slot form checks its sidecar alignment before any launch
+    slot_src = _hip.CsKvSource()
+    slot_src.cache, slot_src.slots = base, base
+    slot_src.s_block, slot_src.s_head, slot_src.s_offset, slot_src.block_size = 4096, 4096, 256, 16
+    slot_src.num_blocks, slot_src.side_rows = 1, 4
+    slot_src.side_k, slot_src.side_v, slot_src.side_s_row, slot_src.side_s_head = base + 2, base, 128, 128
+    args[8] = ctypes.byref(slot_src)
+    assert lib.cs_ccpe_decode_bf16(*args, need, *tail) == _hip.CS_EINVAL
+    assert b"sidecar rows must be 16-byte aligned" in lib.cs_last_error()

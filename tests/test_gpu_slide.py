@@ -288,3 +288,25 @@ def test_empty_moves_leave_the_cache_alone(device):
     torch.cuda.synchronize()
     np.testing.assert_array_equal(bits(cache), before)
     assert torch.equal(mapping.cpu(), torch.arange(10))
+
+
+def test_relocation_rejects_overlaps_and_short_buffers(device):
+    """Overlapping sources/destinations would race inside one launch; a short
+    slot list or output buffer would be read or written past its end."""
+    cache = random_bf16((1, 8, 2, 4, 16), 5).to(device)
+    before = bits(cache).copy()
+    t = lambda xs: torch.tensor(xs, dtype=torch.long, device=device)  # noqa: E731
+    with pytest.raises(ValueError, match="disjoint"):
+        relocate.copy_pages(cache, t([1, 2]), t([2, 3]))
+    with pytest.raises(ValueError, match="distinct"):
+        relocate.copy_pages(cache, t([1, 2]), t([4, 4]))
+    with pytest.raises(ValueError, match="disjoint"):
+        relocate.copy_slots(cache, t([0, 5]), t([9, 0]))
+    np.testing.assert_array_equal(bits(cache), before)   # nothing moved
+    mapping = torch.full((10,), -1, dtype=torch.long, device=device)
+    with pytest.raises(ValueError, match="same length"):
+        relocate.scatter_mapping(mapping, t([1, 2, 3]), t([7, 8]))
+    fl = relocate.SlotFreeList(64, device)
+    with pytest.raises(ValueError, match="acquire needs 5"):
+        fl.acquire(5, out=torch.empty(4, dtype=torch.long, device=device))
+    assert fl.acquire(4, out=torch.empty(4, dtype=torch.long, device=device)).tolist() == [0, 1, 2, 3]
