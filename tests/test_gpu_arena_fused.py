@@ -12,8 +12,6 @@ oracle runs on the gathered K/V.
 
 from __future__ import annotations
 
-from concurrent.futures import Future
-
 import numpy as np
 import pytest
 import torch
@@ -40,29 +38,28 @@ def cope_with(device, e):
     return cope
 
 
-def relocated_arena(device, n=600, decoded=24, hkv=2, bs=16, seed=900):
+def relocated_arena(device, n=600, decoded=24, hkv=2, bs=16, seed=900, mover=None):
     """An arena after promote_selected (sidecar rows, vacated holes), a baseline
     write, update_selected with one mirror skipped under a pin, and decode hole
-    reuse.  Returns the arena and the table column of canonical slots."""
+    reuse.  Returns the arena and its block table (int32, on ``device``)."""
     blocks_needed = (n + decoded + bs - 1) // bs
     nb = blocks_needed + 7
     table = torch.randperm(nb, generator=torch.Generator().manual_seed(seed))[:blocks_needed].tolist()
     cache = seeded((nb, hkv, bs, 256), seed + 1, dtype=torch.bfloat16).to(device)
-    arena = NativePagedKV(cache, table, n, 64, request_id="r", layer_index=3)
+    arena = NativePagedKV(cache, table, n, 64, request_id="r", layer_index=3, mover=mover)
     key = seeded((n, hkv, 128), seed + 2, dtype=torch.bfloat16).to(device)
     value = seeded((n, hkv, 128), seed + 3, dtype=torch.bfloat16).to(device)
     rng = np.random.default_rng(seed)
     selected = sorted(rng.choice(n - 1, 40, replace=False).tolist())
-    loading = Future()
     sel_k = seeded((len(selected), hkv, 128), seed + 4, dtype=torch.bfloat16).to(device)
     sel_v = seeded((len(selected), hkv, 128), seed + 5, dtype=torch.bfloat16).to(device)
-    arena.promote_selected(selected, sel_k, sel_v, load_future=loading)
-    loading.set_result(None)
-    arena.write_prefill(key, value)
-    # fused rows of the selected tokens; the canonical mirror of the first is pinned
     upd_k = seeded((len(selected), hkv, 128), seed + 6, dtype=torch.bfloat16).to(device)
     upd_v = seeded((len(selected), hkv, 128), seed + 7, dtype=torch.bfloat16).to(device)
+    arena.write_prefill(key, value)
+    # a reader pins the first selected token's canonical slot across the
+    # promotion and the fused-row update, so that slot gets no mirror
     with arena.slot_map.pin_slots([arena.canonical_slot(selected[0])]):
+        arena.promote_selected(selected, sel_k, sel_v).result()   # published once written
         arena.update_selected(selected, upd_k, upd_v)
     for t in range(n, n + decoded):
         dk = seeded((hkv, 128), seed + 100 + t, dtype=torch.bfloat16).to(device)

@@ -322,3 +322,27 @@ def test_argument_validation():
         a.write([10, 11, 12], k, v)
     with pytest.raises(TypeError):
         a.promote_selected([0], k[:1], v[:1], load_future=object())
+
+
+def test_relocated_arena_sequence_on_the_host():
+    """The arena sequence the fused-kernel GPU tests build (promotion to the
+    sidecar, baseline write, pinned-mirror update, decode hole reuse), run
+    with the host mover: the slot map names sidecar rows and reused holes,
+    and device_slots yields exactly the slots gather reads."""
+    from tests._helpers import HostMover
+    from tests.test_gpu_arena_fused import relocated_arena
+
+    arena, _ = relocated_arena(torch.device("cpu"), mover=HostMover())
+    n = arena.logical_length()
+    assert n == 624
+    stats = arena.stats()
+    assert stats["physical_hole_reuse"] > 0 and stats["canonical_mirror_writes"] > 0
+    with arena.device_slots(range(n)) as (slots, side_k, side_v):
+        snap = arena.snapshot()
+        assert slots.tolist() == [snap[t] for t in range(n)]
+        assert side_k is not None and side_v is not None
+        canonical = [arena.canonical_slot(t) for t in range(n)]
+        assert any(s >= arena.native_total_slots for s in slots.tolist())
+        assert slots.tolist() != canonical
+    gk, _ = arena.gather(range(n))
+    assert gk.shape == (n, 2, 128)
