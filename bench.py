@@ -470,7 +470,7 @@ def snapshot_measure(device, reps: int = 5) -> dict:
 
     from cacheslide_amd import RequestPlan, _hip
     from cacheslide_amd.snapshot import LayerSnapshots, SnapshotUploader, encode_snapshot
-    from cacheslide_amd.storage import TieredPageStore
+    from cacheslide_amd.pagestore import PageStore
 
     F, HKV, D = 13926, 8, 128
     shapes = {"k": (F, HKV, D), "v": (F, HKV, D)}
@@ -536,7 +536,7 @@ def snapshot_measure(device, reps: int = 5) -> dict:
         return (time.perf_counter() - t0) / L * 1e3
 
     with tempfile.TemporaryDirectory() as root:
-        store = TieredPageStore(root + "/pages", cpu_budget_bytes=(L + 1) * len(data),
+        store = PageStore(root + "/pages", cpu_budget_bytes=(L + 1) * len(data),
                                 disk_budget_bytes=(L + 1) * len(data))
         key = lambda layer: plan.cache_key("bench", layer) + "/kv"
         for layer in range(L):

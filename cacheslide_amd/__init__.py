@@ -5,7 +5,7 @@ attention (position, attention), WCA (wca, policy) and SLIDE slot management
 (slide, paged), computing on hand-written gfx950 kernels in
 _lib/libcacheslide_hip.so; plus fused paged-cache entry points (ccpe),
 batched relocation (relocate), the CCPE profile artifacts (profiles), and
-the layer snapshot pages between the RAM/SSD page store and HBM (storage,
+the layer snapshot pages between a page store and HBM (pagestore,
 snapshot).
 """
 
@@ -24,7 +24,8 @@ from .position import (
 )
 from .slide import LayerSlotMap, SlotWrite, coalesce_slot_writes
 from .snapshot import LayerSnapshots, SnapshotUploader, encode_snapshot, parse_snapshot
-from .storage import CacheCapacityError, CacheIntegrityError, StaleCompletionError, TieredPageStore
+from .errors import CacheCapacityError, CacheIntegrityError, StaleCompletionError
+from .pagestore import PageStore
 from .wca import (
     WCANumericalError,
     WCAState,
@@ -40,8 +41,8 @@ __all__ = [
     "CCPEPositionError", "CCPEProfile", "CacheCapacityError", "CacheIntegrityError",
     "CanonicalPositionPolicy", "ChunkIdentity", "CoPE",
     "CoPEPositionTrace", "LayerSlotMap", "LayerSnapshots", "NativePagedKV", "RequestPlan",
-    "SelectedAssociationPolicy", "SlotWrite", "SnapshotUploader", "StaleCompletionError",
-    "TieredPageStore", "WCAConfig",
+    "PageStore", "SelectedAssociationPolicy", "SlotWrite", "SnapshotUploader",
+    "StaleCompletionError", "WCAConfig",
     "WCANumericalError", "WCAState", "WCAUpdate", "adaptation_weight", "coalesce_slot_writes",
     "cope_attention", "encode_snapshot", "mean_head_cosine", "parse_snapshot", "squared_deviation", "validate_contextual_path",
 ]

@@ -19,7 +19,7 @@ from torch import Tensor
 
 from . import _hip
 from ._hip import call, ptr, vref
-from .storage import CacheCapacityError
+from .errors import CacheCapacityError
 
 
 def _long(t: Tensor, device) -> Tensor:

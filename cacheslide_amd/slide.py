@@ -26,7 +26,7 @@ from concurrent.futures import Future
 from contextlib import contextmanager
 from dataclasses import dataclass, field
 
-from .storage import CacheCapacityError, StaleCompletionError
+from .errors import CacheCapacityError, StaleCompletionError
 
 
 @dataclass(frozen=True)

@@ -3,8 +3,11 @@
 The reference runtime persists, per layer, the fixed tokens' K/V rows
 (``"kv"``: ``k``, ``v`` of ``[fixed, kv_heads, head_dim]``) and layer inputs
 (``"state"``: ``hidden``, ``residual`` of ``[fixed, hidden_size]``) as
-safetensors pages in a ``TieredPageStore``, and reads them back on reuse,
-prefetching the next layer's K/V while the current layer computes.
+safetensors pages in its page store, and reads them back on reuse,
+prefetching the next layer's K/V while the current layer computes.  Any store
+with ``put`` / ``read`` / ``contains`` / ``submit_load`` / ``submit_spill``
+works here; ``cacheslide_amd.pagestore.PageStore`` is the one this package
+ships.
 
 Its read path decodes the page into CPU tensors, checks them for non-finite
 values on the CPU and copies them with ``.to(device, dtype)``, all on the

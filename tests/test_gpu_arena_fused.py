@@ -118,15 +118,13 @@ def test_slot_map_batches_with_sidecar_rows(device, bs):
     side_k = seeded((side_rows, hkv, 128), 702, dtype=torch.bfloat16).to(device)
     side_v = seeded((side_rows, hkv, 128), 703, dtype=torch.bfloat16).to(device)
     native = nb * bs
-    pool = torch.randperm(native + side_rows, generator=gen)
     width = max(lens)
     slots = torch.full((len(lens), width + 5), -7, dtype=torch.long)
-    cursor = 0
     rng = np.random.default_rng(704 + bs)
     for b, n in enumerate(lens):
-        row = pool[cursor:cursor + n].clone()
-        cursor += n
-        # runs of consecutive native slots inside blocks, as after whole-block placement
+        row = torch.randint(0, native + side_rows, (n,), generator=gen)
+        # runs of consecutive native slots, as after whole-block placement
+        # (with 4-slot blocks a run of 8 spans two blocks)
         for start in range(0, n - 8, 64):
             blk = int(rng.integers(0, nb - 2))
             run = torch.arange(blk * bs, blk * bs + 8)

@@ -15,7 +15,7 @@ from safetensors.torch import save as st_save
 from cacheslide_amd import RequestPlan
 from cacheslide_amd.runtime_rows import ReuseFailure
 from cacheslide_amd.snapshot import LayerSnapshots, SnapshotUploader, encode_snapshot, parse_snapshot
-from cacheslide_amd.storage import TieredPageStore
+from cacheslide_amd.pagestore import PageStore
 
 pytestmark = pytest.mark.gpu
 
@@ -35,7 +35,7 @@ def bits(x: torch.Tensor) -> torch.Tensor:
 
 
 def snapshots(tmp_path, device, cpu=1 << 24, write_cache=True, **kwargs):
-    store = TieredPageStore(tmp_path / "pages", cpu_budget_bytes=cpu, disk_budget_bytes=1 << 26)
+    store = PageStore(tmp_path / "pages", cpu_budget_bytes=cpu, disk_budget_bytes=1 << 26)
     snaps = LayerSnapshots(store, plan(), "model", device, layers=4, kv_heads=HKV, head_dim=D,
                            hidden_size=HID, write_cache=write_cache, **kwargs)
     return store, snaps
@@ -161,7 +161,7 @@ def test_prefetch_from_disk_overlaps_and_matches(device, tmp_path):
     reader.prefetch(2, torch.bfloat16)
     reader.release()
     assert reader.kv_future is None
-    assert store.stats()["inflight_cpu_reserved_bytes"] == 0
+    assert store.stats()["inflight_loads"] == 0
     reader.uploader.close()
     store.close()
 

@@ -19,7 +19,7 @@ import torch
 
 from cacheslide_amd import paged
 from cacheslide_amd.paged import NativePagedKV
-from cacheslide_amd.storage import CacheCapacityError, StaleCompletionError
+from cacheslide_amd.errors import CacheCapacityError, StaleCompletionError
 from tests._helpers import HostMover
 
 CANONICAL = {0: 8, 1: 9, 2: 10, 3: 11, 4: 0, 5: 1, 6: 2, 7: 3, 8: 12, 9: 13}

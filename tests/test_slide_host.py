@@ -17,7 +17,7 @@ from concurrent.futures import Future
 import pytest
 
 from cacheslide_amd.slide import LayerSlotMap, SlotWrite, coalesce_slot_writes
-from cacheslide_amd.storage import CacheCapacityError, StaleCompletionError
+from cacheslide_amd.errors import CacheCapacityError, StaleCompletionError
 
 
 def done(value=None) -> Future:

@@ -20,7 +20,7 @@ from safetensors.torch import save as st_save
 from cacheslide_amd import RequestPlan
 from cacheslide_amd import snapshot as snap
 from cacheslide_amd.runtime_rows import ReuseFailure
-from cacheslide_amd.storage import TieredPageStore
+from cacheslide_amd.pagestore import PageStore
 
 HKV, D, HID = 2, 4, 8
 
@@ -67,7 +67,7 @@ def env(tmp_path, monkeypatch):
     # pages encoded from CPU tensors as the reference's _put does
     monkeypatch.setattr(snap, "encode_snapshot", lambda tensors: st_save(
         {n: t.detach().contiguous().cpu() for n, t in tensors.items()}))
-    store = TieredPageStore(tmp_path / "pages", cpu_budget_bytes=1 << 20, disk_budget_bytes=1 << 22)
+    store = PageStore(tmp_path / "pages", cpu_budget_bytes=1 << 20, disk_budget_bytes=1 << 22)
     yield store
     store.close()
 
