@@ -16,6 +16,7 @@ import torch
 _LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libcacheslide_hip.so"
 
 CS_F32, CS_F16, CS_BF16, CS_F64, CS_I32, CS_I64, CS_U8 = range(7)
+DECODE_SCRATCH_BYTES = 64 << 20  # CS_DECODE_SCRATCH_BYTES
 CS_OK, CS_EINVAL, CS_ELAUNCH, CS_EUNSUPPORTED, CS_ECAPACITY = range(5)
 
 FLAG_Q_NONFINITE = 1 << 0
@@ -170,6 +171,11 @@ SIGNATURES = {
         _I32,
         [_P, _I64, _I64, _I32, _I32, _I32, _P, _I32, ctypes.POINTER(CsKvSource), _P,
          _I32, _I32, _P, _I64, _P, _P, _P],
+    ),
+    "cs_ccpe_decode_bf16_noalloc": (
+        _I32,
+        [_P, _I64, _I64, _I32, _I32, _I32, _P, _I32, ctypes.POINTER(CsKvSource), _P,
+         _I32, _I32, _P, _P, _P],
     ),
     "cs_slot_scatter": (_I32, [_VP, _VP, _VP, _P, _P, _I64, _VP, _VP, _P]),
     "cs_slot_gather": (_I32, [_VP, _VP, _VP, _P, _P, _I64, _VP, _VP, _P]),

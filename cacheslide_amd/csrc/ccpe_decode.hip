@@ -30,6 +30,8 @@
 
 #include "common.h"
 
+#include <mutex>
+
 namespace cs {
 namespace {
 
@@ -969,7 +971,75 @@ int launch_decode(decode_params& p, void* workspace, void* stream) {
   return CS_OK;
 }
 
+// Workspace of cs_ccpe_decode_bf16_noalloc: a static device array, one copy
+// per GPU, alive until the process ends.  Host code never passes `scratch`
+// itself to a kernel (on the host it names a stand-in, not device memory): it
+// uses the address hipGetSymbolAddress returns for the current device.
+static __device__ __align__(256) unsigned char scratch[CS_DECODE_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device, looked up on the first
+// call on that device.
+int scratch_address(void* stream, void** out) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) {
+    set_error("hipGetDevice: %s", hipGetErrorString(err));
+    return CS_ELAUNCH;
+  }
+  CS_REQUIRE(dev >= 0 && dev < kMaxDevices, "device ordinal %d out of range", dev);
+  if (stream != nullptr) {
+    int sdev = -1;
+    err = hipStreamGetDevice(as_stream(stream), &sdev);
+    if (err != hipSuccess) {
+      set_error("hipStreamGetDevice: %s", hipGetErrorString(err));
+      return CS_ELAUNCH;
+    }
+    CS_REQUIRE(sdev == dev, "the stream belongs to device %d but device %d is current", sdev, dev);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || ptr == nullptr) {
+      set_error("hipGetSymbolAddress(scratch): %s", hipGetErrorString(err));
+      return CS_ELAUNCH;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return CS_OK;
+}
+
 }  // namespace
+
+extern "C" int cs_ccpe_decode_bf16_noalloc(const void* q, int64_t q_s_batch, int64_t q_s_head,
+                                           int32_t batch, int32_t hq, int32_t hkv,
+                                           const int32_t* nk, int32_t max_nk,
+                                           const cs_kv_source* kv, const float* e,
+                                           int32_t max_positions, int32_t split, void* out,
+                                           int32_t* flags, void* stream) {
+  decode_params p{};
+  const int st = prepare_decode(q, q_s_batch, q_s_head, batch, hq, hkv, nk, max_nk, kv, e,
+                                max_positions, split, out, flags, &p);
+  if (st) return st;
+  const int64_t need = cs_ccpe_decode_workspace_bytes(batch, hq, max_nk, split);
+  CS_REQUIRE(need <= CS_DECODE_SCRATCH_BYTES,
+             "the call needs %lld bytes of decode workspace; the static scratch holds %lld "
+             "(lower batch x heads x ceil(max_nk / split), or use cs_ccpe_decode_bf16)",
+             static_cast<long long>(need), static_cast<long long>(CS_DECODE_SCRATCH_BYTES));
+  if (batch == 0) return CS_OK;
+  void* ws = nullptr;
+  const int sst = scratch_address(stream, &ws);
+  if (sst) return sst;
+  // every workspace field the kernels read is written earlier in the same call
+  // (the queue counter by the first workgroup of the main launch), so the
+  // previous call's contents need no clearing
+  return launch_decode(p, ws, stream);
+}
 
 extern "C" int cs_ccpe_decode_bf16(const void* q, int64_t q_s_batch, int64_t q_s_head,
                                    int32_t batch, int32_t hq, int32_t hkv, const int32_t* nk,

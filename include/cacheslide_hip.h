@@ -262,6 +262,25 @@ int cs_ccpe_decode_bf16(const void* q, int64_t q_s_batch, int64_t q_s_head, int3
                         int32_t split, void* workspace, int64_t workspace_bytes, void* out,
                         int32_t* flags, void* stream);
 
+/* Bytes of the static device scratch behind cs_ccpe_decode_bf16_noalloc. */
+#define CS_DECODE_SCRATCH_BYTES (64ll << 20)
+
+/* cs_ccpe_decode_bf16 without a caller workspace, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  It has no counterpart in the reference.
+ * The workspace is a static device array of CS_DECODE_SCRATCH_BYTES per GPU,
+ * held until the process ends; a call whose
+ * cs_ccpe_decode_workspace_bytes(batch, hq, max_nk, split) exceeds it is
+ * refused (CS_EINVAL).  Runs on the current device (the stream must belong
+ * to it) and allocates nothing.  Every call on one GPU shares the array, so
+ * calls that overlap on one GPU (different streams, or threads without
+ * ordering) race; calls ordered on one stream do not. */
+int cs_ccpe_decode_bf16_noalloc(const void* q, int64_t q_s_batch, int64_t q_s_head,
+                                int32_t batch, int32_t hq, int32_t hkv, const int32_t* nk,
+                                int32_t max_nk, const cs_kv_source* kv, const float* e,
+                                int32_t max_positions, int32_t split, void* out, int32_t* flags,
+                                void* stream);
+
 /* ------------------------------------------------------------------------ *
  * SLIDE slot kernels (paged.py:205-240, 433-472; slide.py:103-112).
  * cache [blocks, H, bs, 2D] any dtype; side_k/side_v [S, H, D] (may be absent).
