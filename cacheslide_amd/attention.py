@@ -22,6 +22,11 @@ from .contracts import RequestPlan
 from .position import ChunkIdentity, validate_contextual_path
 
 
+CHUNK_HAS_FIXED_ROW = 1 << 30   # kernel chunk flag: the chunk holds a fixed query row
+CHUNK_UNKNOWN_ROW = 1 << 29     # ... one whose ordinal the profile has no trace for
+CHUNK_CANON_OUT_OF_RANGE = 1 << 28  # a substituted canonical cell outside [0, P-1]
+
+
 class _LoweredCanonical:
     """Kernel inputs for one CanonicalPositionPolicy over one call's coordinates."""
 
@@ -72,11 +77,18 @@ class _LoweredCanonical:
     def any_fixed_row(self) -> bool:
         return bool((self.q_rows != -1).any().item())
 
-    def raise_lookup_error(self) -> None:
-        """The ValueError profile.lookup raises for a chunk with fixed rows."""
+    def raise_lookup_error(self, chunk_bits: int | None = None) -> None:
+        """The ValueError profile.lookup raises for a chunk with fixed rows
+        (position.py:718-738): a plan/profile mismatch for any such chunk, an
+        untraced query ordinal only for a chunk that holds one (kernel chunk
+        bit 29; without chunk bits, any row of the call)."""
         if self.reason:
             raise ValueError(self.reason)
-        if self.unknown and -2 in self.q_rows.cpu().tolist():
+        if chunk_bits is None:
+            untraced = self.unknown and -2 in self.q_rows.cpu().tolist()
+        else:
+            untraced = bool(chunk_bits & CHUNK_UNKNOWN_ROW)
+        if untraced:
             raise ValueError("CCPE profile has no contextual trace for these query positions")
 
 

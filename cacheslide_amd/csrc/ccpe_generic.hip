@@ -27,6 +27,8 @@ namespace {
 constexpr int kGenWaves = 2;
 constexpr int kMaxDvChunks = 8;  // Dv <= 512
 constexpr int32_t kChunkHasFixedRow = 1 << 30;
+constexpr int32_t kChunkUnknownRow = 1 << 29;  // a fixed row the profile has no trace for
+constexpr int32_t kChunkCanonOutOfRange = 1 << 28;  // a substituted canonical cell outside [0, P-1]
 
 __device__ inline void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -340,19 +342,26 @@ __global__ void __launch_bounds__(64 * kGenWaves) ccpe_generic_kernel(gen_params
       }
     }
   }
-  if (bad_pos) local_flags |= CS_FLAG_POS_INVALID;
+  // With canonical substitution the contextual cells are clamped into range,
+  // so an out-of-range position is a canonical cell: the reference rejects it
+  // in the transform's bounds check of its chunk (position.py:500-515), in
+  // chunk order with the policy's other errors.
+  const bool canon_oob = bad_pos && g.canon && contextual;
+  if (bad_pos && !canon_oob) local_flags |= CS_FLAG_POS_INVALID;
   // one atomic per wave
   int all_flags = local_flags;
   for (int off = 32; off > 0; off >>= 1) all_flags |= __shfl_xor(all_flags, off, 64);
-  int all_path = path_bits;
+  int all_path = path_bits | (canon_oob ? kChunkCanonOutOfRange : 0);
   for (int off = 32; off > 0; off >>= 1) all_path |= __shfl_xor(all_path, off, 64);
   if (lane == 0) {
     if (all_flags) atomicOr(g.flags, all_flags);
     // q_ord == -2 marks a fixed row whose ordinal the profile does not cover:
     // no substitution, but the chunk still counts as holding a fixed row.
     const bool fixed_row = g.canon && g.q_ord && g.q_ord[row] != -1;
+    const bool unknown_row = g.canon && g.q_ord && g.q_ord[row] == -2;
     if (g.chunk_flags && (all_path || fixed_row))
-      atomicOr(&g.chunk_flags[row / g.chunk_rows], all_path | (fixed_row ? kChunkHasFixedRow : 0));
+      atomicOr(&g.chunk_flags[row / g.chunk_rows], all_path | (fixed_row ? kChunkHasFixedRow : 0) |
+                                                        (unknown_row ? kChunkUnknownRow : 0));
   }
 }
 

@@ -632,18 +632,27 @@ def cope_attention(
     return output
 
 
+_TRANSFORM_BOUNDS_MESSAGE = ("positions_transform must return bounded finite positions "
+                             "with the contextual shape, dtype and device")
+
+
 def _raise_policy_errors(ck: _Checks, chunk_flags: Tensor, lowered) -> None:
-    """First chunk holding a fixed query row: profile lookup, then path checks."""
+    """In chunk order, the first chunk holding a fixed query row that fails:
+    profile lookup, then the strict path checks, then the bounds of the
+    substituted positions (position.py:485-516 with attention.py:32-57)."""
+    from .attention import CHUNK_CANON_OUT_OF_RANGE, CHUNK_HAS_FIXED_ROW
+
     ck.finish()
     values = _hip.read_flags(chunk_flags)
-    has_fixed = 1 << 30
     for value in values:
-        if not value & has_fixed:
+        if not value & CHUNK_HAS_FIXED_ROW:
             continue
-        lowered.raise_lookup_error()
-        for bit, text in _PATH_MESSAGES:
+        lowered.raise_lookup_error(value)
+        for bit, text in _PATH_MESSAGES:      # strict validation inside the transform
             if value & bit:
                 raise CCPEPositionError(text)
+        if value & CHUNK_CANON_OUT_OF_RANGE:  # then the bounds check of its result
+            raise CCPEPositionError(_TRANSFORM_BOUNDS_MESSAGE)
 
 
 def _fast_path_ok(query, key, value, e, cope, amask, visibility_mask, fixed_positions, canonical,
@@ -701,8 +710,7 @@ def _chunked_attention(query, key, value, cope, query_positions, key_positions, 
                            "attention logits overflowed the accumulation dtype")
             cc.finish()
             transformed = positions_transform(contextual, qpos, key_positions)
-            message = ("positions_transform must return bounded finite positions "
-                       "with the contextual shape, dtype and device")
+            message = _TRANSFORM_BOUNDS_MESSAGE
             if (
                 not isinstance(transformed, Tensor)
                 or transformed.shape != contextual.shape

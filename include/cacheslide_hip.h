@@ -124,7 +124,12 @@ int cs_check_bias_positions(const cs_view* positions, int64_t max_positions,
  *   canonical [Hq, F, F] with q_ord [nq], k_ord [nk] (int64, -1 = not fixed):
  *       CanonicalPositionPolicy lowering; strict != 0 runs the path checks and
  *       ORs CS_FLAG_PATH_* into chunk_flags[r / chunk_rows], plus bit 30 for a
- *       chunk holding a fixed query row (the policy validates only those).
+ *       chunk holding a fixed query row (the policy validates only those) and
+ *       bit 29 for a chunk holding a fixed row with q_ord == -2 (an ordinal
+ *       the profile has no trace for: CCPEProfile.lookup raises, position.py:
+ *       733-738) and bit 28 for a chunk with a substituted canonical value
+ *       outside [0, P-1] (the transform bounds check, position.py:500-515;
+ *       not reported as CS_FLAG_POS_INVALID).
  *   out [nq, Hq, Dv] (dtype of v) or NULL;  pos_out [Hq, nq, nk] or NULL.
  * ------------------------------------------------------------------------ */
 typedef struct cs_ccpe_args {

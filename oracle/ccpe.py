@@ -27,6 +27,9 @@ PATH_MESSAGES = {
     "available": "causal contextual count exceeds available gates",
     "nonincreasing": "causal contextual path must be nonincreasing",
     "gap": "causal contextual path exceeds one gate per token",
+    # the bounds check of a positions_transform result (position.py:504-516)
+    "transform": "positions_transform must return bounded finite positions "
+                 "with the contextual shape, dtype and device",
 }
 
 
@@ -139,6 +142,9 @@ def cope_attention(
             positions = fixed_positions[:, start:end]
         if positions_transform is not None:
             positions = positions_transform(positions, qpos[start:end], kpos)
+            # position.py:504-516: a transform's result must be finite and in [0, P-1]
+            if not np.isfinite(positions).all() or (positions < 0).any() or (positions > npos - 1).any():
+                raise PathError("transform")
         lg = (lg + positional_bias(qc, e, positions)).astype(acc)
         vis = None
         if visibility_mask is not None:
