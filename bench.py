@@ -8,9 +8,13 @@ paged KV with block size 16 and seeded random-permutation block tables.  One
 step is one launch of the fused MFMA prefill kernel over the whole batch,
 reading K/V through the block table.
 
-Also reported: the decode kernel at the 64-request x 32k-context shape (one
-layer's distinct KV, 8.6 GB, per call), and the CPU baseline (the numpy
-oracle, bounded sample, same op order as the reference).
+Also reported, each in a sub-record of the same JSON line: the decode
+kernel at the 64-request x 32k-context shape (one layer's distinct KV, 8.6 GB
+per call, one request checked against the oracle), the SLIDE relocation step,
+the WCA update, the selective-prefill rows and the layer-snapshot reads.  The
+CPU baselines time the torch CPU restatement of the reference path
+(oracle/torch_cpu.py, the reference's op order) on bounded samples of the
+same workloads, with all host threads torch uses and with one thread.
 
 Prints one JSON line.  Only one GPU is used: --gpus above 1 exits.
 """
@@ -145,36 +149,219 @@ def spot_check_prefill(inputs, host, shape):
     return worst
 
 
-def cpu_baseline(host, shape, heads: int):
-    """Oracle (numpy, reference op order, 64-row query chunks) on batch item 0 and
-    the first `heads` query heads of KV head 0 (one GQA group), all N rows."""
-    import numpy as np
-
-    from oracle import ccpe as orc
-
+def cpu_model() -> str:
     try:
-        from threadpoolctl import threadpool_info
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-    except Exception:  # pragma: no cover - informational only
-        threads = 1
+
+def cpu_median_s(fn, repeats: int = 3) -> float:
+    """One warm-up call, then the median wall time of ``repeats`` calls."""
+    fn()
+    times = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2]
+
+
+def with_threads(n: int, fn):
+    import torch
+
+    old = torch.get_num_threads()
+    torch.set_num_threads(n)
+    try:
+        return fn()
+    finally:
+        torch.set_num_threads(old)
+
+
+def rows_flops(rows, heads: int, d: int, p: int) -> float:
+    """Causal-triangle FLOPs of the given query rows: 4 heads D (r + 1) per
+    row for QK^T and PV plus 2 heads D P per row for Q.E (the prefill formula
+    restricted to a row subset)."""
+    return float(sum(4.0 * heads * d * (int(r) + 1) + 2.0 * heads * d * p for r in rows))
+
+
+def cpu_baseline(host, shape) -> dict:
+    """The torch CPU restatement of cope_attention (oracle/torch_cpu.py, the
+    reference's op order with 64-row query chunks) on the box's host cores:
+    batch item 0 of the prefill workload, all 32 query heads, every fourth of
+    its 4096 rows (each against all keys, as the reference computes them);
+    one warm-up, median of 3.  The one-thread figure runs one GQA group
+    (4 query heads) over every eighth row."""
+    import torch
+
+    from oracle import torch_cpu as tc
+
     N, D, P = shape["N"], shape["D"], shape["P"]
-    q = host["q"][0, :, :heads].float().numpy()
-    k = host["k"][0, :, :1].float().numpy()
-    v = host["v"][0, :, :1].float().numpy()
-    e = host["e"].numpy()
-    t0 = time.perf_counter()
-    orc.cope_attention(q, k, v, e, np.arange(N), query_chunk_size=64)
-    seconds = time.perf_counter() - t0
-    flops = prefill_flops(1, heads, N, D, P)
+    q, k, v, e = host["q"][0], host["k"][0], host["v"][0], host["e"]
+    rows4, rows8 = torch.arange(0, N, 4), torch.arange(0, N, 8)
+    threads = torch.get_num_threads()
+    t_all = cpu_median_s(lambda: tc.cope_attention(q[rows4], k, v, e, rows4))
+    t_one = with_threads(1, lambda: cpu_median_s(
+        lambda: tc.cope_attention(q[rows8, :4], k[:, :1], v[:, :1], e, rows8)))
+    flops_all = rows_flops(rows4.tolist(), shape["HQ"], D, P)
+    flops_one = rows_flops(rows8.tolist(), 4, D, P)
     return {
-        "value": round(flops / seconds / 1e12, 6),
+        "value": round(flops_all / t_all / 1e12, 6),
         "unit": "TFLOP/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"oracle/ccpe.py cope_attention (numpy, query_chunk_size 64) on batch item 0, "
-                  f"{heads} of 32 query heads (one GQA group), all {N} rows: "
-                  f"{flops / 1e9:.1f} GFLOP in {seconds:.2f} s on os.cpu_count()={os.cpu_count()}",
+        "sample": f"oracle/torch_cpu.py cope_attention (torch on the CPU, reference op order, 64-row "
+                  f"query chunks) on batch item 0 of the workload: 32 heads x every 4th of {N} rows, "
+                  f"{flops_all / 1e9:.0f} of the workload's "
+                  f"{prefill_flops(8, shape['HQ'], N, D, P) / 1e9:.0f} GFLOP; median of 3 after one "
+                  f"warm-up: {t_all:.2f} s",
+        "one_thread_value": round(flops_one / t_one / 1e12, 6),
+        "one_thread_sample": f"4 query heads (one GQA group) x every 8th row, median {t_one:.2f} s",
+        "cpu_model": cpu_model(),
+        "os_cpu_count": os.cpu_count(),
+    }
+
+
+def cpu_decode_leg(ctx: int = 32769, requests: int = 2) -> dict:
+    """The reference decode step on the host (oracle/torch_cpu.py decode_step:
+    advanced-indexing gather of the request's canonical slots, then
+    cope_attention at one row) for ``requests`` of the 64 requests of one layer,
+    32q/8kv heads, bf16 cache; scaled to one layer-step of 64 requests."""
+    import torch
+
+    from oracle import torch_cpu as tc
+
+    BS, HQ, HKV, D, P = 16, 32, 8, 128, 64
+    per = (ctx + BS - 1) // BS
+    g = torch.Generator().manual_seed(5100)
+    cache = torch.randn((requests * per, HKV, BS, 2 * D), generator=g).to(torch.bfloat16)
+    table = torch.randperm(requests * per, generator=g).to(torch.int32).view(requests, per)
+    q = torch.randn((requests, 1, HQ, D), generator=g).to(torch.bfloat16)
+    e = torch.randn((D, P), generator=g) * 0.02
+
+    def run(n_req):
+        for b in range(n_req):
+            tc.decode_step(cache, table[b], ctx, q[b], e)
+
+    threads = torch.get_num_threads()
+    t_all = cpu_median_s(lambda: run(requests))
+    t_one = with_threads(1, lambda: cpu_median_s(lambda: run(1)))
+    kv = ctx * HKV * D * 2 * 2
+    return {
+        "value_GBs": round(requests * kv / t_all / 1e9, 3),
+        "layer_step_ms_64_requests": round(t_all / requests * 64 * 1e3, 1),
+        "tok_per_s_32_layers": round(64 / (32 * t_all / requests * 64), 3),
+        "cores": threads,
+        "one_thread_GBs": round(kv / t_one / 1e9, 3),
+        "kind": "port",
+        "sample": f"{requests} of 64 requests x {ctx} keys (one layer), median of 3 after one warm-up; "
+                  f"64-request layer-step time scaled linearly",
+    }
+
+
+def cpu_slide_leg(blocks: int = 10_000, chunks: int = 51) -> dict:
+    """The relocation step on the host (oracle/torch_cpu.py relocate: advanced
+    indexing on the [blocks, 8, 16, 256] bf16 layout, the map update and the
+    freed slots) for one layer of 10k blocks and 51 chunks of 64..2048 tokens
+    (a tenth of the device workload's chunks, one of its 32 layers)."""
+    import numpy as np
+    import torch
+
+    from oracle import torch_cpu as tc
+
+    BS, HKV, REC = 16, 8, 256
+    rng = np.random.default_rng(3100)
+    lens = rng.integers(64, 2049, chunks)
+    pages = [(int(n) + BS - 1) // BS for n in lens]
+    perm = rng.permutation(blocks)
+    need = sum(pages)
+    src_blk, dst_blk = perm[:need], perm[need:2 * need]
+    fs, fd, ps, pd, slot_all = [], [], [], [], []
+    at = 0
+    for n, pg in zip(lens.tolist(), pages):
+        sb, db = src_blk[at:at + pg], dst_blk[at:at + pg]
+        at += pg
+        nfull = n // BS
+        fs += sb[:nfull].tolist()
+        fd += db[:nfull].tolist()
+        for t in range(nfull * BS, n):
+            ps.append(int(sb[t // BS]) * BS + t % BS)
+            pd.append(int(db[t // BS]) * BS + t % BS)
+        slot_all += (np.repeat(db, BS)[:n] * BS + np.tile(np.arange(BS), pg)[:n]).tolist()
+    T = int(lens.sum())
+    cache = torch.empty((blocks, HKV, BS, REC), dtype=torch.bfloat16)
+    cache.view(torch.int16).random_(generator=torch.Generator().manual_seed(3101))
+    L = lambda xs: torch.tensor(xs, dtype=torch.long)  # noqa: E731
+    fs, fd, ps, pd, slots = L(fs), L(fd), L(ps), L(pd), L(slot_all)
+    tokens = torch.arange(T)
+    mapping = torch.full((T,), -1, dtype=torch.long)
+    step = lambda: tc.relocate(cache, fs, fd, ps, pd, mapping, tokens, slots)  # noqa: E731
+    threads = torch.get_num_threads()
+    t_all = cpu_median_s(step)
+    t_one = with_threads(1, lambda: cpu_median_s(step))
+    moved = (fs.numel() * BS + ps.numel()) * HKV * REC * 2
+    traffic = 2 * moved + T * 8 * 3
+    return {
+        "value_GBs": round(traffic / t_all / 1e9, 3),
+        "cores": threads,
+        "one_thread_GBs": round(traffic / t_one / 1e9, 3),
+        "kind": "port",
+        "sample": f"1 layer x [{blocks} blocks, 8, 16, 256] bf16, {chunks} chunks ({T} tokens), "
+                  f"median of 3 after one warm-up",
+    }
+
+
+def cpu_wca_leg(layers: int = 31) -> dict:
+    """WCA on the host (oracle/torch_cpu.py WCA, float64 as wca.py): one
+    request of 16384 tokens x 8 heads x 128, bf16, fraction 0.15: initialize,
+    then ``layers`` layer updates with the runtime's finite checks."""
+    import torch
+
+    from oracle import torch_cpu as tc
+
+    T, H, D = 16384, 8, 128
+    g = torch.Generator().manual_seed(4100)
+    new_k = torch.randn((T, H, D), generator=g).to(torch.bfloat16)
+    new_v = torch.randn((T, H, D), generator=g).to(torch.bfloat16)
+    old_k = (new_k.float() + 0.05 * torch.randn((T, H, D), generator=g)).to(torch.bfloat16)
+    old_v = (new_v.float() + 0.05 * torch.randn((T, H, D), generator=g)).to(torch.bfloat16)
+    reused = torch.ones(T, dtype=torch.bool)
+    reused[-1] = False
+    mandatory = ~reused
+    state = {}
+
+    def init():
+        state["st"] = tc.WCA(old_k, new_k, reused, mandatory)
+
+    def updates(count=layers):
+        st = tc.WCA(old_k, new_k, reused, mandatory)
+        for layer in range(2, 2 + count):
+            idx = st.active
+            st.update(layer, old_k, old_v, new_k[idx], new_v[idx])
+
+    threads = torch.get_num_threads()
+    t_init = cpu_median_s(init)
+    t_traj = cpu_median_s(updates)
+    t_upd = (t_traj - t_init) / layers
+    a = int(state["st"].active.numel())
+    upd_bytes = 2 * T * H * D * 2 + 6 * a * H * D * 2
+    # one thread: a 7-layer trajectory (layers 2..8, two of them gate layers)
+    short = lambda: updates(7)  # noqa: E731
+    t_one_init = with_threads(1, lambda: cpu_median_s(init))
+    t_one_upd = (with_threads(1, lambda: cpu_median_s(short)) - t_one_init) / 7
+    return {
+        "update_ms_per_layer": round(t_upd * 1e3, 3),
+        "update_GBs": round(upd_bytes / t_upd / 1e9, 3),
+        "initialize_ms_per_request": round(t_init * 1e3, 2),
+        "cores": threads,
+        "one_thread_update_ms_per_layer": round(t_one_upd * 1e3, 3),
+        "one_thread_initialize_ms_per_request": round(t_one_init * 1e3, 2),
+        "kind": "port",
+        "sample": f"1 of 4 requests: initialize + {layers} layer updates (one thread: 7), median of 3 "
+                  f"after one warm-up",
     }
 
 
@@ -215,6 +402,15 @@ def decode_measure(device, steps: int, warmup: int):
     ms = time_steps(step, steps, warmup)
     kv_bytes = B * CTX * HKV * D * 2 * 2
     gbs = kv_bytes / (ms * 1e-3) / 1e9
+    # sampled parity: request 0 at full context against the oracle
+    import numpy as np
+
+    from oracle import ccpe as orc
+
+    recs = cache[table[0].long()].permute(0, 2, 1, 3).reshape(-1, HKV, 2 * D)[:CTX].float().cpu().numpy()
+    expected = orc.cope_attention(q[:1].float().cpu().numpy(), recs[..., :D], recs[..., D:],
+                                  e.float().cpu().numpy(), np.array([CTX - 1]))
+    check_err = float(np.abs(out[:1].float().cpu().numpy() - expected).max())
     del cache
     torch.cuda.empty_cache()
     return {
@@ -225,6 +421,7 @@ def decode_measure(device, steps: int, warmup: int):
         "achieved_GBs": round(gbs, 1),
         "hbm_frac": round(gbs / PEAK_HBM_GBS, 4),
         "tok_per_s_attention_32_layers": round(B / (32 * ms * 1e-3), 1),
+        "spot_check_max_abs_err": round(check_err, 5),
     }
 
 
@@ -370,6 +567,7 @@ def wca_measure(device, layers: int = 31) -> dict:
         "update_ms_per_layer": round(upd_s * 1e3 / n_upd, 4),
         "active_rows_per_update": round(rows / n_upd, 1),
         "update_GBs": round(upd_bytes / upd_s / 1e9, 1),
+        "update_hbm_frac": round(upd_bytes / upd_s / 1e9 / PEAK_HBM_GBS, 4),
         "note": "wall-clock per call, host validation and the one status readback per call "
                 "included (transactional API); update bytes = finite checks of the cached K/V "
                 "plus 6 row passes",
@@ -626,7 +824,6 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--cpu-heads", type=int, default=2)
     ap.add_argument("--no-slide", action="store_true")
     ap.add_argument("--slide-layers", type=int, default=32)
     ap.add_argument("--no-wca", action="store_true")
@@ -707,7 +904,17 @@ def main() -> int:
         note(f"snapshot: decode {record['snapshot']['decode_ms_per_page']} ms/page, "
              f"layer loop {record['snapshot']['layer_loop']}")
     if not args.no_cpu_baseline:
-        record["cpu_baseline"] = cpu_baseline(host, shape, args.cpu_heads)
+        note("cpu baseline: prefill")
+        record["cpu_baseline"] = cpu_baseline(host, shape)
+        if "decode" in record:
+            note("cpu baseline: decode")
+            record["decode"]["cpu_baseline"] = cpu_decode_leg()
+        if "slide" in record:
+            note("cpu baseline: slide")
+            record["slide"]["cpu_baseline"] = cpu_slide_leg()
+        if "wca" in record:
+            note("cpu baseline: wca")
+            record["wca"]["cpu_baseline"] = cpu_wca_leg()
     print(json.dumps(record), flush=True)
     return 0
 
