@@ -268,7 +268,7 @@ __device__ inline void hist_add(int* hist, int bin) {
 // scratch[n..n+k).  Skips everything
 // (count 0) when abort_flags has a bit of abort_mask set, so a failed update
 // leaves the selection unchanged.
-__global__ void __launch_bounds__(kSelThreads) wca_promote_kernel(
+__device__ void promote_block(
     const double* key, const uint8_t* candidate, const uint8_t* removed, uint8_t* selected,
     int64_t n, int64_t budget, int64_t* scratch, int64_t* count_out,
     const int32_t* abort_flags, int32_t abort_mask) {
@@ -407,6 +407,14 @@ __global__ void __launch_bounds__(kSelThreads) wca_promote_kernel(
   }
 }
 
+__global__ void __launch_bounds__(kSelThreads) wca_promote_kernel(
+    const double* key, const uint8_t* candidate, const uint8_t* removed, uint8_t* selected,
+    int64_t n, int64_t budget, int64_t* scratch, int64_t* count_out,
+    const int32_t* abort_flags, int32_t abort_mask) {
+  promote_block(key, candidate, removed, selected, n, budget, scratch, count_out, abort_flags,
+                abort_mask);
+}
+
 // Second half of the promotion: orders the k = *count promoted tokens
 // (scratch[0..k) in index order, their key bits at scratch[n..n+k)) by (key
 // descending, index ascending): rank_i = #{j: key_j > key_i} + #{j < i:
@@ -454,9 +462,8 @@ __global__ void __launch_bounds__(64 * kOrderSlices) wca_promote_order_kernel(
 }
 
 // Ascending indices of (a[t] | b[t]) (b may be null).
-__global__ void __launch_bounds__(kSelThreads) mask_nonzero_kernel(const uint8_t* a,
-                                                                   const uint8_t* b, int64_t n,
-                                                                   int64_t* out, int64_t* count) {
+__device__ void nonzero_block(const uint8_t* a, const uint8_t* b, int64_t n, int64_t* out,
+                              int64_t* count) {
   __shared__ int wave_tot[kSelWaves];
   int64_t base = 0;
   for (int64_t c0 = 0; c0 < n; c0 += kChunk) {
@@ -470,6 +477,13 @@ __global__ void __launch_bounds__(kSelThreads) mask_nonzero_kernel(const uint8_t
   }
   if (threadIdx.x == 0) *count = base;
 }
+
+__global__ void __launch_bounds__(kSelThreads) mask_nonzero_kernel(const uint8_t* a,
+                                                                   const uint8_t* b, int64_t n,
+                                                                   int64_t* out, int64_t* count) {
+  nonzero_block(a, b, n, out, count);
+}
+
 // fused = w * new + (1 - w) * old.  One thread per element of [a, H, D].
 __global__ void wca_blend_kernel(dview old_k, dview old_v, const int64_t* rows, dview new_k,
                                  dview new_v, const double* weight, const uint8_t* mandatory,
@@ -595,17 +609,10 @@ __global__ void __launch_bounds__(64 * kWaves) wca_cosine_kernel(dview a, dview 
   if (lane == 0) out[i] = total / static_cast<double>(H);
 }
 
-// bf16 fast path of mean_head_cosine: rows with contiguous 16-byte aligned
-// [H, D] blocks and D / 16 a power of two.  One wavefront per token; each head
-// is held by D / 16 lanes of 16 elements, reduced within those lanes; heads
-// are summed in ascending order as in the generic kernel.
-__global__ void __launch_bounds__(64 * kWaves) wca_cosine_bf16_kernel(
-    const uint16_t* a, int64_t a_s, const uint16_t* b, int64_t b_s, const int64_t* b_rows,
-    int64_t n, int H, int D, double eps, double* out) {
-  const int lane = threadIdx.x & 63;
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
-  if (i >= n) return;
-  const int64_t bi = b_rows ? b_rows[i] : i;
+// mean_head_cosine of one bf16 row pair (a_row, b_row: [H, D] contiguous),
+// returned on every lane of the wavefront.
+__device__ inline double cosine_bf16_row(const uint16_t* a_row, const uint16_t* b_row, int H, int D,
+                                         double eps, int lane) {
   const int L = D / 16, per = 64 / L;
   const double tiny = 2.2250738585072014e-308;
   double total = 0.0;
@@ -613,8 +620,8 @@ __global__ void __launch_bounds__(64 * kWaves) wca_cosine_bf16_kernel(
     const int h = h0 + lane / L;
     const int hc = h < H ? h : H - 1;  // lanes past the last head load it and are ignored
     const int64_t off = static_cast<int64_t>(hc) * D + (lane % L) * 16;
-    const uint4* pa = reinterpret_cast<const uint4*>(a + i * a_s + off);
-    const uint4* pb = reinterpret_cast<const uint4*>(b + bi * b_s + off);
+    const uint4* pa = reinterpret_cast<const uint4*>(a_row + off);
+    const uint4* pb = reinterpret_cast<const uint4*>(b_row + off);
     const uint4 va[2] = {pa[0], pa[1]}, vb[2] = {pb[0], pb[1]};
     double x[16], y[16];
 #pragma unroll
@@ -666,7 +673,22 @@ __global__ void __launch_bounds__(64 * kWaves) wca_cosine_bf16_kernel(
       if (h0 + g < H) total += v;
     }
   }
-  if (lane == 0) out[i] = total / static_cast<double>(H);
+  return total / static_cast<double>(H);
+}
+
+// bf16 fast path of mean_head_cosine: rows with contiguous 16-byte aligned
+// [H, D] blocks and D / 16 a power of two.  One wavefront per token; each head
+// is held by D / 16 lanes of 16 elements, reduced within those lanes; heads
+// are summed in ascending order as in the generic kernel.
+__global__ void __launch_bounds__(64 * kWaves) wca_cosine_bf16_kernel(
+    const uint16_t* a, int64_t a_s, const uint16_t* b, int64_t b_s, const int64_t* b_rows,
+    int64_t n, int H, int D, double eps, double* out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+  if (i >= n) return;
+  const int64_t bi = b_rows ? b_rows[i] : i;
+  const double c = cosine_bf16_row(a + i * a_s, b + bi * b_s, H, D, eps, lane);
+  if (lane == 0) out[i] = c;
 }
 
 // WCAState.initialize masks (wca.py:161-171): candidate = reused & (err > 0);
@@ -730,7 +752,7 @@ __global__ void wca_used_alpha_kernel(const double* alpha, const double* next, c
 // Gate removal (wca.py:277-287): removed = rows[i] with selected[rows[i]] and
 // metric < threshold, metric = cosine (paper_cosine_lt) or 1 - cosine
 // (distance_lt); ascending (rows are ascending).  Single workgroup.
-__global__ void __launch_bounds__(kSelThreads) wca_gate_kernel(
+__device__ void gate_block(
     const double* cosine, const int64_t* rows, const uint8_t* selected, int64_t a,
     int32_t distance, double threshold, int64_t* removed, int64_t* count) {
   __shared__ int wave_tot[kSelWaves];
@@ -751,6 +773,12 @@ __global__ void __launch_bounds__(kSelThreads) wca_gate_kernel(
     base += tot;
   }
   if (threadIdx.x == 0) *count = base;
+}
+
+__global__ void __launch_bounds__(kSelThreads) wca_gate_kernel(
+    const double* cosine, const int64_t* rows, const uint8_t* selected, int64_t a,
+    int32_t distance, double threshold, int64_t* removed, int64_t* count) {
+  gate_block(cosine, rows, selected, a, distance, threshold, removed, count);
 }
 
 // Commit (wca.py:289-293): alpha[rows[i]] = next[i]; the nrem[0] removed
@@ -1012,8 +1040,7 @@ __device__ inline bool words_nonfinite(const uint4* p, int64_t words, int64_t i,
   return bad;
 }
 
-__global__ void __launch_bounds__(256) update_checks_kernel(update_checks c, int32_t* flags) {
-  const int64_t b = blockIdx.x;
+__device__ inline void run_checks(const update_checks& c, int64_t b, int32_t* flags) {
   int seg = 0;
   while (seg < 5 && b >= c.first[seg + 1]) ++seg;
   const int64_t step = (c.first[seg + 1] - c.first[seg]) * 256;
@@ -1032,6 +1059,160 @@ __global__ void __launch_bounds__(256) update_checks_kernel(update_checks c, int
     for (int64_t j = i; j < c.rn; j += step) bad |= c.ra[j] != c.rb[j];
   }
   if (__any(bad) && (threadIdx.x & 63) == 0) atomicOr(flags, bit);
+}
+
+__global__ void __launch_bounds__(256) update_checks_kernel(update_checks c, int32_t* flags) {
+  run_checks(c, blockIdx.x, flags);
+}
+
+// The per-row work of a fused update (bf16 rows, contiguous [H, D] blocks):
+// one wavefront per active row i computes what the separate launches compute
+// -- the exact squared deviation and norm, the weight, the weight used, the
+// blend of K and V, and on gate layers the head cosine -- with the same
+// arithmetic in the same order, so every value and flag bit is theirs.
+struct update_rows {
+  const uint16_t* old_k;
+  int64_t ok_s;
+  const uint16_t* old_v;
+  int64_t ov_s;
+  const uint16_t* new_k;
+  int64_t nk_s;
+  const uint16_t* new_v;
+  int64_t nv_s;
+  uint16_t* fused_k;
+  int64_t fk_s;
+  uint16_t* fused_v;
+  int64_t fv_s;
+  const int64_t* rows;
+  int64_t a, words;
+  int32_t H, D;
+  const double* alpha;
+  const uint8_t* mandatory;
+  double eps;
+  int32_t clamp, previous, gate;
+  double *err, *norm, *next, *used, *cosine;
+};
+
+__device__ inline void update_row(const update_rows& r, int64_t i, int lane, int32_t* flags) {
+  const int64_t row = r.rows[i];
+  const uint4* ok = reinterpret_cast<const uint4*>(r.old_k + row * r.ok_s);
+  const uint4* nk = reinterpret_cast<const uint4*>(r.new_k + i * r.nk_s);
+  // squared deviation and norm (wca_score_bf16_kernel's order), on every lane
+  score_acc acc;
+  for (int64_t w = lane; w < r.words; w += 64) {
+    const uint4 ov = ok[w], fv = nk[w];
+    const uint32_t ow[4] = {ov.x, ov.y, ov.z, ov.w}, fw[4] = {fv.x, fv.y, fv.z, fv.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      acc.add(bf16_to_float(static_cast<uint16_t>(ow[q])), bf16_to_float(static_cast<uint16_t>(fw[q])));
+      acc.add(bf16_to_float(static_cast<uint16_t>(ow[q] >> 16)),
+              bf16_to_float(static_cast<uint16_t>(fw[q] >> 16)));
+    }
+  }
+  const dd e = dd_wave_sum(acc.e), nn = dd_wave_sum(acc.n);
+  const int any_bad = __any(acc.bad);
+  double ev = dd_round(e), nv = dd_round(nn);
+  if (!isfinite(e.hi)) ev = e.hi != e.hi ? e.hi : INFINITY;
+  if (!isfinite(nn.hi)) nv = nn.hi != nn.hi ? nn.hi : INFINITY;
+  int f = 0;
+  if (any_bad) f |= 1;
+  if (!isfinite(ev)) f |= 2;
+  if (!isfinite(nv)) f |= 16;
+  // weight (wca_alpha_kernel) and the weight used (wca_used_alpha_kernel)
+  const double num = ev, den = nv + r.eps;
+  if (!isfinite(num) || !isfinite(den)) f |= 2;
+  double nxt = num / den;
+  if (!isfinite(nxt)) f |= 4;
+  if (r.clamp) nxt = nxt < 0.0 ? 0.0 : (nxt > 1.0 ? 1.0 : nxt);
+  const double wt = r.mandatory[row] ? 1.0 : (r.previous ? r.alpha[row] : nxt);
+  if (lane == 0) {
+    r.err[i] = ev;
+    r.norm[i] = nv;
+    r.next[i] = nxt;
+    r.used[i] = wt;
+  }
+  // blend of K and V (wca_blend_bf16_kernel's arithmetic)
+  const double one_minus = 1.0 - wt;
+  int bad = 0;
+#pragma unroll
+  for (int kv = 0; kv < 2; ++kv) {
+    const uint4* o = kv ? reinterpret_cast<const uint4*>(r.old_v + row * r.ov_s) : ok;
+    const uint4* nw = kv ? reinterpret_cast<const uint4*>(r.new_v + i * r.nv_s) : nk;
+    uint4* out = reinterpret_cast<uint4*>(kv ? r.fused_v + i * r.fv_s : r.fused_k + i * r.fk_s);
+    for (int64_t w = lane; w < r.words; w += 64) {
+      const uint4 ov = o[w], fv = nw[w];
+      uint4 res;
+      res.x = blend_pair(ov.x, fv.x, wt, one_minus, bad);
+      res.y = blend_pair(ov.y, fv.y, wt, one_minus, bad);
+      res.z = blend_pair(ov.z, fv.z, wt, one_minus, bad);
+      res.w = blend_pair(ov.w, fv.w, wt, one_minus, bad);
+      out[w] = res;
+    }
+  }
+  if (__any(bad)) f |= 8;
+  if (r.gate) {
+    const double c = cosine_bf16_row(r.new_k + i * r.nk_s, r.old_k + row * r.ok_s, r.H, r.D, r.eps, lane);
+    if (lane == 0) r.cosine[i] = c;
+  }
+  if (lane == 0 && f) atomicOr(flags, f);
+}
+
+// Opening checks and the row pass in one launch: workgroups [0, first[5])
+// check, the rest serve four active rows each.
+__global__ void __launch_bounds__(256) update_fused_kernel(update_checks c, update_rows r, int32_t* flags) {
+  const int64_t b = blockIdx.x;
+  if (b < c.first[5]) {
+    run_checks(c, b, flags);
+    return;
+  }
+  const int64_t i = (b - c.first[5]) * 4 + (threadIdx.x >> 6);
+  if (i < r.a) update_row(r, i, threadIdx.x & 63, flags);
+}
+
+// The rest of a fused update in one workgroup: the gate's removed rows, the
+// commit (skipped when a registered check fired), the promotion's selection
+// and the next active rows -- the bodies of the separate launches, in their
+// order.
+struct update_final {
+  double* alpha;
+  const double* next;
+  const int64_t* rows;
+  int64_t a;
+  const double* cosine;
+  uint8_t *selected, *candidate, *removed_mask;
+  const uint8_t* mandatory;
+  const double* deviation;
+  int64_t n, budget;
+  int64_t* scratch;
+  int64_t *removed, *active, *counts;
+  int32_t gate, distance;
+  double threshold;
+  const int32_t* flags;
+  int32_t abort_mask;
+};
+
+__global__ void __launch_bounds__(kSelThreads) update_finalize_kernel(update_final f) {
+  const int tid = threadIdx.x;
+  if (f.gate)
+    gate_block(f.cosine, f.rows, f.selected, f.a, f.distance, f.threshold, f.removed, f.counts);
+  else if (tid == 0)
+    f.counts[0] = 0;
+  __syncthreads();
+  if (!(*f.flags & f.abort_mask)) {
+    for (int64_t i = tid; i < f.a; i += kSelThreads) f.alpha[f.rows[i]] = f.next[i];
+    const int64_t nrem = f.gate ? f.counts[0] : 0;
+    for (int64_t i = tid; i < nrem; i += kSelThreads) {
+      const int64_t t = f.removed[i];
+      f.selected[t] = 0;
+      f.candidate[t] = 0;
+      f.removed_mask[t] = 1;
+    }
+  }
+  __syncthreads();
+  promote_block(f.deviation, f.candidate, f.removed_mask, f.selected, f.n, f.budget, f.scratch,
+                f.counts + 1, f.flags, f.abort_mask);
+  __syncthreads();
+  nonzero_block(f.selected, f.mandatory, f.n, f.active, f.counts + 2);
 }
 
 // Fills one check segment when v is contiguous, 16-byte aligned and floating;
@@ -1064,6 +1245,25 @@ bool check_segment(const cs_view* v, int32_t bit, update_checks& c, int seg, int
 }  // namespace
 }  // namespace cs
 
+namespace cs {
+namespace {
+// The fused update applies to bf16 K/V with contiguous, 16-byte aligned
+// [H, D] rows (D a multiple of 16 with D / 16 a power of two) whose finite
+// checks fit the single opening launch.
+bool fused_update_ok(const cs_wca_update_args* u) {
+  const cs_view* v[6] = {&u->cached_k, &u->cached_v, &u->recomputed_k, &u->recomputed_v, &u->fused_k,
+                         &u->fused_v};
+  for (const cs_view* x : v) {
+    if (!x->data || x->ndim != 3 || !bf16_rows16(x)) return false;
+    if (x->shape[1] != u->cached_k.shape[1] || x->shape[2] != u->cached_k.shape[2]) return false;
+  }
+  const int64_t D = u->cached_k.shape[2], L = D / 16;
+  return u->rows && u->a > 0 && u->recomputed_k.shape[0] == u->a && D % 16 == 0 && L >= 1 && L <= 64 &&
+         (L & (L - 1)) == 0 && u->cached_k.shape[1] <= (1 << 20) && u->n <= (1ll << 24);
+}
+}  // namespace
+}  // namespace cs
+
 extern "C" int cs_wca_update(const cs_wca_update_args* u, void* stream) {
   CS_REQUIRE(u && u->flags && u->counts, "null arguments");
   CS_REQUIRE(u->a >= 0 && (!u->computed || u->a == 0 || u->rows), "null arguments");
@@ -1089,6 +1289,73 @@ extern "C" int cs_wca_update(const cs_wca_update_args* u, void* stream) {
       blocks += std::min<int64_t>(ceil_div(u->a, 256), 1024);
     }
     c.first[5] = blocks;
+  }
+  if (fused && fused_update_ok(u)) {
+    // three launches: checks + rows, the one-workgroup finish, the promotion order
+    update_rows r{};
+    r.old_k = static_cast<const uint16_t*>(u->cached_k.data);
+    r.ok_s = u->cached_k.stride[0];
+    r.old_v = static_cast<const uint16_t*>(u->cached_v.data);
+    r.ov_s = u->cached_v.stride[0];
+    r.new_k = static_cast<const uint16_t*>(u->recomputed_k.data);
+    r.nk_s = u->recomputed_k.stride[0];
+    r.new_v = static_cast<const uint16_t*>(u->recomputed_v.data);
+    r.nv_s = u->recomputed_v.stride[0];
+    r.fused_k = static_cast<uint16_t*>(u->fused_k.data);
+    r.fk_s = u->fused_k.stride[0];
+    r.fused_v = static_cast<uint16_t*>(u->fused_v.data);
+    r.fv_s = u->fused_v.stride[0];
+    r.rows = u->rows;
+    r.a = u->a;
+    r.H = static_cast<int32_t>(u->cached_k.shape[1]);
+    r.D = static_cast<int32_t>(u->cached_k.shape[2]);
+    r.words = static_cast<int64_t>(r.H) * r.D / 8;
+    r.alpha = u->alpha;
+    r.mandatory = u->mandatory;
+    r.eps = u->epsilon;
+    r.clamp = u->clamp;
+    r.previous = u->previous_layer;
+    r.gate = u->gate;
+    r.err = u->err;
+    r.norm = u->norm;
+    r.next = u->next_alpha;
+    r.used = u->used;
+    r.cosine = u->cosine;
+    const int64_t grid = blocks + ceil_div(u->a, 4);
+    CS_REQUIRE(grid < (1ll << 31), "grid too large");
+    hipStream_t s = as_stream(stream);
+    hipLaunchKernelGGL(update_fused_kernel, dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, c, r, f);
+    update_final fin{};
+    fin.alpha = u->alpha;
+    fin.next = u->next_alpha;
+    fin.rows = u->rows;
+    fin.a = u->a;
+    fin.cosine = u->cosine;
+    fin.selected = u->selected;
+    fin.candidate = u->candidate;
+    fin.removed_mask = u->removed_mask;
+    fin.mandatory = u->mandatory;
+    fin.deviation = u->deviation;
+    fin.n = u->n;
+    fin.budget = u->budget;
+    fin.scratch = u->scratch;
+    fin.removed = u->removed;
+    fin.active = u->active;
+    fin.counts = u->counts;
+    fin.gate = u->gate;
+    fin.distance = u->distance_mode;
+    fin.threshold = u->threshold;
+    fin.flags = f;
+    fin.abort_mask = u->abort_mask;
+    hipLaunchKernelGGL(update_finalize_kernel, dim3(1), dim3(kSelThreads), 0, s, fin);
+    const int64_t kmax = u->budget < u->n ? (u->budget > 0 ? u->budget : 0) : u->n;
+    if (kmax > 0)
+      hipLaunchKernelGGL(wca_promote_order_kernel, dim3(ceil_div(kmax, 64)), dim3(64 * kOrderSlices), 0,
+                         s, u->scratch, u->n, u->counts + 1, u->promoted);
+    CS_LAUNCH_CHECK("wca_update");
+    return CS_OK;
+  }
+  if (fused) {
     if (blocks > 0) {
       hipLaunchKernelGGL(update_checks_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                          as_stream(stream), c, f);
