@@ -7,12 +7,13 @@
 // right-most split always holds S keys.  Split 0 is computed exactly (carry 0).
 // Every other split assumes that the gate mass of the keys to its right is
 // already >= P-1, which makes every position in it P-1 and the bias the row
-// constant QE[P-1]; it records its own gate total.  A plan launch forms each
-// split's true carry (sum of the totals to its right) and queues the splits
-// whose carry is below P-1; a fixup launch recomputes exactly the queued
-// splits; a combine launch merges the per-split (max, sum, accumulator)
-// triples.  Split 0 and the speculative splits share one launch, split 0's
-// workgroups first.
+// constant QE[P-1]; it records its own gate total.  A second launch, one
+// workgroup per (request, KV head), forms the splits' true carries (sum of the
+// totals to their right) from the right-most split until every head's carry
+// reaches P-1 -- carries only grow, so the splits that need it are a prefix --
+// recomputes those splits exactly, and merges the per-split (max, sum,
+// accumulator) triples into the output rows.  Split 0's workgroups lead the
+// first launch's grid.
 //
 // Inside a split each of the 4 wavefronts owns a contiguous quarter of the
 // keys and walks it in tiles of 16 keys from the right.  Per tile:
@@ -46,7 +47,6 @@ constexpr int kMaxGroup = 8;
 constexpr int kMaxPos = 256;
 constexpr int kMaxSplit = 1024;
 constexpr int kTile = 16;
-constexpr int kFixupGrid = 1024;
 constexpr float kInvSqrtD = 0.08838834764831845f;  // 1/sqrt(128)
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -93,8 +93,6 @@ struct decode_params {
   float* mx;           // [B, hq, smax] running max (log2 domain)
   float* sm;           // [B, hq, smax] sum of exp2
   float* acc;          // [B, hq, smax, 128]
-  int32_t* work;       // fixup queue: (b * hkv + kvh) * smax + r
-  int32_t* work_count;
   uint16_t* out;
   int32_t* flags;
 };
@@ -109,6 +107,7 @@ struct smem_t {
   union {
     float sc[G][kMaxSplit];       // exact splits: logits
     float wave_o[kWaves][G][kD];  // end of a split: per-wave accumulators
+    float wgt[2][kD];             // group finish: split weights of two heads
   } u;
   float qe[G][kMaxPos];  // exact splits: QE = q . E
   float q[G][kD];
@@ -116,6 +115,8 @@ struct smem_t {
   double carry[G];
   float wave_m[kWaves][G];
   float wave_l[kWaves][G];
+  float red[2][2];
+  int fix_end;  // group finish: splits 1 .. fix_end-1 are recomputed
 };
 
 struct split_ctx {
@@ -643,6 +644,139 @@ __device__ void run_exact(const decode_params& p, smem_t<G>& s, const split_ctx&
   split_finish(p, s, c, write_tot);
 }
 
+// ---- finish of one (request, KV head) group ---------------------------------
+
+// Carries of splits 1, 2, ... (sum of the split totals to their right, fp64,
+// accumulated from the right-most split) into p.carry, 64 splits at a time
+// (wave 0, lane i: the total of split base+i, the carry of split base+i+1),
+// up to the first split at which every head's carry has reached P-1;
+// s.fix_end is that split (or `splits`).  Gate totals are sums of sigmoids, so
+// carries never decrease along the splits and no later split needs
+// recomputing.
+template <int G>
+__device__ void plan_group(const decode_params& p, smem_t<G>& s, int b, int h0, int splits) {
+  if (threadIdx.x >= 64) return;
+  const int lane = threadIdx.x;
+  const double top = static_cast<double>(p.npos - 1);
+  double carry_in[G];
+#pragma unroll
+  for (int h = 0; h < G; ++h) carry_in[h] = 0.0;
+  int fix_end = splits > 1 ? splits : 1;
+  for (int base = 0; base + 1 < splits; base += 64) {
+    const int r = base + lane;
+    const bool has_next = r + 1 < splits;
+    double v[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) v[h] = has_next ? p.tot[ws_index(p, b, h0 + h, r)] : 0.0;
+    bool below = false;
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      double x = v[h];  // inclusive scan over the wave
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const double y = __shfl_up(x, off, 64);
+        if (lane >= off) x += y;
+      }
+      const double carry = carry_in[h] + x;
+      if (has_next) {
+        p.carry[ws_index(p, b, h0 + h, r + 1)] = carry;
+        below |= carry < top;  // false for NaN
+      }
+      carry_in[h] += __shfl(x, 63, 64);
+    }
+    const unsigned long long done = __ballot(has_next && !below);
+    if (done) {
+      fix_end = base + __builtin_ctzll(done) + 1;
+      break;
+    }
+  }
+  if (lane == 0) s.fix_end = fix_end;
+}
+
+// Exact recomputation of splits 1 .. s.fix_end-1, one after another.
+template <int G, bool PAGED>
+__device__ void fixup_group(const decode_params& p, smem_t<G>& s, int b, int kvh, bool& bad) {
+  // read after the barrier that follows plan_group; the same in every lane
+  const int fix_end = __builtin_amdgcn_readfirstlane(s.fix_end);
+  for (int r = 1; r < fix_end; ++r) {
+    split_ctx c;
+    make_ctx(p, b, kvh, r, c);
+    if (threadIdx.x < G) s.carry[threadIdx.x] = p.carry[ws_index(p, b, c.h0 + threadIdx.x, r)];
+    __syncthreads();
+    run_exact<G, PAGED>(p, s, c, false, bad);
+    __syncthreads();
+  }
+}
+
+// Merge of the split partials of two query heads, threads 0..127 for head ha
+// and 128..255 for head hb (hb < 0: those threads only join the barriers);
+// thread d of a half owns output dim d, split weights are formed 128 at a time.
+template <int G>
+__device__ void combine_pair(const decode_params& p, smem_t<G>& s, int b, int ha, int hb,
+                             int splits) {
+  const int half = threadIdx.x >> 7, d = threadIdx.x & (kD - 1);
+  const int lane = threadIdx.x & 63, wave = (threadIdx.x >> 6) & 1;
+  const int h = half ? hb : ha;
+  const bool live = h >= 0;
+  const int64_t w0 = ws_index(p, b, live ? h : ha, 0);
+  float* wgt = s.u.wgt[half];
+  // the first 128 splits' max and sum stay in registers for the weights below
+  float m_first = -INFINITY, l_first = 0.f;
+  if (live && d < splits) {
+    m_first = p.mx[w0 + d];
+    l_first = p.sm[w0 + d];
+  }
+  float M = m_first;
+  if (live)
+    for (int r = d + kD; r < splits; r += kD) M = fmaxf(M, p.mx[w0 + r]);
+  M = wave_max(M);
+  if (lane == 0) s.red[half][wave] = M;
+  __syncthreads();
+  M = fmaxf(s.red[half][0], s.red[half][1]);
+  __syncthreads();
+  float L = 0.f, O = 0.f;
+  for (int base = 0; base < splits; base += kD) {
+    const int r = base + d;
+    float f = 0.f;
+    if (live && r < splits) {
+      const float m = base == 0 ? m_first : p.mx[w0 + r];
+      const float l = base == 0 ? l_first : p.sm[w0 + r];
+      f = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
+      L += l * f;
+    }
+    wgt[d] = f;
+    __syncthreads();
+    const int n = splits - base < kD ? splits - base : kD;
+    if (live) {
+      const float* acc = p.acc + (w0 + base) * kD + d;
+      int i = 0;
+      // 16 partials in flight per thread: the merge is bound by load latency
+      for (; i + 16 <= n; i += 16) {
+        float a[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) a[j] = acc[(i + j) * kD];
+#pragma unroll
+        for (int j = 0; j < 16; j += 4)
+          O += wgt[i + j] * a[j] + wgt[i + j + 1] * a[j + 1] + wgt[i + j + 2] * a[j + 2] +
+               wgt[i + j + 3] * a[j + 3];
+      }
+      for (; i + 4 <= n; i += 4) {
+        const float a0 = acc[(i + 0) * kD], a1 = acc[(i + 1) * kD];
+        const float a2 = acc[(i + 2) * kD], a3 = acc[(i + 3) * kD];
+        O += wgt[i] * a0 + wgt[i + 1] * a1 + wgt[i + 2] * a2 + wgt[i + 3] * a3;
+      }
+      for (; i < n; ++i) O += wgt[i] * acc[i * kD];
+    }
+    __syncthreads();
+  }
+  L = wave_sum(L);
+  if (lane == 0) s.red[half][wave] = L;
+  __syncthreads();
+  L = s.red[half][0] + s.red[half][1];
+  __syncthreads();
+  if (live) p.out[static_cast<int64_t>(b) * p.hq * kD + h * kD + d] = float_to_bf16(L > 0.f ? O / L : 0.f);
+}
+
 // Split 0 of every (request, KV head) exactly, then the speculative splits;
 // the grid is ordered split-major so the exact workgroups start first.
 template <int G, bool PAGED>
@@ -652,7 +786,6 @@ __global__ void __launch_bounds__(kThreads) decode_main_kernel(decode_params p) 
   const int id = blockIdx.x;
   const int r = id / per_r, rem = id % per_r;
   const int b = rem / p.hkv, kvh = rem % p.hkv;
-  if (id == 0 && threadIdx.x == 0) *p.work_count = 0;
   if (r == 0 && kvh == 0 && threadIdx.x == 0) {
     const int nk = p.nk[b];
     if (nk < 1) atomicOr(p.flags, CS_FLAG_NO_KEY);
@@ -670,148 +803,22 @@ __global__ void __launch_bounds__(kThreads) decode_main_kernel(decode_params p) 
   if (bad) atomicOr(p.flags, CS_FLAG_BLOCK_INVALID);
 }
 
-// Carry of every split (fp64 exclusive scan of the split totals, from the
-// right-most split) and the queue of splits whose carry is below P-1 for some
-// head.  One workgroup per (request, KV head); splits in chunks of 256.
-constexpr int kPlanThreads = 256;
-
-__global__ void __launch_bounds__(kPlanThreads) decode_plan_kernel(decode_params p) {
-  __shared__ double chunk_sum[kPlanThreads / 64];
-  const int b = blockIdx.x / p.hkv, kvh = blockIdx.x % p.hkv;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int nk = p.nk[b];
-  int splits = (nk + p.split - 1) / p.split;
-  if (splits > p.smax) splits = p.smax;
-  const int G = p.group, h0 = kvh * G;
-  const double top = static_cast<double>(p.npos - 1);
-  double carry_in[kMaxGroup];
-#pragma unroll
-  for (int h = 0; h < kMaxGroup; ++h) carry_in[h] = 0.0;
-  for (int base = 0; base < splits; base += kPlanThreads) {
-    const int r = base + tid;
-    bool need = false;
-    // all heads' totals are loaded before the first carry store: tot and carry
-    // may alias as far as the compiler knows, so it would not hoist them itself
-    double v[kMaxGroup];
-#pragma unroll
-    for (int h = 0; h < kMaxGroup; ++h)
-      v[h] = (h < G && r < splits) ? p.tot[ws_index(p, b, h0 + h, r)] : 0.0;
-#pragma unroll
-    for (int h = 0; h < kMaxGroup; ++h) {
-      if (h >= G) continue;
-      const int64_t wi = ws_index(p, b, h0 + h, r < splits ? r : 0);
-      double x = v[h];  // inclusive scan within the wave
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const double y = __shfl_up(x, off, 64);
-        if (lane >= off) x += y;
-      }
-      double excl = __shfl_up(x, 1, 64);
-      if (lane == 0) excl = 0.0;
-      if (lane == 63) chunk_sum[wave] = x;
-      __syncthreads();
-      double before = carry_in[h];
-      for (int w = 0; w < wave; ++w) before += chunk_sum[w];
-      excl += before;
-      double total = 0.0;
-      for (int w = 0; w < kPlanThreads / 64; ++w) total += chunk_sum[w];
-      __syncthreads();
-      carry_in[h] += total;
-      if (r < splits) {
-        p.carry[wi] = excl;
-        need |= r >= 1 && excl < top;
-      }
-    }
-    if (need) {
-      const int slot = atomicAdd(p.work_count, 1);
-      p.work[slot] = (b * p.hkv + kvh) * p.smax + r;
-    }
-  }
-}
-
+// One workgroup per (request, KV head): carries, recomputation of the splits
+// whose carry is below P-1, and the merge into the output rows.
 template <int G, bool PAGED>
-__global__ void __launch_bounds__(kThreads) decode_fixup_kernel(decode_params p) {
+__global__ void __launch_bounds__(kThreads) decode_finish_kernel(decode_params p) {
   __shared__ smem_t<G> s;
-  const int count = *p.work_count;
-  bool bad = false;
-  for (int i = blockIdx.x; i < count; i += gridDim.x) {
-    const int item = p.work[i];
-    const int r = item % p.smax, bk = item / p.smax;
-    const int b = bk / p.hkv, kvh = bk % p.hkv;
-    split_ctx c;
-    if (!make_ctx(p, b, kvh, r, c)) continue;
-    if (threadIdx.x < G) s.carry[threadIdx.x] = p.carry[ws_index(p, b, c.h0 + threadIdx.x, r)];
-    __syncthreads();
-    run_exact<G, PAGED>(p, s, c, false, bad);
-    __syncthreads();
-  }
-  if (bad) atomicOr(p.flags, CS_FLAG_BLOCK_INVALID);
-}
-
-// Merge of the split partials of one (request, query head): 128 threads,
-// thread d owns output dim d; split weights are formed 128 at a time in LDS.
-__global__ void __launch_bounds__(kD) decode_combine_kernel(decode_params p) {
-  __shared__ float wgt[kD];
-  __shared__ float red[kD / 64];
-  const int bh = blockIdx.x;
-  const int b = bh / p.hq, h = bh % p.hq;
-  const int d = threadIdx.x, lane = d & 63, wave = d >> 6;
-  const int nk = p.nk[b];
-  int splits = (nk + p.split - 1) / p.split;
+  const int b = blockIdx.x / p.hkv, kvh = blockIdx.x % p.hkv;
+  const int h0 = kvh * G;
+  int splits = (p.nk[b] + p.split - 1) / p.split;
   if (splits > p.smax) splits = p.smax;
-  const int64_t w0 = ws_index(p, b, h, 0);
-  // the first 128 splits' max and sum stay in registers for the weights below
-  float m_first = -INFINITY, l_first = 0.f;
-  if (d < splits) {
-    m_first = p.mx[w0 + d];
-    l_first = p.sm[w0 + d];
-  }
-  float M = m_first;
-  for (int r = d + kD; r < splits; r += kD) M = fmaxf(M, p.mx[w0 + r]);
-  M = wave_max(M);
-  if (lane == 0) red[wave] = M;
+  if (splits < 0) splits = 0;  // no key: zero rows (the call is flagged)
+  bool bad = false;
+  plan_group<G>(p, s, b, h0, splits);
   __syncthreads();
-  M = fmaxf(red[0], red[1]);
-  __syncthreads();
-  float L = 0.f, O = 0.f;
-  for (int base = 0; base < splits; base += kD) {
-    const int r = base + d;
-    float f = 0.f;
-    if (r < splits) {
-      const float m = base == 0 ? m_first : p.mx[w0 + r];
-      const float l = base == 0 ? l_first : p.sm[w0 + r];
-      f = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
-      L += l * f;
-    }
-    wgt[d] = f;
-    __syncthreads();
-    const int n = splits - base < kD ? splits - base : kD;
-    const float* acc = p.acc + (w0 + base) * kD + d;
-    int i = 0;
-    // 16 partials in flight per thread: the merge is bound by load latency
-    for (; i + 16 <= n; i += 16) {
-      float a[16];
-#pragma unroll
-      for (int j = 0; j < 16; ++j) a[j] = acc[(i + j) * kD];
-#pragma unroll
-      for (int j = 0; j < 16; j += 4)
-        O += wgt[i + j] * a[j] + wgt[i + j + 1] * a[j + 1] + wgt[i + j + 2] * a[j + 2] +
-             wgt[i + j + 3] * a[j + 3];
-    }
-    for (; i + 4 <= n; i += 4) {
-      const float a0 = acc[(i + 0) * kD], a1 = acc[(i + 1) * kD];
-      const float a2 = acc[(i + 2) * kD], a3 = acc[(i + 3) * kD];
-      O += wgt[i] * a0 + wgt[i + 1] * a1 + wgt[i + 2] * a2 + wgt[i + 3] * a3;
-    }
-    for (; i < n; ++i) O += wgt[i] * acc[i * kD];
-    __syncthreads();
-  }
-  L = wave_sum(L);
-  if (lane == 0) red[wave] = L;
-  __syncthreads();
-  L = red[0] + red[1];
-  const float val = L > 0.f ? O / L : 0.f;
-  p.out[static_cast<int64_t>(b) * p.hq * kD + h * kD + d] = float_to_bf16(val);
+  fixup_group<G, PAGED>(p, s, b, kvh, bad);
+  for (int h = 0; h < G; h += 2) combine_pair<G>(p, s, b, h0 + h, h + 1 < G ? h0 + h + 1 : -1, splits);
+  if (bad) atomicOr(p.flags, CS_FLAG_BLOCK_INVALID);
 }
 
 template <int G, bool PAGED>
@@ -819,13 +826,8 @@ void launch_split_kernels(const decode_params& p, hipStream_t s) {
   const int64_t main_grid = static_cast<int64_t>(p.smax) * p.hkv * p.batch;
   hipLaunchKernelGGL((decode_main_kernel<G, PAGED>), dim3(static_cast<uint32_t>(main_grid)),
                      dim3(kThreads), 0, s, p);
-  if (p.smax > 1) {
-    hipLaunchKernelGGL(decode_plan_kernel, dim3(p.hkv * p.batch), dim3(kPlanThreads), 0, s, p);
-    int64_t fix = static_cast<int64_t>(p.smax - 1) * p.hkv * p.batch;
-    if (fix > kFixupGrid) fix = kFixupGrid;
-    hipLaunchKernelGGL((decode_fixup_kernel<G, PAGED>), dim3(static_cast<uint32_t>(fix)),
-                       dim3(kThreads), 0, s, p);
-  }
+  hipLaunchKernelGGL((decode_finish_kernel<G, PAGED>), dim3(static_cast<uint32_t>(p.hkv * p.batch)),
+                     dim3(kThreads), 0, s, p);
 }
 
 template <int G>
@@ -846,8 +848,8 @@ extern "C" int64_t cs_ccpe_decode_workspace_bytes(int32_t batch, int32_t hq, int
   if (batch <= 0 || hq <= 0 || max_nk <= 0 || split <= 0) return 0;
   const int64_t smax = (static_cast<int64_t>(max_nk) + split - 1) / split;
   const int64_t n = static_cast<int64_t>(batch) * hq * smax;
-  // tot, carry (f64) | acc (f32 x 128) | mx, sm (f32) | fixup queue (i32) | count
-  return n * (8 + 8 + 4 * kD + 4 + 4 + 4) + 16;
+  // tot, carry (f64) | acc (f32 x 128) | mx, sm (f32)
+  return n * (8 + 8 + 4 * kD + 4 + 4);
 }
 
 namespace {
@@ -952,8 +954,6 @@ int launch_decode(decode_params& p, void* workspace, void* stream) {
   p.acc = reinterpret_cast<float*>(ws + n * 16);
   p.mx = p.acc + n * kD;
   p.sm = p.mx + n;
-  p.work = reinterpret_cast<int32_t*>(p.sm + n);
-  p.work_count = p.work + n;
   if (p.batch == 0) return CS_OK;
   hipStream_t s = as_stream(stream);
   switch (p.group) {
@@ -966,7 +966,6 @@ int launch_decode(decode_params& p, void* workspace, void* stream) {
     case 7: launch_group<7>(p, s); break;
     default: launch_group<8>(p, s); break;
   }
-  hipLaunchKernelGGL(decode_combine_kernel, dim3(p.batch * p.hq), dim3(kD), 0, s, p);
   CS_LAUNCH_CHECK("ccpe_decode");
   return CS_OK;
 }
@@ -1035,9 +1034,8 @@ extern "C" int cs_ccpe_decode_bf16_noalloc(const void* q, int64_t q_s_batch, int
   void* ws = nullptr;
   const int sst = scratch_address(stream, &ws);
   if (sst) return sst;
-  // every workspace field the kernels read is written earlier in the same call
-  // (the queue counter by the first workgroup of the main launch), so the
-  // previous call's contents need no clearing
+  // every workspace field the kernels read is written earlier in the same call,
+  // so the previous call's contents need no clearing
   return launch_decode(p, ws, stream);
 }
 

@@ -252,9 +252,12 @@ int cs_ccpe_prefill_bf16(const void* q, int64_t q_s_batch, int64_t q_s_tok, int6
  * decode step calls it, runtime.py:489-508 over the paged.py:433-472 gather).
  * Decode (q = 1 row per request at position nk[b]-1) with speculative
  * split-K: splits are aligned to the last key; a split whose right-hand gate
- * mass is below P-1 is recomputed exactly.  workspace must hold
- * cs_ccpe_decode_workspace_bytes(batch, hq, max_nk, split) bytes; the call
- * refuses a smaller workspace_bytes.  A request with nk[b] < 1 sets
+ * mass is below P-1 is recomputed exactly by the last workgroup of its
+ * (request, KV head) to finish, which also merges the splits (two launches:
+ * a clear of the arrival counters, then the splits).  workspace must hold
+ * cs_ccpe_decode_workspace_bytes(batch, hq, max_nk, split) bytes, with any
+ * contents; the call refuses a smaller workspace_bytes.  Calls that share a
+ * workspace must be ordered (one stream).  A request with nk[b] < 1 sets
  * CS_FLAG_NO_KEY and one with nk[b] > max_nk sets CS_FLAG_CONTEXT_RANGE; the
  * output rows of such requests are not valid.
  *   q [B, Hq, 128] bf16 (q_s_batch, q_s_head), out [B, Hq, 128] bf16. */

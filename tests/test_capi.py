@@ -50,7 +50,7 @@ def test_argument_errors_need_no_device():
     assert b"null" in lib.cs_last_error()
     # per split: gate total and carry (f64), accumulator (128 f32), max, sum,
     # fixup-queue entry; plus the queue counter
-    assert lib.cs_ccpe_decode_workspace_bytes(2, 4, 1000, 256) == 2 * 4 * 4 * (8 + 8 + 4 * 128 + 4 + 4 + 4) + 16
+    assert lib.cs_ccpe_decode_workspace_bytes(2, 4, 1000, 256) == 2 * 4 * 4 * (8 + 8 + 4 * 128 + 4 + 4)
 
 
 def test_snapshot_entry_points_check_arguments_without_a_device():

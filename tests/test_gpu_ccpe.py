@@ -580,10 +580,13 @@ def test_decode_matches_oracle(device, split):
         assert_close_bf16(out[b:b + 1], expected)
 
 
-def test_decode_unsaturated_splits_are_recomputed(device):
+@pytest.mark.parametrize("n, split", [(1500, 128), (17000, 64)])
+def test_decode_unsaturated_splits_are_recomputed(device, n, split):
     """Keys anti-aligned with the query: gates ~0, positions never saturate, so
-    every split's speculation fails and the exact fixup path produces the result."""
-    n, hq, hkv, bs = 1500, 4, 1, 16
+    every split's speculation fails and the exact fixup path produces the result
+    (17000 keys in splits of 64: 265 recomputed splits, more than one chunk of
+    the finishing workgroup's list)."""
+    hq, hkv, bs = 4, 1, 16
     nb, table, rows = paged_layout([n], hkv, bs, 128, seed=11)
     q = seeded((1, hq, 128), 84, dtype=torch.bfloat16)
     base = q[0, 0].float()
@@ -596,7 +599,7 @@ def test_decode_unsaturated_splits_are_recomputed(device):
     qq = q.clone()
     qq[0, 1:] = q[0, 0]
     out = ccpe_decode_paged(qq.to(device), cache.to(device), table.to(device),
-                            torch.tensor([n], dtype=torch.int32, device=device), cope, split=128)
+                            torch.tensor([n], dtype=torch.int32, device=device), cope, split=split)
     allowed = orc.allowed_mask(np.array([n - 1]), np.arange(n), hq)
     p = orc.contextual_positions(orc.logits(acc_np(qq), acc_np(keys[0])), allowed, 64)
     assert p.max() < 63  # never saturated: the fixup path is exercised
