@@ -172,7 +172,7 @@ def ccpe_prefill_paged(
         ptr(e), cope.max_positions, ptr(out), ptr(flags), _hip.stream_of(device),
     )
     if check:
-        _raise_flags(flags)
+        raise_flags(flags)
     return out
 
 
@@ -216,6 +216,8 @@ def ccpe_decode_paged(
     max_context: int | None = None,
     split: int = 1024,
     workspace: Tensor | None = None,
+    out: Tensor | None = None,
+    flags: Tensor | None = None,
     check: bool = True,
 ) -> Tensor:
     """Batched CCPE decode: row b attends keys 0..context_lens[b]-1 at position context_lens[b]-1.
@@ -227,7 +229,11 @@ def ccpe_decode_paged(
     omitted); a larger context raises ValueError, as does an empty one
     (position.py:149-150).  ``split`` is the number of keys per split-K work
     item (multiple of 64, <= 1024).  ``workspace`` (uint8, device) must hold
-    ``decode_workspace_bytes(B, Hq, max_context, split)`` bytes.
+    ``decode_workspace_bytes(B, Hq, max_context, split)`` bytes.  ``out``
+    (bf16 [B, Hq, 128], contiguous) receives the rows when given.  ``flags``
+    (from ``_hip.new_flags``) collects the error bits of this and earlier
+    calls when given, for a caller that checks once (``raise_flags``) after a
+    loop of calls with ``check=False``.
     """
     device = _hip.require_device(query, cache, context_lens, block_table, slots)
     if query.ndim != 3 or query.dtype != torch.bfloat16 or query.shape[2] != 128 or query.stride(2) != 1:
@@ -256,15 +262,22 @@ def ccpe_decode_paged(
     have = workspace.numel() * workspace.element_size()
     if have < need:
         raise ValueError(f"decode workspace holds {have} bytes, the call needs {need}")
-    flags = _hip.new_flags(device)
-    out = torch.empty((b, hq, 128), dtype=torch.bfloat16, device=device)
+    if flags is None:
+        flags = _hip.new_flags(device)
+    elif flags.device != device or flags.dtype != torch.int32 or flags.numel() < 1:
+        raise ValueError("flags must be an int32 tensor on the query device")
+    if out is None:
+        out = torch.empty((b, hq, 128), dtype=torch.bfloat16, device=device)
+    elif (out.shape != (b, hq, 128) or out.dtype != torch.bfloat16 or out.device != device
+          or not out.is_contiguous()):
+        raise ValueError("out must be a contiguous bf16 [batch, heads, 128] tensor on the query device")
     call(
         "cs_ccpe_decode_bf16", ptr(query), query.stride(0), query.stride(1), b, hq, hkv,
         ptr(context_lens), max_context, src, ptr(e), cope.max_positions, split, ptr(workspace),
         have, ptr(out), ptr(flags), _hip.stream_of(device),
     )
     if check:
-        _raise_flags(flags)
+        raise_flags(flags)
     return out
 
 
@@ -285,7 +298,9 @@ def ccpe_decode_arena(query: Tensor, arena, cope, *, split: int = 1024, check: b
                                  check=check)
 
 
-def _raise_flags(flags: Tensor) -> None:
+def raise_flags(flags: Tensor) -> None:
+    """Raise the error the fused decode / prefill calls recorded in ``flags``
+    (reads them back, so it waits for those calls)."""
     value = _hip.read_flags(flags)[0]
     if value & _hip.FLAG_NO_KEY:
         raise ValueError("attention requires at least one key")
