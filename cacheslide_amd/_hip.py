@@ -42,6 +42,7 @@ FLAG_PATH_GAP = 1 << 19
 FLAG_ROW_LOST = 1 << 20
 FLAG_ROWS_UNSORTED = 1 << 21
 FLAG_ROW_INDEX = 1 << 22
+FLAG_POLICY_GENERIC = 1 << 23
 COPY_H2D, COPY_D2H, COPY_D2D = range(3)
 
 _DTYPE_CODES = {
@@ -154,6 +155,8 @@ SIGNATURES = {
     "cs_check_positions": (_I32, [_P, _I64, _I32, _P, _P]),
     "cs_check_bias_positions": (_I32, [_VP, _I64, _P, _P]),
     "cs_ccpe_attention": (_I32, [ctypes.POINTER(CsCcpeArgs), _P]),
+    "cs_ccpe_prefill_policy_workspace_bytes": (_I64, [_I32, _I32, _I64]),
+    "cs_ccpe_prefill_policy_bf16": (_I32, [ctypes.POINTER(CsCcpeArgs), _P, _I64, _P]),
     "cs_cope_positional_bias": (_I32, [_VP, _VP, _VP, _VP, _P, _P]),
     "cs_contextual_positions": (_I32, [_VP, _VP, _I64, _VP, _P, _P]),
     "cs_ccpe_logits": (_I32, [_VP, _VP, _VP, _P, _P]),

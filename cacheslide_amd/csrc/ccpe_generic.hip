@@ -20,15 +20,13 @@
 // position dtype, which is what torch's CPU cumsum does for fp32 inputs.
 
 #include "common.h"
+#include "ccpe_path.h"
 
 namespace cs {
 namespace {
 
 constexpr int kGenWaves = 2;
 constexpr int kMaxDvChunks = 8;  // Dv <= 512
-constexpr int32_t kChunkHasFixedRow = 1 << 30;
-constexpr int32_t kChunkUnknownRow = 1 << 29;  // a fixed row the profile has no trace for
-constexpr int32_t kChunkCanonOutOfRange = 1 << 28;  // a substituted canonical cell outside [0, P-1]
 
 __device__ inline void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -80,47 +78,6 @@ struct gen_params {
   int64_t wave_bytes;  // LDS bytes per wave
   int64_t p_pad;
 };
-
-template <typename TP> struct pos_traits;
-template <> struct pos_traits<float> {
-  __device__ static float eps() { return 1.1920928955078125e-07f; }  // 2^-23
-};
-template <> struct pos_traits<double> {
-  __device__ static double eps() { return 2.220446049250313e-16; }  // 2^-52
-};
-
-// The strict path checks of validate_contextual_path (position.py:98-114) for
-// one valid cell and (optionally) its valid right-hand neighbour, evaluated
-// with the reference's operation order and no contraction.
-template <typename TP>
-__device__ inline int path_violations(TP p, bool valid, TP p_right, bool pair_valid,
-                                      int64_t qp, int64_t kp, int64_t kp_right, TP atol) {
-#pragma clang fp contract(off)
-  int bits = 0;
-  if (!valid) return 0;
-  const TP eps = pos_traits<TP>::eps();
-  TP rounding = eps * (p < 0 ? -p : p);
-  TP neg_tol = atol + rounding;
-  if (p < -neg_tol) bits |= CS_FLAG_PATH_NEGATIVE;
-  int64_t diff = qp - kp;
-  TP available = static_cast<TP>(diff);
-  if (available < TP(-1)) available = TP(-1);
-  available = available + TP(1);
-  TP upper = available + atol;
-  upper = upper + rounding;
-  if (p > upper) bits |= CS_FLAG_PATH_AVAILABLE;
-  if (pair_valid) {
-    TP r_right = eps * (p_right < 0 ? -p_right : p_right);
-    TP d = p - p_right;
-    TP pair_tol = atol + rounding;
-    pair_tol = pair_tol + r_right;
-    if (d < -pair_tol) bits |= CS_FLAG_PATH_INCREASING;
-    TP gap = static_cast<TP>(kp_right - kp);
-    TP gap_tol = gap + pair_tol;
-    if (d > gap_tol) bits |= CS_FLAG_PATH_GAP;
-  }
-  return bits;
-}
 
 template <typename Acc>
 __device__ inline Acc sigmoid_of(Acc x) {

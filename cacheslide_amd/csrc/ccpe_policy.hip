@@ -1,0 +1,147 @@
+// Checks of the CanonicalPositionPolicy transform for the MFMA policy prefill
+// (attention.py:32-57 over position.py:485-516), over dense bf16 keys at
+// coordinates 0..nk-1 with no attention mask.
+//
+// For a fixed query row the transform's result is the contextual row with the
+// fixed-key cells replaced by the profile's canonical row.  Its bounds check
+// (position.py:500-515: every cell a finite value in [0, P-1]) can only fail
+// at a canonical cell, and of the strict path checks (position.py:98-114)
+// contextual cells and pairs of adjacent contextual cells pass by
+// construction: a contextual position is a clamped suffix sum of the gates of
+// the keys from it to the query, each gate in [0, 1].  What remains is the
+// canonical cells, the pairs of adjacent fixed keys, and the pairs of a fixed
+// key with a dynamic neighbour; the latter need the contextual position of
+// that dynamic key, which is recomputed here the way the generic kernel forms
+// it (fp32 logits and sigmoid gates, fp64 suffix sum rounded once, clamped),
+// stopping once the sum reaches P-1.  One wave per (query row, head); rows
+// that are not fixed return at once.
+
+#include "common.h"
+#include "ccpe_path.h"
+
+namespace cs {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kD = 128;
+
+__device__ inline void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__global__ void __launch_bounds__(64 * kWaves) policy_check_kernel(policy_check_args a) {
+  __shared__ float qs[kWaves][kD];
+  __shared__ float bctx[kWaves][kPolicyMaxBoundary];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * kWaves + wave;
+  if (item >= static_cast<int64_t>(a.nq) * a.hq) return;  // no block barrier follows
+  const int row = static_cast<int>(item / a.hq), h = static_cast<int>(item % a.hq);
+  const int64_t qo = a.q_ord[row];
+  if (qo == -1) return;
+  int32_t* chunk = a.chunk_flags + row / a.chunk_rows;
+  if (qo < 0) {  // a fixed row the profile has no trace for: the lookup raises
+    if (lane == 0) atomicOr(chunk, kChunkHasFixedRow | kChunkUnknownRow);
+    return;
+  }
+  const int64_t qp = a.qpos[row];
+  const int64_t kend = qp + 1 < a.nk ? qp + 1 : a.nk;  // causal keys [0, kend)
+  const float top = static_cast<float>(a.npos - 1);
+  const float* crow = a.canon + h * a.c_s0 + qo * a.c_s1;
+  const int kvh = h / a.group;
+
+  if (a.strict) {
+    // contextual positions of the dynamic keys beside a fixed key
+    const uint16_t* qrow = a.q + row * a.q_s_tok + h * a.q_s_head;
+    for (int d = lane; d < kD; d += 64) qs[wave][d] = bf16_to_float(qrow[d]);
+    wave_sync();
+    const float sqrt_d = static_cast<float>(sqrt(static_cast<double>(kD)));
+    const int nb = *a.bnd_count;
+    for (int bi = 0; bi < nb; ++bi) {
+      const int64_t key = a.bnd_keys[bi];
+      float val = 0.f;
+      if (key < kend) {
+        double sum = 0.0;  // wave-uniform after each reduction
+        for (int64_t base = key; base < kend && sum < static_cast<double>(top); base += 64) {
+          const int64_t i = base + lane;
+          double g = 0.0;
+          if (i < kend) {
+            const uint16_t* kr = a.k + i * a.k_s_tok + kvh * a.k_s_head;
+            float dot = 0.f;
+            for (int d = 0; d < kD; ++d) dot += qs[wave][d] * bf16_to_float(kr[d]);
+            const float logit = dot / sqrt_d;
+            g = static_cast<double>(1.f / (1.f + expf(-logit)));
+          }
+          sum += wave_sum(g);
+        }
+        float pc = static_cast<float>(sum);
+        if (pc < 0.f) pc = 0.f;
+        if (pc > top) pc = top;
+        val = pc;
+      }
+      if (lane == 0) bctx[wave][bi] = val;
+    }
+    wave_sync();
+  }
+
+  // Right to left over the keys (lane = key), so the pair of the last lane of
+  // a tile takes the first key of the tile to its right.
+  int bits = 0;
+  bool out_of_range = false;
+  float prev_p = 0.f;
+  bool prev_known = false, prev_fixed = false;
+  const float atol = static_cast<float>(1e-6);
+  for (int64_t t = (a.nk + 63) / 64 - 1; t >= 0; --t) {
+    const int64_t j = t * 64 + lane;
+    const int64_t ko = j < a.nk ? a.k_ord[j] : -1;
+    const bool fixed = ko >= 0;
+    float pv = 0.f;
+    if (fixed) {
+      pv = crow[ko * a.c_s2];
+      if (!(pv >= 0.f && pv <= top)) out_of_range = true;  // NaN included
+    }
+    if (a.strict) {
+      const bool causal = j < kend;
+      bool known = causal && fixed;
+      if (causal && !fixed) {
+        const int slot = a.bnd_slot[j];
+        if (slot >= 0) {
+          pv = bctx[wave][slot];
+          known = true;
+        }
+      }
+      float right = __shfl_down(pv, 1, 64);
+      bool right_known = __shfl_down(known ? 1 : 0, 1, 64) != 0;
+      bool right_fixed = __shfl_down(fixed ? 1 : 0, 1, 64) != 0;
+      if (lane == 63) {
+        right = prev_p;
+        right_known = prev_known;
+        right_fixed = prev_fixed;
+      }
+      const bool pair = known && right_known && (fixed || right_fixed);
+      bits |= path_violations<float>(pv, known, right, pair, qp, j, j + 1, atol);
+      prev_p = __shfl(pv, 0, 64);
+      prev_known = __shfl(known ? 1 : 0, 0, 64) != 0;
+      prev_fixed = __shfl(fixed ? 1 : 0, 0, 64) != 0;
+    }
+  }
+  for (int off = 32; off > 0; off >>= 1) bits |= __shfl_xor(bits, off, 64);
+  const bool any_oob = __any(out_of_range);
+  if (lane == 0) atomicOr(chunk, bits | (any_oob ? kChunkCanonOutOfRange : 0) | kChunkHasFixedRow);
+}
+
+}  // namespace
+
+int launch_policy_check(const policy_check_args& a, hipStream_t stream) {
+  const int64_t items = static_cast<int64_t>(a.nq) * a.hq;
+  if (items == 0) return CS_OK;
+  const int64_t blocks = (items + kWaves - 1) / kWaves;
+  CS_REQUIRE(blocks < (int64_t(1) << 31), "too many rows for the policy checker");
+  hipLaunchKernelGGL(policy_check_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(64 * kWaves), 0, stream,
+                     a);
+  CS_LAUNCH_CHECK("ccpe_policy_check");
+  return CS_OK;
+}
+
+}  // namespace cs

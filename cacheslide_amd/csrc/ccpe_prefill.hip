@@ -55,6 +55,7 @@
 // lane's record.
 
 #include "common.h"
+#include "ccpe_path.h"
 
 namespace cs {
 namespace {
@@ -138,6 +139,13 @@ struct prefill_params {
   int32_t npos, tab_stride;
   uint16_t* out;
   int32_t* flags;
+  // Policy lowering (dense calls of the POLICY variant): selected rows, fixed
+  // keys as a bitmap (bit j % 32 of word j / 32), the canonical position of
+  // each (head, row)'s own key (NaN: no substitution) and the fixed-row map.
+  const uint8_t* sel_rows;
+  const uint32_t* fixed_bits;
+  const float* canon_self;  // [hq, nq]
+  const int64_t* q_ord;     // -1: not a fixed row
 };
 
 __device__ inline bf16x8 as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
@@ -190,8 +198,11 @@ struct stage_t {
   uint4 v[kStageSlots];
 };
 
-// WAVES wavefronts of 32 columns each; two wavefronts per SIMD
-template <int MODE, int WAVES>
+// WAVES wavefronts of 32 columns each; two wavefronts per SIMD.  POLICY (dense
+// K/V only): SelectedAssociationPolicy visibility and the canonical position
+// of each selected fixed row's own key, for calls in which every fixed query
+// row is selected (its only visible fixed key is then itself).
+template <int MODE, int WAVES, bool POLICY = false>
 __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(prefill_params p) {
   constexpr bool PAGED = MODE != 0;
   constexpr bool SLOTS = MODE == 2;
@@ -222,6 +233,17 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
   const bool row_ok = row < p.nq;
   const int nk = p.nk[b];
   const int64_t qp = row_ok ? p.qpos[b * p.qpos_sb + row] : -1;
+  bool sel_col = false;   // the column's row is selected: fixed keys other than its own are invisible
+  float canon_self = 0.f;  // canonical position of the column's own key (NaN: contextual)
+  if constexpr (POLICY) {
+    canon_self = __builtin_nanf("");
+    if (row_ok) {
+      sel_col = p.sel_rows[row] != 0;
+      if (p.canon_self) canon_self = p.canon_self[static_cast<int64_t>(head) * p.nq + row];
+      // a fixed row that is not selected sees every fixed key: not this variant
+      if (p.q_ord && p.q_ord[row] != -1 && !sel_col) atomicOr(p.flags, CS_FLAG_POLICY_GENERIC);
+    }
+  }
 
   if (tid == 0) wg_max_pos = 0;
   __syncthreads();
@@ -519,6 +541,14 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
   auto compute = [&](int t, const uint4* kst, const uint4* vst) {
     const int base = t * kTileN;
     if (base > wmax32) return;  // every column of the wave precedes the tile
+    uint32_t fixed_word = 0;
+    if constexpr (POLICY) {
+      // A tile of fixed keys is invisible to selected columns except at their
+      // own key, and a saturated column's positions no longer depend on its
+      // gates: when that holds for the whole wave, the tile adds nothing.
+      fixed_word = p.fixed_bits[t];
+      if (fixed_word == 0xFFFFFFFFu && __all(!row_ok || (sel_col && carry >= top))) return;
+    }
     // all K operands first, then the 8 MFMAs of S^T
     // key n, chunk 2 ks + h: slot (n / 4) * 64 + ((2 ks + h) ^ g) * 4 + n % 4 with
     // g = n / 4 % 4, i.e. one of two per-lane bases (ks even / odd) + 16 (ks / 2)
@@ -582,9 +612,19 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
       float start[4];  // position of the first (right-most) key of each run
 #pragma unroll
       for (int j4 = 0; j4 < 4; ++j4) start[j4] = carry + after[j4];
+      // the canonical position replaces the contextual one at the row's own key
+      // (CanonicalPositionPolicy; its other fixed x fixed cells are invisible)
+      int self_v = -1;
+      if constexpr (POLICY) {
+        const int self_key = static_cast<int>(qp) - base - 4 * h;  // 8 j4 + i for this lane's half
+        if (!__builtin_isnan(canon_self) && self_key >= 0 && self_key < kTileN - 4 * h &&
+            (self_key & 4) == 0)
+          self_v = 4 * (self_key >> 3) + (self_key & 3);
+      }
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         float pos = start[v >> 2] + gsuf[v];
+        if constexpr (POLICY) pos = v == self_v ? canon_self : pos;
         pos = pos < top ? pos : top;  // NaN becomes top: table reads stay in range
         pos = pos > 0.f ? pos : 0.f;
         const int lo = static_cast<int>(pos);  // pos >= 0: truncation is floor
@@ -598,6 +638,20 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
         s[v] = fmaf(bias, kSqrtD * kLn2, s[v]);
       }
       carry += total;
+    }
+    if constexpr (POLICY) {
+      // SelectedAssociationPolicy: fixed keys other than the row's own are
+      // invisible to selected rows (after the gates: the positions above
+      // still count them).  Lane (n, h) holds keys 8 j4 + 4h + i.
+      const int self_key = static_cast<int>(qp) - base;  // in [0, 32) when in this tile
+      uint32_t hide = sel_col ? fixed_word : 0u;
+      if (self_key >= 0 && self_key < kTileN) hide &= ~(1u << self_key);
+      hide = (hide >> (4 * h)) & 0x0F0F0F0Fu;
+      if (__any(hide != 0u)) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          if ((hide >> (8 * (v >> 2) + (v & 3))) & 1u) s[v] = -INFINITY;
+      }
     }
     // V^T operands, read after the bias work (not live across it, which keeps
     // registers for the 8 K operands above) and consumed after the softmax.
@@ -804,12 +858,15 @@ int fill_kv(const cs_kv_source* kv, cs::kv_addr* a) {
 }
 }  // namespace
 
-extern "C" int cs_ccpe_prefill_bf16(const void* q, int64_t q_s_batch, int64_t q_s_tok,
-                                    int64_t q_s_head, const int64_t* qpos, int64_t qpos_s_batch,
-                                    int32_t batch, int32_t nq, int32_t hq, int32_t hkv,
-                                    const int32_t* nk, const cs_kv_source* kv, const float* e,
-                                    int32_t max_positions, void* out, int32_t* flags,
-                                    void* stream) {
+namespace {
+
+// Validate a prefill call and fill its parameters, LDS size and wave count
+// (CS_OK, or an error code with the message set).
+int prepare_prefill(const void* q, int64_t q_s_batch, int64_t q_s_tok, int64_t q_s_head,
+                    const int64_t* qpos, int64_t qpos_s_batch, int32_t batch, int32_t nq, int32_t hq,
+                    int32_t hkv, const int32_t* nk, const cs_kv_source* kv, const float* e,
+                    int32_t max_positions, void* out, int32_t* flags, cs::prefill_params* pp,
+                    int* waves_out, size_t* smem_out) {
   CS_REQUIRE(q && qpos && nk && e && out && flags, "null arguments");
   CS_REQUIRE(batch >= 0 && nq >= 0 && hq > 0 && hkv > 0 && hq % hkv == 0, "bad head counts");
   CS_REQUIRE(max_positions >= 2 && max_positions <= kMaxPos, "max_positions must be in [2, %d]",
@@ -838,7 +895,6 @@ extern "C" int cs_ccpe_prefill_bf16(const void* q, int64_t q_s_batch, int64_t q_
     set_error("the MFMA prefill kernel needs a power-of-two block size (got %d)", kv->block_size);
     return CS_EUNSUPPORTED;
   }
-  if (batch == 0 || nq == 0) return CS_OK;
   p.q = static_cast<const uint16_t*>(q);
   p.q_sb = q_s_batch;
   p.q_st = q_s_tok;
@@ -876,6 +932,129 @@ extern "C" int cs_ccpe_prefill_bf16(const void* q, int64_t q_s_batch, int64_t q_
     set_error("prefill LDS %zu bytes exceeds the workgroup limit", smem + kStaticLds);
     return CS_EUNSUPPORTED;
   }
+  *pp = p;
+  *waves_out = waves;
+  *smem_out = smem;
+  return CS_OK;
+}
+
+// Fixed-key bitmap, the dynamic keys beside a fixed key (ascending, with a
+// per-key slot map) and the key count of a policy call: one workgroup.
+constexpr int kPackThreads = 1024;
+constexpr int kMaxBoundary = cs::kPolicyMaxBoundary;
+
+__global__ void __launch_bounds__(kPackThreads) policy_pack_kernel(const uint8_t* fixed_keys, int64_t nk,
+                                                                  uint32_t* bits, int32_t* bnd_count,
+                                                                  int32_t* bnd_keys, int32_t* bnd_slot,
+                                                                  int32_t* nk_dev, int32_t* flags) {
+  __shared__ int wave_count[kPackThreads / 64];
+  __shared__ int running;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (tid == 0) {
+    running = 0;
+    nk_dev[0] = static_cast<int32_t>(nk);
+  }
+  const int64_t words = (nk + 31) / 32;
+  for (int64_t w = tid; w < words; w += kPackThreads) {
+    uint32_t word = 0;
+    for (int i = 0; i < 32; ++i) {
+      const int64_t j = 32 * w + i;
+      if (j < nk && fixed_keys[j]) word |= 1u << i;
+    }
+    bits[w] = word;
+  }
+  __syncthreads();
+  for (int64_t base = 0; base < nk; base += kPackThreads) {
+    const int64_t j = base + tid;
+    bool bnd = false;
+    if (j < nk && !fixed_keys[j])
+      bnd = (j > 0 && fixed_keys[j - 1]) || (j + 1 < nk && fixed_keys[j + 1]);
+    const unsigned long long m = __ballot(bnd);
+    if (lane == 0) wave_count[wave] = __popcll(m);
+    __syncthreads();
+    int before = running;
+    for (int w = 0; w < wave; ++w) before += wave_count[w];
+    before += __popcll(m & ((1ull << lane) - 1ull));
+    if (j < nk) {
+      const bool kept = bnd && before < kMaxBoundary;
+      bnd_slot[j] = kept ? before : -1;
+      if (kept) bnd_keys[before] = static_cast<int32_t>(j);
+      if (bnd && !kept) atomicOr(flags, CS_FLAG_POLICY_GENERIC);  // more boundary keys than the checker holds
+    }
+    __syncthreads();
+    if (tid == 0) {
+      int add = 0;
+      for (int w = 0; w < kPackThreads / 64; ++w) add += wave_count[w];
+      running += add;
+    }
+    __syncthreads();
+  }
+  if (tid == 0) bnd_count[0] = running < kMaxBoundary ? running : kMaxBoundary;
+}
+
+// Canonical position of each (head, row)'s own key, NaN when the row is not a
+// fixed row the profile covers: canonical[h][q_ord[row]][k_ord[qpos[row]]].
+__global__ void policy_self_kernel(const float* canon, int64_t c_s0, int64_t c_s1, int64_t c_s2,
+                                   const int64_t* q_ord, const int64_t* k_ord, const int64_t* qpos,
+                                   int32_t nq, int32_t hq, int64_t nk, float* out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= static_cast<int64_t>(nq) * hq) return;
+  const int h = static_cast<int>(i / nq), row = static_cast<int>(i % nq);
+  float v = __builtin_nanf("");
+  const int64_t qo = q_ord[row];
+  const int64_t qp = qpos[row];
+  if (qo >= 0 && qp >= 0 && qp < nk) {
+    const int64_t ko = k_ord[qp];
+    if (ko >= 0) v = canon[h * c_s0 + qo * c_s1 + ko * c_s2];
+  }
+  out[i] = v;
+}
+
+constexpr int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+
+struct policy_ws {
+  int32_t* nk_dev;
+  uint32_t* bits;
+  int32_t* bnd_count;
+  int32_t* bnd_keys;
+  int32_t* bnd_slot;
+  float* canon_self;
+  int64_t bytes;
+};
+
+policy_ws carve_policy(char* base, int32_t nq, int32_t hq, int64_t nk) {
+  policy_ws w{};
+  int64_t off = 0;
+  auto take = [&](int64_t bytes) {
+    char* at = base ? base + off : nullptr;
+    off += align256(bytes);
+    return at;
+  };
+  w.nk_dev = reinterpret_cast<int32_t*>(take(16));
+  w.bits = reinterpret_cast<uint32_t*>(take(4 * ((nk + 31) / 32)));
+  w.bnd_count = reinterpret_cast<int32_t*>(take(16));
+  w.bnd_keys = reinterpret_cast<int32_t*>(take(4 * kMaxBoundary));
+  w.bnd_slot = reinterpret_cast<int32_t*>(take(4 * nk));
+  w.canon_self = reinterpret_cast<float*>(take(4 * static_cast<int64_t>(nq) * hq));
+  w.bytes = off;
+  return w;
+}
+
+}  // namespace
+
+extern "C" int cs_ccpe_prefill_bf16(const void* q, int64_t q_s_batch, int64_t q_s_tok,
+                                    int64_t q_s_head, const int64_t* qpos, int64_t qpos_s_batch,
+                                    int32_t batch, int32_t nq, int32_t hq, int32_t hkv,
+                                    const int32_t* nk, const cs_kv_source* kv, const float* e,
+                                    int32_t max_positions, void* out, int32_t* flags,
+                                    void* stream) {
+  cs::prefill_params p{};
+  int waves = 4;
+  size_t smem = 0;
+  const int st = prepare_prefill(q, q_s_batch, q_s_tok, q_s_head, qpos, qpos_s_batch, batch, nq, hq,
+                                 hkv, nk, kv, e, max_positions, out, flags, &p, &waves, &smem);
+  if (st) return st;
+  if (batch == 0 || nq == 0) return CS_OK;
   const dim3 grid(p.total_wg), block(64 * waves);
   hipStream_t s = as_stream(stream);
   const int mode = p.kv.slots ? 2 : (p.kv.block_table ? 1 : 0);
@@ -892,5 +1071,121 @@ extern "C" int cs_ccpe_prefill_bf16(const void* q, int64_t q_s_batch, int64_t q_
   else
     hipLaunchKernelGGL((ccpe_prefill_kernel<0, 4>), grid, block, smem, s, p);
   CS_LAUNCH_CHECK("ccpe_prefill");
+  return CS_OK;
+}
+
+extern "C" int64_t cs_ccpe_prefill_policy_workspace_bytes(int32_t nq, int32_t hq, int64_t nk) {
+  if (nq < 0 || hq <= 0 || nk < 0) return 0;
+  return carve_policy(nullptr, nq, hq, nk).bytes;
+}
+
+extern "C" int cs_ccpe_prefill_policy_bf16(const cs_ccpe_args* a, void* workspace,
+                                           int64_t workspace_bytes, void* stream) {
+  CS_REQUIRE(a != nullptr, "null arguments");
+  const cs_view& qv = a->q;
+  const cs_view& kv = a->k;
+  const cs_view& vv = a->v;
+  const cs_view& ev = a->e;
+  CS_REQUIRE(qv.data && kv.data && vv.data && ev.data && a->out.data && a->qpos && a->flags,
+             "null arguments");
+  CS_REQUIRE(qv.ndim == 3 && kv.ndim == 3 && vv.ndim == 3 && a->out.ndim == 3,
+             "q, k, v and out must be [tokens, heads, 128]");
+  CS_REQUIRE(qv.dtype == CS_BF16 && kv.dtype == CS_BF16 && vv.dtype == CS_BF16 && a->out.dtype == CS_BF16,
+             "the MFMA policy prefill takes bf16 q, k, v and out");
+  CS_REQUIRE(qv.shape[2] == kD && kv.shape[2] == kD && vv.shape[2] == kD && a->out.shape[2] == kD,
+             "the MFMA policy prefill needs head dim 128");
+  CS_REQUIRE(kv.shape[0] == vv.shape[0] && kv.shape[1] == vv.shape[1], "K and V must match");
+  CS_REQUIRE(a->out.shape[0] == qv.shape[0] && a->out.shape[1] == qv.shape[1] && a->out.stride[2] == 1 &&
+                 a->out.stride[1] == kD && a->out.stride[0] == kD * qv.shape[1],
+             "out must be contiguous [nq, Hq, 128]");
+  CS_REQUIRE(qv.stride[2] == 1 && kv.stride[2] == 1 && vv.stride[2] == 1, "rows must be contiguous");
+  CS_REQUIRE(ev.dtype == CS_F32 && ev.ndim == 2 && ev.shape[0] == kD && ev.stride[1] == 1 &&
+                 ev.stride[0] == ev.shape[1],
+             "e must be contiguous fp32 [128, P]");
+  CS_REQUIRE(a->kpos == nullptr, "the MFMA policy prefill takes the default key coordinates 0..nk-1");
+  CS_REQUIRE(!a->attn_mask.data && !a->vis_mask.data && !a->fixed_pos.data && !a->pos_out.data,
+             "the MFMA policy prefill takes no masks, fixed positions or position output");
+  CS_REQUIRE(a->sel_rows && a->fixed_keys, "the MFMA policy prefill needs the selected-row lowering");
+  const bool canon = a->canonical.data != nullptr;
+  if (canon) {
+    const cs_view& c = a->canonical;
+    CS_REQUIRE(c.ndim == 3 && c.shape[0] == qv.shape[1] && c.dtype == CS_F32 && a->q_ord && a->k_ord &&
+                   a->chunk_flags && a->chunk_rows > 0,
+               "canonical must be fp32 [Hq, F, F] with ordinal maps and chunk flags");
+  }
+  const int64_t nq64 = qv.shape[0], nk = kv.shape[0];
+  CS_REQUIRE(nq64 < (1ll << 31) && nk < (1ll << 31), "too many rows or keys");
+  const int32_t nq = static_cast<int32_t>(nq64), hq = static_cast<int32_t>(qv.shape[1]);
+  const int32_t hkv = static_cast<int32_t>(kv.shape[1]);
+  const policy_ws need = carve_policy(nullptr, nq, hq, nk);
+  CS_REQUIRE(workspace != nullptr && workspace_bytes >= need.bytes &&
+                 (reinterpret_cast<uintptr_t>(workspace) % 256) == 0,
+             "policy workspace holds %lld bytes, the call needs %lld (256-byte aligned)",
+             static_cast<long long>(workspace_bytes), static_cast<long long>(need.bytes));
+  const policy_ws w = carve_policy(static_cast<char*>(workspace), nq, hq, nk);
+  cs_kv_source src{};
+  src.k = kv.data;
+  src.v = vv.data;
+  src.k_s_tok = kv.stride[0];
+  src.k_s_head = kv.stride[1];
+  src.v_s_tok = vv.stride[0];
+  src.v_s_head = vv.stride[1];
+  cs::prefill_params p{};
+  int waves = 4;
+  size_t smem = 0;
+  const int st = prepare_prefill(qv.data, 0, qv.stride[0], qv.stride[1], a->qpos, 0, 1, nq, hq, hkv, w.nk_dev,
+                                 &src, static_cast<const float*>(ev.data), static_cast<int32_t>(ev.shape[1]),
+                                 a->out.data, a->flags, &p, &waves, &smem);
+  if (st) return st;
+  if (nq == 0) return CS_OK;
+  hipStream_t s = as_stream(stream);
+  hipLaunchKernelGGL(policy_pack_kernel, dim3(1), dim3(kPackThreads), 0, s, a->fixed_keys, nk, w.bits,
+                     w.bnd_count, w.bnd_keys, w.bnd_slot, w.nk_dev, a->flags);
+  p.sel_rows = a->sel_rows;
+  p.fixed_bits = w.bits;
+  if (canon) {
+    const cs_view& c = a->canonical;
+    const int64_t cells = static_cast<int64_t>(nq) * hq;
+    hipLaunchKernelGGL(policy_self_kernel, dim3(static_cast<uint32_t>((cells + 255) / 256)), dim3(256), 0, s,
+                       static_cast<const float*>(c.data), c.stride[0], c.stride[1], c.stride[2], a->q_ord,
+                       a->k_ord, a->qpos, nq, hq, nk, w.canon_self);
+    p.canon_self = w.canon_self;
+    p.q_ord = a->q_ord;
+  }
+  const dim3 grid(p.total_wg), block(64 * waves);
+  if (waves == 8)
+    hipLaunchKernelGGL((ccpe_prefill_kernel<0, 8, true>), grid, block, smem, s, p);
+  else
+    hipLaunchKernelGGL((ccpe_prefill_kernel<0, 4, true>), grid, block, smem, s, p);
+  CS_LAUNCH_CHECK("ccpe_prefill_policy");
+  if (canon) {
+    cs::policy_check_args c{};
+    c.q = static_cast<const uint16_t*>(qv.data);
+    c.q_s_tok = qv.stride[0];
+    c.q_s_head = qv.stride[1];
+    c.k = static_cast<const uint16_t*>(kv.data);
+    c.k_s_tok = kv.stride[0];
+    c.k_s_head = kv.stride[1];
+    c.qpos = a->qpos;
+    c.nq = nq;
+    c.hq = hq;
+    c.group = hq / hkv;
+    c.nk = nk;
+    c.canon = static_cast<const float*>(a->canonical.data);
+    c.c_s0 = a->canonical.stride[0];
+    c.c_s1 = a->canonical.stride[1];
+    c.c_s2 = a->canonical.stride[2];
+    c.q_ord = a->q_ord;
+    c.k_ord = a->k_ord;
+    c.bnd_count = w.bnd_count;
+    c.bnd_keys = w.bnd_keys;
+    c.bnd_slot = w.bnd_slot;
+    c.npos = static_cast<int32_t>(ev.shape[1]);
+    c.strict = a->strict;
+    c.chunk_rows = a->chunk_rows;
+    c.chunk_flags = a->chunk_flags;
+    const int cst = cs::launch_policy_check(c, s);
+    if (cst) return cst;
+  }
   return CS_OK;
 }

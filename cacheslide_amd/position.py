@@ -12,6 +12,8 @@ the exception of the first failing check in the reference's order.
 
 from __future__ import annotations
 
+import ctypes
+
 import math
 import re
 from collections import Counter
@@ -620,7 +622,11 @@ def cope_attention(
         keep += [sel_rows, fixed_keys]
         args.sel_rows = ptr(sel_rows)
         args.fixed_keys = ptr(fixed_keys)
-    call("cs_ccpe_attention", args, ck.stream)
+    if not (selected is not None and default_keys
+            and _policy_fast_ok(query, key, value, e, cope, amask, visibility_mask, fixed_positions,
+                                return_positions, lowered if canonical is not None else None)
+            and _policy_prefill(args, query, key, chunk_flags, ck)):
+        call("cs_ccpe_attention", args, ck.stream)
     ck.device_step(_hip.FLAG_LOGIT_NONFINITE, ValueError, "attention logits overflowed the accumulation dtype")
     ck.device_step(_hip.FLAG_POS_INVALID, ValueError, "positions must be bounded query-dependent [head,query,key]")
     ck.device_step(_hip.FLAG_SCORE_NONFINITE, ValueError, "contextual attention logits are not finite")
@@ -653,6 +659,43 @@ def _raise_policy_errors(ck: _Checks, chunk_flags: Tensor, lowered) -> None:
                 raise CCPEPositionError(text)
         if value & CHUNK_CANON_OUT_OF_RANGE:  # then the bounds check of its result
             raise CCPEPositionError(_TRANSFORM_BOUNDS_MESSAGE)
+
+
+def _policy_fast_ok(query, key, value, e, cope, amask, visibility_mask, fixed_positions, return_positions,
+                    lowered) -> bool:
+    """The reuse call of runtime.py:576-609 on MFMA: the dense fast path's
+    conditions with a SelectedAssociationPolicy and, if any, an fp32 profile."""
+    if not _fast_path_ok(query, key, value, e, cope, amask, visibility_mask, fixed_positions, None, None,
+                         return_positions):
+        return False
+    return lowered is None or lowered.canonical.dtype == torch.float32
+
+
+def _policy_prefill(args, query: Tensor, key: Tensor, chunk_flags: Tensor | None, ck: _Checks) -> bool:
+    """cs_ccpe_prefill_policy_bf16 into args.out; False when the call needs the
+    generic kernel (an unsupported layout, or a fixed query row that is not
+    selected: its flag is cleared and the chunk flags reset for that run)."""
+    device = ck.device
+    lib = _hip.load()
+    nq, hq, nk = query.shape[0], query.shape[1], key.shape[0]
+    need = int(lib.cs_ccpe_prefill_policy_workspace_bytes(nq, hq, nk))
+    workspace = torch.empty(need + 256, dtype=torch.uint8, device=device)
+    start = (-workspace.data_ptr()) % 256
+    kpos = args.kpos
+    args.kpos = None  # keys at their default coordinates 0..nk-1
+    try:
+        status = lib.cs_ccpe_prefill_policy_bf16(ctypes.byref(args), workspace.data_ptr() + start, need, ck.stream)
+    finally:
+        args.kpos = kpos
+    if status == _hip.CS_EUNSUPPORTED:
+        return False
+    _hip.check(status, "cs_ccpe_prefill_policy_bf16")
+    if not _hip.read_flags(ck.flags)[0] & _hip.FLAG_POLICY_GENERIC:
+        return True
+    ck.flags.bitwise_and_(~_hip.FLAG_POLICY_GENERIC)
+    if chunk_flags is not None:
+        chunk_flags.zero_()
+    return False
 
 
 def _fast_path_ok(query, key, value, e, cope, amask, visibility_mask, fixed_positions, canonical,

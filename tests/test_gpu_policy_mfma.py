@@ -1,0 +1,193 @@
+"""The reuse call of ``CacheSlideRuntime._attend`` (src/cacheslide_vllm/
+runtime.py:576-609) on the MFMA policy path: bf16 Q/K/V with head dim 128,
+dense keys at coordinates 0..n-1, a ``CanonicalPositionPolicy``
+(attention.py:18-57) and a ``SelectedAssociationPolicy`` in updated_and_self
+mode (attention.py:60-72) whose selected rows are every fixed query row.
+
+Checked against the oracle's per-chunk evaluation of the two policies
+(oracle/ccpe.py canonical_policy, selected_visibility, cope_attention): the
+same decision (accept, or the same error type and message from the same
+chunk) and, when accepted, outputs within the bf16 tolerance (2e-2 absolute,
+1e-2 relative).  Each test also checks which kernel ran: the MFMA path, or the
+generic kernel when some fixed query row is not selected.
+
+Layout: reused chunk A, a recomputed chunk, reused chunk B (make_plan);
+8 query heads over 2 KV heads; CoPE P = 64, table N(0, 0.1).  The profile is
+calibrated on the oracle (contextual positions of the fixed x fixed cells of
+a calibration layout: the same chunks, the recomputed chunk ``shift`` tokens
+longer), optionally perturbed or missing some ordinals.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import cacheslide_amd.position as position_module
+from cacheslide_amd import CanonicalPositionPolicy, CCPEPositionError, CoPE, SelectedAssociationPolicy, cope_attention
+from oracle import ccpe as orc
+from tests._helpers import assert_close_bf16
+from tests.test_gpu_policies import make_plan, oracle_run, profile_for
+
+pytestmark = pytest.mark.gpu
+
+HQ, HKV, D, P = 8, 2, 128, 64
+
+
+def bf16_normal(rng, shape, scale=1.0):
+    x = torch.from_numpy((rng.standard_normal(shape) * scale).astype(np.float32)).to(torch.bfloat16)
+    return x.float().numpy()
+
+
+def contextual(q, k, rows):
+    allowed = orc.allowed_mask(rows, np.arange(k.shape[0]), HQ)
+    return orc.contextual_positions(orc.logits(q[rows], k), allowed, P)
+
+
+def scenario(seed, *, a, dyn, b, shift=0, perturb=0.0, drop=0, n_sel=60):
+    plan = make_plan(a, dyn, b)
+    n = a + dyn + b
+    rng = np.random.default_rng(seed)
+    q, k, v = bf16_normal(rng, (n, HQ, D)), bf16_normal(rng, (n, HKV, D)), bf16_normal(rng, (n, HKV, D))
+    e = (rng.standard_normal((D, P)) * 0.1).astype(np.float32)
+    fixed = np.array(plan.fixed_indices)
+    cq = np.concatenate([q[:a], bf16_normal(rng, (dyn + shift, HQ, D)) if shift else q[a:a + dyn], q[a + dyn:]])
+    ck = np.concatenate([k[:a], bf16_normal(rng, (dyn + shift, HKV, D)) if shift else k[a:a + dyn], k[a + dyn:]])
+    cal_fixed = np.concatenate([np.arange(a), np.arange(a + dyn + shift, n + shift)])
+    cal = contextual(cq, ck, cal_fixed)[:, :, cal_fixed]
+    if perturb:
+        cal = np.clip(cal + rng.standard_normal(cal.shape).astype(np.float32) * perturb, 0, P - 1)
+    sel = np.sort(rng.choice(fixed, n_sel, replace=False))
+    ordinal_of = {int(pos): i for i, pos in enumerate(fixed)}
+    dropped = {ordinal_of[int(p)] for p in rng.choice(sel, drop, replace=False)} if drop else set()
+    ordinals = sorted(set(range(len(fixed))) - dropped)
+    rows = np.unique(np.concatenate([sel, np.arange(a, a + dyn)]))
+    rows = rows[rng.permutation(len(rows))]
+    return q, k, v, e, rows, plan, cal[:, ordinals], ordinals, sel
+
+
+def device_run(q, k, v, e, rows, plan, profile, mode, selected, chunk, device, monkeypatch):
+    """cope_attention on the device -> (decision, kernels called)."""
+    called = []
+    real = position_module.call
+
+    def spy(name, *args):
+        called.append(name)
+        return real(name, *args)
+
+    monkeypatch.setattr(position_module, "call", spy)
+    cope = CoPE(D, P, device=device)
+    with torch.no_grad():
+        cope.position_embeddings.copy_(torch.from_numpy(e))
+    policy = CanonicalPositionPolicy(plan, profile, "ckpt", mode=mode) if profile is not None else None
+    visibility = SelectedAssociationPolicy(plan.fixed_indices, torch.tensor(selected, device=device))
+    as_bf16 = lambda x: torch.from_numpy(x).to(device=device, dtype=torch.bfloat16)  # noqa: E731
+    try:
+        out = cope_attention(as_bf16(q[rows]), as_bf16(k), as_bf16(v), cope, torch.from_numpy(rows).to(device),
+                             positions_transform=policy, visibility_transform=visibility, query_chunk_size=chunk)
+        result = ("ok", out)
+    except CCPEPositionError as err:
+        result = ("error", CCPEPositionError, str(err))
+    except ValueError as err:
+        result = ("error", ValueError, str(err))
+    monkeypatch.setattr(position_module, "call", real)
+    return result, called
+
+
+def compare(expected, actual):
+    assert expected[0] == actual[0], (expected[:1] + expected[1:] if expected[0] == "error" else "ok", actual[:3])
+    if expected[0] == "error":
+        assert expected[1] is actual[1] and expected[2] == actual[2], (expected, actual)
+        return
+    assert_close_bf16(actual[1], expected[1])
+
+
+BIG = dict(a=700, dyn=150, b=900, n_sel=60)
+SMALL = dict(a=40, dyn=30, b=60, n_sel=50)   # positions never saturate: the boundary pairs decide
+
+CASES = {
+    # name: (layout, seed, shift, perturb, drop, mode, chunk, expected decision)
+    "same_layout_strict": (BIG, 1, 0, 0.0, 0, "strict_contextual", 64, "ok"),
+    "same_layout_mixed": (BIG, 2, 0, 0.0, 0, "mixed_bias_override", 64, "ok"),
+    "shifted_strict": (BIG, 3, 24, 0.0, 0, "strict_contextual", 64, "ok"),
+    "shifted_mixed": (BIG, 4, 24, 0.0, 0, "mixed_bias_override", 32, "ok"),
+    "perturbed_strict": (BIG, 5, 0, 0.05, 0, "strict_contextual", 48, "error"),
+    "perturbed_mixed": (BIG, 6, 0, 0.5, 0, "mixed_bias_override", 128, "ok"),
+    "untraced_strict": (BIG, 7, 0, 0.0, 4, "strict_contextual", 32, "error"),
+    # the fixed key before the recomputed chunk against its contextual neighbour:
+    # the calibration chunk was longer (gap) or its gates summed lower (order)
+    "boundary_gap_strict": (SMALL, 20, 8, 0.0, 0, "strict_contextual", 16, "error"),
+    "boundary_order_strict": (SMALL, 20, 4, 0.0, 0, "strict_contextual", 16, "error"),
+    "boundary_mixed": (SMALL, 20, 8, 0.0, 0, "mixed_bias_override", 16, "ok"),
+}
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_mfma_policy_call_matches_oracle(device, monkeypatch, name):
+    """BIG: a 700-token chunk, 150 recomputed tokens, a 900-token chunk, 60
+    selected fixed rows and the recomputed rows; tiles of A's fixed keys are
+    skipped once a selected row's positions saturate.  SMALL: 40 + 30 + 60."""
+    layout, seed, shift, perturb, drop, mode, chunk, want = CASES[name]
+    q, k, v, e, rows, plan, canonical, ordinals, sel = scenario(seed, shift=shift, perturb=perturb, drop=drop,
+                                                                **layout)
+    strict = mode == "strict_contextual"
+    expected = oracle_run(q, k, v, e, rows, plan, canonical, ordinals, strict, sel, chunk)
+    assert expected[0] == want, expected[:3] if expected[0] == "error" else "ok"
+    actual, called = device_run(q, k, v, e, rows, plan, profile_for(plan, canonical, ordinals), mode, sel, chunk,
+                                device, monkeypatch)
+    compare(expected, actual)
+    assert "cs_ccpe_attention" not in called, called
+
+
+def test_selected_rows_without_profile(device, monkeypatch):
+    """Visibility policy alone (a layer without a profile): the MFMA path."""
+    q, k, v, e, rows, plan, _, _, sel = scenario(9, a=500, dyn=200, b=640)
+    fixed = list(plan.fixed_indices)
+
+    def visibility(qpos, kpos):
+        return orc.selected_visibility(qpos, kpos, fixed, sel)
+
+    want = orc.cope_attention(q[rows], k, v, e, rows, visibility_transform=visibility, query_chunk_size=64)
+    actual, called = device_run(q, k, v, e, rows, plan, None, "strict_contextual", sel, 64, device, monkeypatch)
+    assert actual[0] == "ok"
+    assert_close_bf16(actual[1], want)
+    assert "cs_ccpe_attention" not in called
+
+
+def test_unselected_fixed_row_runs_the_generic_kernel(device, monkeypatch):
+    """A fixed query row outside the selected set sees every fixed key with
+    its canonical position: the MFMA path flags the call and the generic
+    kernel runs it instead, with the oracle's result."""
+    q, k, v, e, rows, plan, canonical, ordinals, sel = scenario(10, a=300, dyn=100, b=400)
+    partial = sel[1:]                       # sel[0] stays an active fixed row, now not selected
+    expected = oracle_run(q, k, v, e, rows, plan, canonical, ordinals, False, partial, 64)
+    actual, called = device_run(q, k, v, e, rows, plan, profile_for(plan, canonical, ordinals),
+                                "mixed_bias_override", partial, 64, device, monkeypatch)
+    compare(expected, actual)
+    assert "cs_ccpe_attention" in called
+
+
+def test_policy_errors_in_chunk_order(device, monkeypatch):
+    """One row per chunk: a recomputed row, a fixed row whose own canonical
+    cell claims 60 positions with one key available, a fixed row with an
+    out-of-range cell at a future key; strict mode raises the path error of
+    the first failing chunk, mixed mode the bounds error, and reordering the
+    rows reorders the decision."""
+    q, k, v, e, _, plan, canonical, ordinals, sel = scenario(11, a=300, dyn=100, b=400)
+    fixed = list(plan.fixed_indices)
+    bad_self, bad_future = 250, 500           # ordinals of two fixed rows
+    canonical = canonical.copy()
+    canonical[:, bad_self, bad_self] = 60.0
+    canonical[:, bad_future, 650] = P + 3.0   # key fixed[650] lies after row fixed[500]
+    profile = profile_for(plan, canonical, ordinals)
+    sel = np.unique(np.concatenate([sel, [fixed[bad_self], fixed[bad_future]]]))
+    for mode, order in (("strict_contextual", [320, fixed[bad_self], fixed[bad_future]]),
+                        ("strict_contextual", [320, fixed[bad_future], fixed[bad_self]]),
+                        ("mixed_bias_override", [320, fixed[bad_self], fixed[bad_future]])):
+        rows = np.array(order)
+        expected = oracle_run(q, k, v, e, rows, plan, canonical, ordinals, mode == "strict_contextual", sel, 1)
+        actual, called = device_run(q, k, v, e, rows, plan, profile, mode, sel, 1, device, monkeypatch)
+        compare(expected, actual)
+        assert actual[0] == "error", (mode, order)
+        assert "cs_ccpe_attention" not in called
