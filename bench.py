@@ -12,7 +12,8 @@ Also reported, each in a sub-record of the same JSON line: the decode
 kernel at the 64-request x 32k-context shape (one layer's distinct KV, 8.6 GB
 per call, one request checked against the oracle), end-to-end greedy decoding
 of a random Mistral-7B-shaped model over 64 x 32k-token reused contexts, the
-SLIDE relocation step,
+reuse call's attention with both runtime policies (MFMA path and generic
+kernel on the same call), the SLIDE relocation step,
 the WCA update, the selective-prefill rows and the layer-snapshot reads.  The
 CPU baselines time the torch CPU restatement of the reference path
 (oracle/torch_cpu.py, the reference's op order) on bounded samples of the
@@ -486,6 +487,90 @@ def decode_e2e_measure(device, tokens: int = 128, warmup: int = 4) -> dict:
     }
 
 
+def reuse_measure(device, steps: int = 5) -> dict:
+    """The reuse call of runtime.py:576-609 at a 16384-token context: 8 reused
+    chunks of 2016 tokens (16128 fixed) and a recomputed 256-token question;
+    the active rows are 15% of the fixed rows (2420, seeded, as WCA selects
+    them) and the question's rows, 32q/8kv heads x 128, bf16 Q/K/V ~ N(0, 1),
+    CoPE P = 64 (table N(0, 0.1)), strict_contextual canonical positions from
+    a [32, 16128, 16128] fp32 profile (one calibration-like path 0.5 per token
+    shared by the heads, a broadcast view), updated_and_self visibility.  Timed:
+    cope_attention on the MFMA policy path (``steps`` calls) and, once, the same
+    call on the generic kernel (explicit key coordinates); the two outputs
+    are compared."""
+    import math
+
+    import torch
+
+    from cacheslide_amd import (CCPEProfile, CanonicalPositionPolicy, ChunkIdentity, CoPE, RequestPlan,
+                                SelectedAssociationPolicy, cope_attention)
+
+    CH, CHUNKS, DYN, HQ, HKV, D, P = 2016, 8, 256, 32, 8, 128, 64
+    F = CH * CHUNKS
+    n = F + DYN
+    spec = [{"id": f"C{i}", "role": "reuse", "start": i * CH, "end": (i + 1) * CH} for i in range(CHUNKS)]
+    spec.append({"id": "question", "role": "recompute", "start": F, "end": n})
+    plan = RequestPlan.parse({"version": 1, "namespace": "bench", "task_id": "reuse", "operation": "reuse",
+                              "chunks": spec}, [(7 * i) % 32000 for i in range(n)])
+    gen = torch.Generator(device=device).manual_seed(6006)
+    q_all = torch.randn((n, HQ, D), generator=gen, device=device).to(torch.bfloat16)
+    k = torch.randn((n, HKV, D), generator=gen, device=device).to(torch.bfloat16)
+    v = torch.randn((n, HKV, D), generator=gen, device=device).to(torch.bfloat16)
+    cope = CoPE(D, P, device=device)
+    with torch.no_grad():
+        cope.position_embeddings.copy_(torch.randn((D, P), generator=seed_gen(6, 1)) * 0.1)
+    n_sel = math.ceil(0.15 * F)
+    sel = torch.randperm(F, generator=seed_gen(6, 2))[:n_sel].sort().values
+    rows = torch.cat([sel, torch.arange(F, n)]).to(device)
+    ords = torch.arange(F, device=device, dtype=torch.float32)
+    path = ((ords[:, None] - ords[None, :] + 1) * 0.5).clamp_(0, P - 1)
+    path.masked_fill_(ords[None, :] > ords[:, None], 0.0)        # future keys: in bounds, never validated
+    profile = CCPEProfile(trained_profile_version="v1", checkpoint_id="ckpt",
+                          chunks=tuple(ChunkIdentity(*c) for c in plan.fixed_layout),
+                          query_positions=torch.arange(F), key_positions=torch.arange(F),
+                          canonical_positions=path.expand(HQ, F, F), max_positions=P, histogram_bin_width=0.25,
+                          sample_count=1)
+    policy = CanonicalPositionPolicy(plan, profile, "ckpt", mode="strict_contextual")
+    visibility = SelectedAssociationPolicy(plan.fixed_indices, sel.to(device))
+    q = q_all[rows].contiguous()
+    keys = torch.arange(n, device=device)
+
+    def run(explicit_keys=False):
+        return cope_attention(q, k, v, cope, rows, keys if explicit_keys else None, positions_transform=policy,
+                              visibility_transform=visibility, query_chunk_size=64)
+
+    out = run()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        out = run()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    t0 = time.perf_counter()
+    ref = run(explicit_keys=True)
+    torch.cuda.synchronize()
+    ms_generic = (time.perf_counter() - t0) * 1e3
+    err = float((out.float() - ref.float()).abs().max())
+    causal = float((rows.double() + 1).sum())
+    flops = 4.0 * HQ * D * causal + 2.0 * HQ * D * P * len(rows)
+    canon_bytes = n_sel * HQ * F * 4
+    del path, profile, policy
+    torch.cuda.empty_cache()
+    return {
+        "workload": "cope_attention reuse call: 16384 keys (8 reused chunks x 2016 + 256 recomputed), 2676 active "
+                    "rows (2420 selected fixed + 256), 32q/8kv heads x 128, bf16, P=64, strict canonical profile "
+                    "[32, 16128, 16128] fp32, updated_and_self visibility",
+        "ms_per_call": round(ms, 3),
+        "generic_ms_per_call": round(ms_generic, 2),
+        "speedup_vs_generic": round(ms_generic / ms, 1),
+        "max_abs_diff_vs_generic": round(err, 5),
+        "reference_flop_per_call": flops,
+        "reference_equivalent_TFLOPs": round(flops / (ms * 1e-3) / 1e12, 1),
+        "canonical_bytes_checked": canon_bytes,
+        "canonical_GBs_whole_call": round(canon_bytes / (ms * 1e-3) / 1e9, 1),
+    }
+
+
 def note(message: str) -> None:
     """Progress line on stderr (stdout carries only the JSON record)."""
     print(f"bench: {message}", file=sys.stderr, flush=True)
@@ -886,6 +971,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end decoding run")
+    ap.add_argument("--no-reuse", action="store_true", help="skip the reuse-call attention")
     ap.add_argument("--e2e-tokens", type=int, default=128)
     ap.add_argument("--no-slide", action="store_true")
     ap.add_argument("--slide-layers", type=int, default=32)
@@ -951,6 +1037,9 @@ def main() -> int:
     if not args.no_e2e:
         record["decode_e2e"] = decode_e2e_measure(device, args.e2e_tokens)
         note(f"decode e2e: {record['decode_e2e']['tok_per_s']} tok/s")
+    if not args.no_reuse:
+        record["reuse"] = reuse_measure(device)
+        note(f"reuse: {record['reuse']['ms_per_call']} ms/call (generic {record['reuse']['generic_ms_per_call']})")
     if not args.no_slide:
         try:
             record["slide"] = slide_measure(device, max(3, args.steps // 10), args.slide_layers)

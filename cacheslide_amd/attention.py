@@ -27,27 +27,46 @@ CHUNK_UNKNOWN_ROW = 1 << 29     # ... one whose ordinal the profile has no trace
 CHUNK_CANON_OUT_OF_RANGE = 1 << 28  # a substituted canonical cell outside [0, P-1]
 
 
+_FIXED_CACHE: dict[int, tuple] = {}
+
+
+def _fixed_positions(fixed: tuple[int, ...]) -> Tensor:
+    """The plan's fixed positions as a CPU int64 tensor (ascending, as the plan
+    lists them), cached per tuple: the runtime reuses one plan for every layer."""
+    hit = _FIXED_CACHE.get(id(fixed))
+    if hit is not None and hit[0] is fixed:
+        return hit[1]
+    tensor = torch.tensor(fixed, dtype=torch.long)
+    if len(_FIXED_CACHE) >= 8:
+        _FIXED_CACHE.clear()
+    _FIXED_CACHE[id(fixed)] = (fixed, tensor)
+    return tensor
+
+
 class _LoweredCanonical:
     """Kernel inputs for one CanonicalPositionPolicy over one call's coordinates."""
 
     def __init__(self, policy: "CanonicalPositionPolicy", device, query_positions, key_positions):
-        fixed = policy.plan.fixed_indices
-        ordinal = {pos: i for i, pos in enumerate(fixed)}
+        fixed = _fixed_positions(policy.plan.fixed_indices)
+        count = fixed.numel()
         profile = policy.profile
-        known = {pos: index for index, pos in enumerate(profile.query_positions.tolist())}
-        size = (max(fixed) + 1) if fixed else 1
-        q_table = [-1] * size
-        k_table = [-1] * size
-        self.unknown = False
-        for pos, o in ordinal.items():
-            k_table[pos] = o
-            if o in known:
-                q_table[pos] = known[o]
-            else:
-                q_table[pos] = -2
-                self.unknown = True
-        q_dev = torch.tensor(q_table, dtype=torch.long, device=device)
-        k_dev = torch.tensor(k_table, dtype=torch.long, device=device)
+        traced = profile.query_positions.detach().to("cpu", torch.long).reshape(-1)
+        size = int(fixed.max()) + 1 if count else 1
+        # profile row of each fixed ordinal, -2 when untraced (for a repeated
+        # ordinal, its last row)
+        rows_of = torch.full((count,), -2, dtype=torch.long)
+        inside = (traced >= 0) & (traced < count)
+        if count and bool(inside.any()):
+            rows_of.scatter_reduce_(0, traced[inside], torch.arange(traced.numel())[inside], reduce="amax",
+                                    include_self=False)
+        self.unknown = bool((rows_of == -2).any())
+        q_table = torch.full((size,), -1, dtype=torch.long)
+        k_table = torch.full((size,), -1, dtype=torch.long)
+        if count:
+            q_table[fixed] = rows_of
+            k_table[fixed] = torch.arange(count)
+        q_dev = q_table.to(device)
+        k_dev = k_table.to(device)
         self.q_rows = torch.empty(query_positions.shape[0], dtype=torch.long, device=device)
         self.k_ord = torch.empty(key_positions.shape[0], dtype=torch.long, device=device)
         stream = _hip.stream_of(device)
@@ -57,8 +76,8 @@ class _LoweredCanonical:
              key_positions.shape[0], stream)
         self._tables = (q_dev, k_dev)
         self.canonical = policy._canonical_on(device)
-        self.profile_rows = len(known)
-        self.fixed_count = len(fixed)
+        self.profile_rows = int(torch.unique(traced).numel())
+        self.fixed_count = count
         chunks = tuple(ChunkIdentity(*entry) for entry in policy.plan.fixed_layout)
         self.reason = profile.lookup_reason(
             chunks, None, None, policy.checkpoint_id, profile.trained_profile_version
@@ -166,9 +185,12 @@ class SelectedAssociationPolicy:
     selected_indices: Tensor
 
     def _sets(self, device) -> tuple[Tensor, Tensor]:
-        fixed = torch.tensor(self.fixed_indices, dtype=torch.long, device=device)
-        selected = self.selected_indices.to(device=device, dtype=torch.long).contiguous()
-        return fixed, selected
+        """Fixed and selected positions on the device, each sorted ascending
+        (the kernels test membership by binary search)."""
+        fixed = _fixed_positions(tuple(self.fixed_indices)).to(device)
+        fixed = torch.sort(fixed).values
+        selected = self.selected_indices.to(device=device, dtype=torch.long).reshape(-1)
+        return fixed, torch.sort(selected).values
 
     def _lower(self, device, query_positions: Tensor, key_positions: Tensor) -> tuple[Tensor, Tensor]:
         fixed, selected = self._sets(device)

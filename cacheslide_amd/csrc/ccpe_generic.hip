@@ -473,15 +473,18 @@ __global__ void __launch_bounds__(64 * kGenWaves) positional_bias_kernel(
   if (__any(bad) && lane == 0) atomicOr(flags, CS_FLAG_POS_INVALID);
 }
 
+// Membership by binary search: `set` is sorted ascending.
 __global__ void isin_kernel(const int64_t* values, int64_t n, const int64_t* set, int64_t m,
                             uint8_t* out) {
   int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
   if (i >= n) return;
-  int64_t x = values[i];
-  uint8_t hit = 0;
-  for (int64_t s = 0; s < m; ++s)
-    if (set[s] == x) { hit = 1; break; }
-  out[i] = hit;
+  const int64_t x = values[i];
+  int64_t lo = 0, hi = m;  // first element >= x
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (set[mid] < x) lo = mid + 1; else hi = mid;
+  }
+  out[i] = (lo < m && set[lo] == x) ? 1 : 0;
 }
 
 __global__ void selected_visibility_kernel(const int64_t* queries, int64_t nq,

@@ -48,6 +48,35 @@ __device__ inline int path_violations(TP p, bool valid, TP p_right, bool pair_va
   return bits;
 }
 
+// path_violations<float> for keys at coordinates 0..n-1 (a unit gap to the
+// right-hand neighbour), with diff = qp - kp >= 0: the same operations in the
+// same order, 32-bit coordinates.
+__device__ inline int path_violations_unit(float p, bool valid, float p_right, bool pair_valid, int32_t diff,
+                                           float atol) {
+#pragma clang fp contract(off)
+  int bits = 0;
+  if (!valid) return 0;
+  const float eps = pos_traits<float>::eps();
+  const float rounding = eps * (p < 0 ? -p : p);
+  const float neg_tol = atol + rounding;
+  if (p < -neg_tol) bits |= CS_FLAG_PATH_NEGATIVE;
+  float available = static_cast<float>(diff);
+  available = available + 1.f;
+  float upper = available + atol;
+  upper = upper + rounding;
+  if (p > upper) bits |= CS_FLAG_PATH_AVAILABLE;
+  if (pair_valid) {
+    const float r_right = eps * (p_right < 0 ? -p_right : p_right);
+    const float d = p - p_right;
+    float pair_tol = atol + rounding;
+    pair_tol = pair_tol + r_right;
+    if (d < -pair_tol) bits |= CS_FLAG_PATH_INCREASING;
+    const float gap_tol = 1.f + pair_tol;
+    if (d > gap_tol) bits |= CS_FLAG_PATH_GAP;
+  }
+  return bits;
+}
+
 // chunk bits of the canonical-policy lowering (besides CS_FLAG_PATH_*)
 constexpr int32_t kChunkHasFixedRow = 1 << 30;       // the chunk holds a fixed query row
 constexpr int32_t kChunkUnknownRow = 1 << 29;        // ... whose ordinal the profile lacks
@@ -69,10 +98,9 @@ struct policy_check_args {
   const float* canon;
   int64_t c_s0, c_s1, c_s2;
   const int64_t* q_ord;
-  const int64_t* k_ord;
-  const int32_t* bnd_count;  // dynamic keys beside a fixed key: count,
-  const int32_t* bnd_keys;   // ascending keys,
-  const int32_t* bnd_slot;   // and each key's index in bnd_keys (-1: none)
+  const int32_t* code;       // per key: fixed ordinal (>= 0), -2 - s (boundary slot s), -1
+  const int32_t* bnd_count;  // dynamic keys beside a fixed key: count
+  const int32_t* bnd_keys;   // and the keys, ascending
   int32_t npos, strict, chunk_rows;
   int32_t* chunk_flags;
 };

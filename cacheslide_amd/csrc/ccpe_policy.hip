@@ -85,46 +85,69 @@ __global__ void __launch_bounds__(64 * kWaves) policy_check_kernel(policy_check_
     wave_sync();
   }
 
-  // Right to left over the keys (lane = key), so the pair of the last lane of
-  // a tile takes the first key of the tile to its right.
+  // Right to left over blocks of 256 keys, lane l holding keys 4l .. 4l+3 of
+  // a block: the right-hand neighbour of its last key is the next lane's
+  // first, and that of lane 63's last key the first key of the block to the
+  // right.  Blocks past the query need only the bounds check.
   int bits = 0;
   bool out_of_range = false;
   float prev_p = 0.f;
   bool prev_known = false, prev_fixed = false;
   const float atol = static_cast<float>(1e-6);
-  for (int64_t t = (a.nk + 63) / 64 - 1; t >= 0; --t) {
-    const int64_t j = t * 64 + lane;
-    const int64_t ko = j < a.nk ? a.k_ord[j] : -1;
-    const bool fixed = ko >= 0;
-    float pv = 0.f;
-    if (fixed) {
-      pv = crow[ko * a.c_s2];
-      if (!(pv >= 0.f && pv <= top)) out_of_range = true;  // NaN included
+  for (int64_t t = (a.nk + 255) / 256 - 1; t >= 0; --t) {
+    const int64_t j0 = t * 256 + 4 * lane;
+    int32_t code[4];
+    if (j0 + 3 < a.nk) {
+      const int4 c4 = *reinterpret_cast<const int4*>(a.code + j0);
+      code[0] = c4.x;
+      code[1] = c4.y;
+      code[2] = c4.z;
+      code[3] = c4.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) code[i] = j0 + i < a.nk ? a.code[j0 + i] : -1;
     }
-    if (a.strict) {
-      const bool causal = j < kend;
-      bool known = causal && fixed;
-      if (causal && !fixed) {
-        const int slot = a.bnd_slot[j];
-        if (slot >= 0) {
-          pv = bctx[wave][slot];
-          known = true;
-        }
+    float pv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      pv[i] = 0.f;
+      if (code[i] >= 0) {
+        pv[i] = crow[static_cast<int64_t>(code[i]) * a.c_s2];
+        if (!(pv[i] >= 0.f && pv[i] <= top)) out_of_range = true;  // NaN included
       }
-      float right = __shfl_down(pv, 1, 64);
-      bool right_known = __shfl_down(known ? 1 : 0, 1, 64) != 0;
-      bool right_fixed = __shfl_down(fixed ? 1 : 0, 1, 64) != 0;
-      if (lane == 63) {
-        right = prev_p;
-        right_known = prev_known;
-        right_fixed = prev_fixed;
-      }
-      const bool pair = known && right_known && (fixed || right_fixed);
-      bits |= path_violations<float>(pv, known, right, pair, qp, j, j + 1, atol);
-      prev_p = __shfl(pv, 0, 64);
-      prev_known = __shfl(known ? 1 : 0, 0, 64) != 0;
-      prev_fixed = __shfl(fixed ? 1 : 0, 0, 64) != 0;
     }
+    if (!a.strict) continue;
+    if (t * 256 >= kend) {  // no causal key in the block
+      prev_known = false;
+      continue;
+    }
+    bool known[4], fixed[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      fixed[i] = code[i] >= 0;
+      known[i] = j0 + i < kend && (fixed[i] || code[i] <= -2);
+      if (known[i] && code[i] <= -2) pv[i] = bctx[wave][-2 - code[i]];  // a dynamic key beside a fixed key
+    }
+    float right = __shfl_down(pv[0], 1, 64);
+    bool right_known = __shfl_down(known[0] ? 1 : 0, 1, 64) != 0;
+    bool right_fixed = __shfl_down(fixed[0] ? 1 : 0, 1, 64) != 0;
+    if (lane == 63) {
+      right = prev_p;
+      right_known = prev_known;
+      right_fixed = prev_fixed;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float pr = i < 3 ? pv[i + 1] : right;
+      const bool kr = i < 3 ? known[i + 1] : right_known;
+      const bool fr = i < 3 ? fixed[i + 1] : right_fixed;
+      const bool pair = known[i] && kr && (fixed[i] || fr);
+      // causal keys only reach here (diff >= 0, below 2^31 for keys 0..nk-1)
+      bits |= path_violations_unit(pv[i], known[i], pr, pair, static_cast<int32_t>(qp - (j0 + i)), atol);
+    }
+    prev_p = __shfl(pv[0], 0, 64);
+    prev_known = __shfl(known[0] ? 1 : 0, 0, 64) != 0;
+    prev_fixed = __shfl(fixed[0] ? 1 : 0, 0, 64) != 0;
   }
   for (int off = 32; off > 0; off >>= 1) bits |= __shfl_xor(bits, off, 64);
   const bool any_oob = __any(out_of_range);

@@ -938,14 +938,17 @@ int prepare_prefill(const void* q, int64_t q_s_batch, int64_t q_s_tok, int64_t q
   return CS_OK;
 }
 
-// Fixed-key bitmap, the dynamic keys beside a fixed key (ascending, with a
-// per-key slot map) and the key count of a policy call: one workgroup.
+// Fixed-key bitmap, the dynamic keys beside a fixed key (ascending), the key
+// count, and for the checker one code per key: the fixed ordinal (>= 0), -2 - s
+// for the dynamic key in boundary slot s, -1 for other dynamic keys.  One
+// workgroup.
 constexpr int kPackThreads = 1024;
 constexpr int kMaxBoundary = cs::kPolicyMaxBoundary;
 
-__global__ void __launch_bounds__(kPackThreads) policy_pack_kernel(const uint8_t* fixed_keys, int64_t nk,
+__global__ void __launch_bounds__(kPackThreads) policy_pack_kernel(const uint8_t* fixed_keys,
+                                                                  const int64_t* k_ord, int64_t nk,
                                                                   uint32_t* bits, int32_t* bnd_count,
-                                                                  int32_t* bnd_keys, int32_t* bnd_slot,
+                                                                  int32_t* bnd_keys, int32_t* code,
                                                                   int32_t* nk_dev, int32_t* flags) {
   __shared__ int wave_count[kPackThreads / 64];
   __shared__ int running;
@@ -977,7 +980,8 @@ __global__ void __launch_bounds__(kPackThreads) policy_pack_kernel(const uint8_t
     before += __popcll(m & ((1ull << lane) - 1ull));
     if (j < nk) {
       const bool kept = bnd && before < kMaxBoundary;
-      bnd_slot[j] = kept ? before : -1;
+      const int64_t ko = k_ord ? k_ord[j] : -1;
+      code[j] = ko >= 0 ? static_cast<int32_t>(ko) : (kept ? -2 - before : -1);
       if (kept) bnd_keys[before] = static_cast<int32_t>(j);
       if (bnd && !kept) atomicOr(flags, CS_FLAG_POLICY_GENERIC);  // more boundary keys than the checker holds
     }
@@ -1017,7 +1021,7 @@ struct policy_ws {
   uint32_t* bits;
   int32_t* bnd_count;
   int32_t* bnd_keys;
-  int32_t* bnd_slot;
+  int32_t* code;
   float* canon_self;
   int64_t bytes;
 };
@@ -1034,7 +1038,7 @@ policy_ws carve_policy(char* base, int32_t nq, int32_t hq, int64_t nk) {
   w.bits = reinterpret_cast<uint32_t*>(take(4 * ((nk + 31) / 32)));
   w.bnd_count = reinterpret_cast<int32_t*>(take(16));
   w.bnd_keys = reinterpret_cast<int32_t*>(take(4 * kMaxBoundary));
-  w.bnd_slot = reinterpret_cast<int32_t*>(take(4 * nk));
+  w.code = reinterpret_cast<int32_t*>(take(4 * nk));
   w.canon_self = reinterpret_cast<float*>(take(4 * static_cast<int64_t>(nq) * hq));
   w.bytes = off;
   return w;
@@ -1139,8 +1143,9 @@ extern "C" int cs_ccpe_prefill_policy_bf16(const cs_ccpe_args* a, void* workspac
   if (st) return st;
   if (nq == 0) return CS_OK;
   hipStream_t s = as_stream(stream);
-  hipLaunchKernelGGL(policy_pack_kernel, dim3(1), dim3(kPackThreads), 0, s, a->fixed_keys, nk, w.bits,
-                     w.bnd_count, w.bnd_keys, w.bnd_slot, w.nk_dev, a->flags);
+  hipLaunchKernelGGL(policy_pack_kernel, dim3(1), dim3(kPackThreads), 0, s, a->fixed_keys,
+                     canon ? a->k_ord : nullptr, nk, w.bits, w.bnd_count, w.bnd_keys, w.code, w.nk_dev,
+                     a->flags);
   p.sel_rows = a->sel_rows;
   p.fixed_bits = w.bits;
   if (canon) {
@@ -1176,10 +1181,9 @@ extern "C" int cs_ccpe_prefill_policy_bf16(const cs_ccpe_args* a, void* workspac
     c.c_s1 = a->canonical.stride[1];
     c.c_s2 = a->canonical.stride[2];
     c.q_ord = a->q_ord;
-    c.k_ord = a->k_ord;
+    c.code = w.code;
     c.bnd_count = w.bnd_count;
     c.bnd_keys = w.bnd_keys;
-    c.bnd_slot = w.bnd_slot;
     c.npos = static_cast<int32_t>(ev.shape[1]);
     c.strict = a->strict;
     c.chunk_rows = a->chunk_rows;

@@ -206,14 +206,14 @@ int cs_validate_contextual_path(const cs_view* positions, const int64_t* qpos,
 
 /* SelectedAssociationPolicy.__call__ (attention.py:65-72): bool mask [nq, nk]
  * in out[0 .. nq*nk); out must have nq*nk + nq + nk bytes (the tail holds the
- * row/column membership flags). */
+ * row/column membership flags).  fixed and selected are sorted ascending. */
 int cs_selected_visibility(const int64_t* queries, int64_t nq, const int64_t* keys,
                            int64_t nk, const int64_t* fixed, int64_t nfixed,
                            const int64_t* selected, int64_t nselected, uint8_t* out,
                            void* stream);
 
 /* out[i] = values[i] is in set[0..m) (the torch.isin of
- * SelectedAssociationPolicy, attention.py:60-72). */
+ * SelectedAssociationPolicy, attention.py:60-72); set sorted ascending. */
 int cs_isin(const int64_t* values, int64_t n, const int64_t* set, int64_t m, uint8_t* out,
             void* stream);
 
