@@ -414,6 +414,7 @@ def decode_measure(device, steps: int, warmup: int):
     expected = orc.cope_attention(q[:1].float().cpu().numpy(), recs[..., :D], recs[..., D:],
                                   e.float().cpu().numpy(), np.array([CTX - 1]))
     check_err = float(np.abs(out[:1].float().cpu().numpy() - expected).max())
+    ceilings = read_ceilings(cache, table, B, HKV, BS, D, device)
     del cache
     torch.cuda.empty_cache()
     return {
@@ -425,6 +426,47 @@ def decode_measure(device, steps: int, warmup: int):
         "hbm_frac": round(gbs / PEAK_HBM_GBS, 4),
         "tok_per_s_attention_32_layers": round(B / (32 * ms * 1e-3), 1),
         "spot_check_max_abs_err": round(check_err, 5),
+        **ceilings,
+        "frac_of_pattern_read_rate": round(gbs / ceilings["read_rate_pattern_GBs"], 4),
+    }
+
+
+def read_ceilings(cache, table, B: int, HKV: int, BS: int, D: int, device) -> dict:
+    """What this device reads per second from the decode's 8.6 GB cache
+    (cs_read_probe): streamed once, and in the decode kernel's pattern -- per
+    workgroup the 64 blocks x (16 keys x 512 B) of one KV head of a 1024-key
+    split, split-major, through the same random block tables (each request's
+    2049 blocks padded to 33 x 64 by wrapping)."""
+    import torch
+
+    from cacheslide_amd import _hip
+
+    lib = _hip.load()
+    per = table.shape[1]
+    chunk = BS * 2 * D * 2                                  # one KV head's records of a block
+    splits = (per + 63) // 64
+    cols = torch.arange(splits * 64, device=device) % per
+    blocks = table.long()[:, cols].view(B, splits, 64).permute(1, 0, 2)        # [split, request, 64]
+    offsets = (blocks[:, :, None, :] * (HKV * chunk)
+               + torch.arange(HKV, device=device)[None, None, :, None] * chunk).reshape(-1).contiguous()
+    groups = offsets.numel() // 64
+    sink = torch.empty(groups * 256, dtype=torch.int32, device=device)
+    nbytes = cache.numel() * cache.element_size()
+    stream = _hip.stream_of(device)
+
+    def streamed():
+        _hip.check(lib.cs_read_probe(_hip.ptr(cache), nbytes, None, 0, 0, 0, _hip.ptr(sink), sink.numel(),
+                                     stream), "cs_read_probe")
+
+    def pattern():
+        _hip.check(lib.cs_read_probe(_hip.ptr(cache), nbytes, _hip.ptr(offsets), offsets.numel(), 64, chunk,
+                                     _hip.ptr(sink), sink.numel(), stream), "cs_read_probe")
+
+    ms_stream = time_steps(streamed, 10, 3)
+    ms_pattern = time_steps(pattern, 10, 3)
+    return {
+        "read_rate_stream_GBs": round(nbytes / (ms_stream * 1e-3) / 1e9, 1),
+        "read_rate_pattern_GBs": round(offsets.numel() * chunk / (ms_pattern * 1e-3) / 1e9, 1),
     }
 
 

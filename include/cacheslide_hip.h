@@ -548,6 +548,17 @@ int cs_copy_async(void* dst, const void* src, int64_t bytes, int32_t kind, void*
 int cs_snapshot_convert(const cs_view* src, const cs_view* dst, int32_t bit, int32_t* flags,
                         void* stream);
 
+/* ------------------------------------------------------------------------ *
+ * Measurement support (no reference counterpart): the read rate of this
+ * device for a buffer streamed once (chunks == NULL), or for chunks of
+ * chunk_bytes at the byte offsets chunks[0 .. n_chunks), per_wg chunks per
+ * 256-thread workgroup in order (an access pattern under study; a chunk
+ * outside the buffer or not 16-byte aligned is skipped).  sink: uint32 device
+ * words, one per thread (at most 16384 x 256 in streaming mode). */
+int cs_read_probe(const void* base, int64_t bytes, const int64_t* chunks, int64_t n_chunks,
+                  int32_t per_wg, int32_t chunk_bytes, uint32_t* sink, int64_t sink_words,
+                  void* stream);
+
 #ifdef __cplusplus
 }
 #endif
