@@ -55,11 +55,6 @@ constexpr float kLog2e = 1.4426950408889634f;
 // exactly (a load under a branch makes it wait for all of them).
 __device__ __attribute__((aligned(16))) uint32_t g_zero_record[kD] = {};
 
-// A key's record offset in LDS: an element offset from the cache base, or,
-// with kSideBit set, from the sidecar bases (K and V share the offset); -1
-// when the key's block or slot is invalid.
-constexpr int64_t kSideBit = int64_t(1) << 62;
-
 struct kv_addr {
   const uint16_t* cache;
   int64_t s_block, s_head, s_offset;
@@ -103,7 +98,12 @@ __device__ inline int64_t ws_index(const decode_params& p, int b, int h, int r) 
 
 template <int G>
 struct smem_t {
-  int64_t koff[kMaxSplit];  // record offset of each key of the split (paged), -1 if invalid
+  // K and V rows of each key of the split (paged), as element offsets from
+  // the cache base (sidecar rows and the zero record included, so that every
+  // row load is a global-memory load off one kernel argument); entry
+  // kMaxSplit and the entries of invalid keys hold the zero record's
+  int64_t krow[kMaxSplit + 1];
+  int64_t vrow[kMaxSplit + 1];
   union {
     float sc[G][kMaxSplit];       // exact splits: logits
     float wave_o[kWaves][G][kD];  // end of a split: per-wave accumulators
@@ -187,25 +187,38 @@ __device__ inline int64_t native_record(const kv_addr& kv, int64_t blk, int64_t 
   return blk * kv.s_block + kvh * kv.s_head + o * kv.s_offset;
 }
 
-// Resolve the record offsets of keys [lo, hi) through the block table or the
-// slot map.
+// Resolve the K and V rows of keys [lo, hi) through the block table or the
+// slot map (native slot or sidecar row), as element offsets from the cache
+// base; invalid keys read the zero record and set `bad`.
 template <int G>
 __device__ void load_offsets(const decode_params& p, smem_t<G>& s, const split_ctx& c, bool& bad) {
   const int n = static_cast<int>(c.hi - c.lo);
+  const int64_t zk = zero_record() - p.kv.cache;
+  if (threadIdx.x == 0) {
+    s.krow[kMaxSplit] = zk;
+    s.vrow[kMaxSplit] = zk + kD;
+  }
   if (p.kv.slots) {
     const int64_t* row = p.kv.slots + c.b * p.kv.slots_stride;
+    const int64_t sk = p.kv.side_k ? p.kv.side_k - p.kv.cache : 0;
+    const int64_t sv = p.kv.side_v ? p.kv.side_v - p.kv.cache : 0;
     for (int i = threadIdx.x; i < n; i += kThreads) {
       const int64_t slot = row[c.lo + i];
-      int64_t off = -1;
+      int64_t kr = zk, vr = zk + kD;
       if (slot >= 0 && slot < p.kv.native_slots) {
         const int64_t blk = p.kv.bs_shift >= 0 ? (slot >> p.kv.bs_shift) : slot / p.kv.block_size;
         const int64_t o = slot - blk * p.kv.block_size;
-        off = native_record(p.kv, blk, o, c.kvh);
+        kr = native_record(p.kv, blk, o, c.kvh);
+        vr = kr + kD;
       } else if (slot >= p.kv.native_slots && slot - p.kv.native_slots < p.kv.side_rows) {
-        off = kSideBit | ((slot - p.kv.native_slots) * p.kv.side_sr + c.kvh * p.kv.side_sh);
+        const int64_t so = (slot - p.kv.native_slots) * p.kv.side_sr + c.kvh * p.kv.side_sh;
+        kr = sk + so;
+        vr = sv + so;
+      } else {
+        bad = true;
       }
-      if (off < 0) bad = true;
-      s.koff[i] = off;
+      s.krow[i] = kr;
+      s.vrow[i] = vr;
     }
     return;
   }
@@ -213,17 +226,19 @@ __device__ void load_offsets(const decode_params& p, smem_t<G>& s, const split_c
   for (int i = threadIdx.x; i < n; i += kThreads) {
     const int64_t j = c.lo + i;
     const int64_t bi = p.kv.bs_shift >= 0 ? (j >> p.kv.bs_shift) : j / p.kv.block_size;
-    int64_t off = -1;
-    if (bi < p.kv.bt_cols) {
-      const int64_t blk = p.kv.block_table[c.b * p.kv.bt_stride + bi];
-      if (blk >= 0 && blk < p.kv.num_blocks) {
-        const int64_t o =
-            p.kv.bs_shift >= 0 ? (j & ((int64_t(1) << p.kv.bs_shift) - 1)) : j % p.kv.block_size;
-        off = native_record(p.kv, blk, o, c.kvh);
-      }
+    int64_t kr = zk, vr = zk + kD;
+    int64_t blk = -1;
+    if (bi < p.kv.bt_cols) blk = p.kv.block_table[c.b * p.kv.bt_stride + bi];
+    if (blk >= 0 && blk < p.kv.num_blocks) {
+      const int64_t o =
+          p.kv.bs_shift >= 0 ? (j & ((int64_t(1) << p.kv.bs_shift) - 1)) : j % p.kv.block_size;
+      kr = native_record(p.kv, blk, o, c.kvh);
+      vr = kr + kD;
+    } else {
+      bad = true;
     }
-    if (off < 0) bad = true;
-    s.koff[i] = off;
+    s.krow[i] = kr;
+    s.vrow[i] = vr;
   }
 }
 
@@ -233,9 +248,7 @@ template <int G, bool PAGED>
 __device__ inline const uint16_t* k_row(const decode_params& p, const smem_t<G>& s,
                                         const split_ctx& c, int64_t j, bool valid) {
   if constexpr (PAGED) {
-    const int64_t o = s.koff[valid ? j - c.lo : 0];
-    if (!valid || o < 0) return zero_record();
-    return (o & kSideBit) ? p.kv.side_k + (o ^ kSideBit) : p.kv.cache + o;
+    return p.kv.cache + s.krow[valid ? static_cast<int>(j - c.lo) : kMaxSplit];
   } else {
     return valid ? p.kv.k + c.b * p.kv.k_sb + j * p.kv.k_st + c.kvh * p.kv.k_sh : zero_record();
   }
@@ -245,9 +258,7 @@ template <int G, bool PAGED>
 __device__ inline const uint16_t* v_row(const decode_params& p, const smem_t<G>& s,
                                         const split_ctx& c, int64_t j, bool valid) {
   if constexpr (PAGED) {
-    const int64_t o = s.koff[valid ? j - c.lo : 0];
-    if (!valid || o < 0) return zero_record() + kD;
-    return (o & kSideBit) ? p.kv.side_v + (o ^ kSideBit) : p.kv.cache + o + kD;
+    return p.kv.cache + s.vrow[valid ? static_cast<int>(j - c.lo) : kMaxSplit];
   } else {
     return valid ? p.kv.v + c.b * p.kv.v_sb + j * p.kv.v_st + c.kvh * p.kv.v_sh : zero_record() + kD;
   }
@@ -495,20 +506,42 @@ __device__ void run_spec(const decode_params& p, smem_t<G>& s, const split_ctx& 
     st.tsum += static_cast<double>(tg);
     accumulate(st, x, vt);
   };
-  // tiles in pairs (a masked tile pads an odd count); the loads of the next
-  // tile are always in flight while the current one is consumed
-  ktile ka, kb;
-  vtile va, vb;
+  // Three tile buffers where registers allow (two waves per SIMD): the loads
+  // of the next two tiles are in flight while the current one is consumed;
+  // two buffers otherwise.  Loads past the wave's range read the zero record
+  // and are not consumed.
+  constexpr bool kTriple = PAGED ? G <= 8 : G <= 6;
+  ktile ka, kb, kc;
+  vtile va, vb, vc;
   load_k<G, PAGED>(ka, p, s, c, whi - kTile, wlo, lane);
   load_v<G, PAGED>(va, p, s, c, whi - kTile, wlo, lane);
-  for (int i = 0; i < ntiles; i += 2) {
-    const int64_t t0 = whi - static_cast<int64_t>(i + 1) * kTile;
-    load_k<G, PAGED>(kb, p, s, c, t0 - kTile, wlo, lane);
-    load_v<G, PAGED>(vb, p, s, c, t0 - kTile, wlo, lane);
-    tile(ka, va, t0);
-    load_k<G, PAGED>(ka, p, s, c, t0 - 2 * kTile, wlo, lane);
-    load_v<G, PAGED>(va, p, s, c, t0 - 2 * kTile, wlo, lane);
-    tile(kb, vb, t0 - kTile);
+  if constexpr (kTriple) {
+    load_k<G, PAGED>(kb, p, s, c, whi - 2 * kTile, wlo, lane);
+    load_v<G, PAGED>(vb, p, s, c, whi - 2 * kTile, wlo, lane);
+    for (int i = 0; i < ntiles; i += 3) {
+      const int64_t t0 = whi - static_cast<int64_t>(i + 1) * kTile;
+      load_k<G, PAGED>(kc, p, s, c, t0 - 2 * kTile, wlo, lane);
+      load_v<G, PAGED>(vc, p, s, c, t0 - 2 * kTile, wlo, lane);
+      tile(ka, va, t0);
+      if (i + 1 >= ntiles) break;
+      load_k<G, PAGED>(ka, p, s, c, t0 - 3 * kTile, wlo, lane);
+      load_v<G, PAGED>(va, p, s, c, t0 - 3 * kTile, wlo, lane);
+      tile(kb, vb, t0 - kTile);
+      if (i + 2 >= ntiles) break;
+      load_k<G, PAGED>(kb, p, s, c, t0 - 4 * kTile, wlo, lane);
+      load_v<G, PAGED>(vb, p, s, c, t0 - 4 * kTile, wlo, lane);
+      tile(kc, vc, t0 - 2 * kTile);
+    }
+  } else {
+    for (int i = 0; i < ntiles; i += 2) {
+      const int64_t t0 = whi - static_cast<int64_t>(i + 1) * kTile;
+      load_k<G, PAGED>(kb, p, s, c, t0 - kTile, wlo, lane);
+      load_v<G, PAGED>(vb, p, s, c, t0 - kTile, wlo, lane);
+      tile(ka, va, t0);
+      load_k<G, PAGED>(ka, p, s, c, t0 - 2 * kTile, wlo, lane);
+      load_v<G, PAGED>(va, p, s, c, t0 - 2 * kTile, wlo, lane);
+      tile(kb, vb, t0 - kTile);
+    }
   }
   __syncthreads();
   wave_finish(st, s, wave, lane);
