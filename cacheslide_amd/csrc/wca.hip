@@ -424,11 +424,11 @@ __global__ void __launch_bounds__(kSelThreads) wca_promote_kernel(
 constexpr int kOrderSlices = 16;
 
 __global__ void __launch_bounds__(64 * kOrderSlices) wca_promote_order_kernel(
-    const int64_t* scratch, int64_t n, const int64_t* count, int64_t* promoted) {
+    const int64_t* scratch, int64_t n, const int64_t* count, int64_t* promoted, int64_t done_upto) {
   __shared__ int partial[kOrderSlices][64];
   const int64_t k = *count;
   const int64_t e0 = static_cast<int64_t>(blockIdx.x) * 64;
-  if (e0 >= k) return;
+  if (e0 >= k || k <= done_upto) return;  // done_upto: promotions already ordered
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint64_t* keys = reinterpret_cast<const uint64_t*>(scratch + n);
@@ -911,7 +911,7 @@ extern "C" int cs_wca_promote(const double* key, const uint8_t* candidate, const
   const int64_t kmax = budget < n ? (budget > 0 ? budget : 0) : n;  // bound on the device count
   if (kmax > 0)
     hipLaunchKernelGGL(wca_promote_order_kernel, dim3(ceil_div(kmax, 64)), dim3(64 * kOrderSlices),
-                       0, s, scratch, n, count_out, promoted);
+                       0, s, scratch, n, count_out, promoted, int64_t(0));
   CS_LAUNCH_CHECK("wca_promote");
   return CS_OK;
 }
@@ -1067,9 +1067,10 @@ __global__ void __launch_bounds__(256) update_checks_kernel(update_checks c, int
 
 // The per-row work of a fused update (bf16 rows, contiguous [H, D] blocks):
 // one wavefront per active row i computes what the separate launches compute
-// -- the exact squared deviation and norm, the weight, the weight used, the
-// blend of K and V, and on gate layers the head cosine -- with the same
-// arithmetic in the same order, so every value and flag bit is theirs.
+// -- the finite checks of recomputed row i, the exact squared deviation and
+// norm, the weight, the weight used, the blend of K and V, and on gate layers
+// the head cosine -- with the same arithmetic in the same order, so every
+// value and flag bit is theirs.
 struct update_rows {
   const uint16_t* old_k;
   int64_t ok_s;
@@ -1097,10 +1098,14 @@ __device__ inline void update_row(const update_rows& r, int64_t i, int lane, int
   const int64_t row = r.rows[i];
   const uint4* ok = reinterpret_cast<const uint4*>(r.old_k + row * r.ok_s);
   const uint4* nk = reinterpret_cast<const uint4*>(r.new_k + i * r.nk_s);
-  // squared deviation and norm (wca_score_bf16_kernel's order), on every lane
+  // squared deviation and norm (wca_score_bf16_kernel's order), on every lane;
+  // the finite checks of the recomputed rows ride on the loads of this pass
+  // and of the V blend (the rows are exactly the recomputed tensors' rows)
   score_acc acc;
+  bool bad_nk = false, bad_nv = false;
   for (int64_t w = lane; w < r.words; w += 64) {
     const uint4 ov = ok[w], fv = nk[w];
+    bad_nk |= word_nonfinite<0>(fv);
     const uint32_t ow[4] = {ov.x, ov.y, ov.z, ov.w}, fw[4] = {fv.x, fv.y, fv.z, fv.w};
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -1141,6 +1146,7 @@ __device__ inline void update_row(const update_rows& r, int64_t i, int lane, int
     uint4* out = reinterpret_cast<uint4*>(kv ? r.fused_v + i * r.fv_s : r.fused_k + i * r.fk_s);
     for (int64_t w = lane; w < r.words; w += 64) {
       const uint4 ov = o[w], fv = nw[w];
+      if (kv) bad_nv |= word_nonfinite<0>(fv);
       uint4 res;
       res.x = blend_pair(ov.x, fv.x, wt, one_minus, bad);
       res.y = blend_pair(ov.y, fv.y, wt, one_minus, bad);
@@ -1150,6 +1156,8 @@ __device__ inline void update_row(const update_rows& r, int64_t i, int lane, int
     }
   }
   if (__any(bad)) f |= 8;
+  if (__any(bad_nk)) f |= 1 << 21;
+  if (__any(bad_nv)) f |= 1 << 23;
   if (r.gate) {
     const double c = cosine_bf16_row(r.new_k + i * r.nk_s, r.old_k + row * r.ok_s, r.H, r.D, r.eps, lane);
     if (lane == 0) r.cosine[i] = c;
@@ -1157,15 +1165,17 @@ __device__ inline void update_row(const update_rows& r, int64_t i, int lane, int
   if (lane == 0 && f) atomicOr(flags, f);
 }
 
-// Opening checks and the row pass in one launch: workgroups [0, first[5])
-// check, the rest serve four active rows each.
+// Opening checks and the row pass in one launch: the first workgroups serve
+// four active rows each (their chains of dependent loads and reductions start
+// first), the remaining first[5] workgroups stream the checks behind them.
 __global__ void __launch_bounds__(256) update_fused_kernel(update_checks c, update_rows r, int32_t* flags) {
+  const int64_t row_blocks = (r.a + 3) / 4;
   const int64_t b = blockIdx.x;
-  if (b < c.first[5]) {
-    run_checks(c, b, flags);
+  if (b >= row_blocks) {
+    run_checks(c, b - row_blocks, flags);
     return;
   }
-  const int64_t i = (b - c.first[5]) * 4 + (threadIdx.x >> 6);
+  const int64_t i = b * 4 + (threadIdx.x >> 6);
   if (i < r.a) update_row(r, i, threadIdx.x & 63, flags);
 }
 
@@ -1185,6 +1195,7 @@ struct update_final {
   int64_t n, budget;
   int64_t* scratch;
   int64_t *removed, *active, *counts;
+  int64_t* promoted;  // the small finish orders promotions of up to kRankMax tokens here
   int32_t gate, distance;
   double threshold;
   const int32_t* flags;
@@ -1213,6 +1224,228 @@ __global__ void __launch_bounds__(kSelThreads) update_finalize_kernel(update_fin
                 f.counts + 1, f.flags, f.abort_mask);
   __syncthreads();
   nonzero_block(f.selected, f.mandatory, f.n, f.active, f.counts + 2);
+}
+
+// Stores the 16 bits of a run as bytes 0 / 1 (run_mask's inverse).
+__device__ inline void store_run_mask(uint8_t* p, int64_t start, int64_t n, uint32_t m) {
+  if (start + kRun <= n && (reinterpret_cast<uintptr_t>(p + start) & 15) == 0) {
+    uint32_t w[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t x = (m >> (4 * q)) & 0xFu;
+      w[q] = (x & 1u) | ((x & 2u) << 7) | ((x & 4u) << 14) | ((x & 8u) << 21);
+    }
+    *reinterpret_cast<uint4*>(p + start) = make_uint4(w[0], w[1], w[2], w[3]);
+  } else {
+    for (int j = 0; j < kRun; ++j)
+      if (start + j < n) p[start + j] = static_cast<uint8_t>((m >> j) & 1u);
+  }
+}
+
+constexpr int kRankMax = 4096;  // promotions the small finish orders itself
+
+// update_finalize_kernel for a request of at most one chunk (n <= kChunk
+// tokens).  Thread t owns tokens [16 t, 16 t + 16) and holds their selected,
+// candidate, removed and mandatory bits in registers, loaded once at the
+// start with the flags; the gate reads the selected bits from LDS, removals
+// reach the owning thread through LDS, and the promotion's radix select runs
+// on keys held in registers.  The phases, their order and every result are
+// those of update_finalize_kernel (gate_block, commit, promote_block,
+// nonzero_block); the three masks are stored once at the end.
+__global__ void __launch_bounds__(kSelThreads) update_finalize_small_kernel(update_final f) {
+  __shared__ uint32_t sel_run[kSelThreads];
+  __shared__ uint32_t rm_run[kSelThreads];
+  __shared__ int wave_tot[kSelWaves];
+  __shared__ int hist[256];
+  __shared__ uint64_t s_prefix, s_mask;
+  __shared__ int64_t s_remaining;
+  __shared__ int s_done;
+  __shared__ uint64_t p_key[kRankMax];  // promoted tokens in index order and their key bits
+  __shared__ int32_t p_tok[kRankMax];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int64_t n = f.n, a = f.a;
+  const int64_t s = static_cast<int64_t>(tid) * kRun;
+  uint32_t sel = run_mask(f.selected, s, n);
+  uint32_t cand = run_mask(f.candidate, s, n);
+  uint32_t remm = run_mask(f.removed_mask, s, n);
+  const uint32_t mand = f.mandatory ? run_mask(f.mandatory, s, n) : 0u;
+  const bool abort = (*f.flags & f.abort_mask) != 0;
+  // commit of the next weights, first (nothing below reads alpha): the
+  // loads of a thread go out with the mask loads, the stores once the flags
+  // have arrived
+  for (int64_t i0 = 0; i0 < a; i0 += 4 * kSelThreads) {
+    int64_t r4[4];
+    double n4[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t i = i0 + u * kSelThreads + tid;
+      r4[u] = i < a ? f.rows[i] : -1;
+      n4[u] = i < a ? f.next[i] : 0.0;
+    }
+    if (!abort) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (r4[u] >= 0) f.alpha[r4[u]] = n4[u];
+    }
+  }
+  sel_run[tid] = sel;
+  rm_run[tid] = 0;
+  __syncthreads();
+
+  // gate (gate_block): the selected rows whose metric is below the threshold
+  int64_t nrem = 0;
+  if (f.gate) {
+    for (int64_t c0 = 0; c0 < a; c0 += kChunk) {
+      const int64_t s2 = c0 + s;
+      uint32_t fl = 0;
+#pragma unroll
+      for (int j = 0; j < kRun; ++j) {
+        if (s2 + j < a) {
+          const int64_t t = f.rows[s2 + j];
+          const double metric = f.distance ? 1.0 - f.cosine[s2 + j] : f.cosine[s2 + j];
+          if (((sel_run[t >> 4] >> (t & 15)) & 1u) && metric < f.threshold) fl |= 1u << j;
+        }
+      }
+      int pos;
+      const int tot = block_scan(__popc(fl), wave_tot, pos);
+      for (; fl; fl &= fl - 1) {
+        const int64_t t = f.rows[s2 + (__ffs(fl) - 1)];
+        f.removed[nrem + pos++] = t;
+        if (!abort) atomicOr(&rm_run[t >> 4], 1u << (t & 15));
+      }
+      nrem += tot;
+    }
+  }
+  if (tid == 0) f.counts[0] = nrem;
+  __syncthreads();
+  if (!abort) {
+    const uint32_t r = rm_run[tid];
+    sel &= ~r;
+    cand &= ~r;
+    remm |= r;
+  }
+
+  // promotion (promote_block, one chunk): slots = max(0, budget - #selected),
+  // available = candidate & ~selected & ~removed, the k largest keys taken
+  const uint32_t av = cand & ~sel & ~remm;
+  int ex;
+  const int total_sel = block_scan(__popc(sel), wave_tot, ex);
+  const int total_av = block_scan(__popc(av), wave_tot, ex);
+  int64_t slots = f.budget - total_sel;
+  if (slots < 0) slots = 0;
+  const int64_t k = abort ? 0 : (slots < total_av ? slots : total_av);
+  if (tid == 0) {
+    s_prefix = 0;
+    s_mask = 0;
+    s_remaining = k;
+    s_done = k == total_av;
+    f.counts[1] = k;
+  }
+  __syncthreads();
+  if (k > 0) {
+    uint64_t kb[kRun] = {};
+    if (s < n) load_key_run(f.deviation, s, n, kb);
+    for (int pass = 0; pass < 8 && !s_done; ++pass) {
+      const int shift = 56 - 8 * pass;
+      for (int i = tid; i < 256; i += kSelThreads) hist[i] = 0;
+      __syncthreads();
+      const uint64_t prefix = s_prefix, mask = s_mask;
+#pragma unroll
+      for (int j = 0; j < kRun; ++j) {
+        const bool in = ((av >> j) & 1u) && (kb[j] & mask) == prefix;
+        hist_add(hist, in ? static_cast<int>((kb[j] >> shift) & 255) : -1);
+      }
+      __syncthreads();
+      if (tid < 64) {
+        int hb[4], mine = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          hb[q] = hist[4 * lane + q];
+          mine += hb[q];
+        }
+        int above = mine;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+          const int t = __shfl_down(above, d, 64);
+          if (lane + d < 64) above += t;
+        }
+        above -= mine;
+        const int64_t need = s_remaining;
+        if (above < need && above + mine >= need) {
+          int64_t cum = above;
+          for (int q = 3; q >= 0; --q) {
+            if (cum + hb[q] >= need) {
+              const int bin = 4 * lane + q;
+              s_remaining = need - cum;
+              s_prefix = prefix | (static_cast<uint64_t>(bin) << shift);
+              s_mask = mask | (255ull << shift);
+              s_done = (need - cum) == hb[q];
+              break;
+            }
+            cum += hb[q];
+          }
+        }
+      }
+      __syncthreads();
+    }
+    const uint64_t thr = s_prefix, mask = s_mask;
+    const int64_t need_eq = s_remaining;
+    uint32_t gt = 0, eq = 0;
+#pragma unroll
+    for (int j = 0; j < kRun; ++j) {
+      const uint64_t km = kb[j] & mask;
+      if (((av >> j) & 1u) && km > thr) gt |= 1u << j;
+      if (((av >> j) & 1u) && km == thr) eq |= 1u << j;
+    }
+    int eq_rank;
+    block_scan(__popc(eq), wave_tot, eq_rank);
+    uint32_t take = gt;
+    for (uint32_t m = eq; m; m &= m - 1) {
+      if (eq_rank < need_eq) take |= m & (~m + 1);
+      ++eq_rank;
+    }
+    int pos;
+    block_scan(__popc(take), wave_tot, pos);
+    for (uint32_t m = take; m; m &= m - 1) {
+      const int j = __ffs(m) - 1;
+      f.scratch[pos] = s + j;
+      f.scratch[n + pos] = static_cast<int64_t>(kb[j]);
+      if (pos < kRankMax) {
+        p_tok[pos] = static_cast<int32_t>(s + j);
+        p_key[pos] = kb[j];
+      }
+      ++pos;
+    }
+    sel |= take;
+    // order of the promotions (wca_promote_order_kernel's rank: key
+    // descending, index ascending) when they fit the LDS lists
+    __syncthreads();
+    if (k <= kRankMax) {
+      for (int e = tid; e < k; e += kSelThreads) {
+        const uint64_t ke = p_key[e];
+        int rank = 0;
+        for (int j = 0; j < k; ++j) {
+          const uint64_t kj = p_key[j];
+          rank += (kj > ke) || (kj == ke && j < e);
+        }
+        f.promoted[rank] = p_tok[e];
+      }
+    }
+  }
+
+  // next active rows (nonzero_block): ascending tokens of selected | mandatory
+  {
+    uint32_t m = sel | mand;
+    int pos;
+    const int tot = block_scan(__popc(m), wave_tot, pos);
+    for (; m; m &= m - 1) f.active[pos++] = s + (__ffs(m) - 1);
+    if (tid == 0) f.counts[2] = tot;
+  }
+  if (s < n) {
+    store_run_mask(f.selected, s, n, sel);
+    store_run_mask(f.candidate, s, n, cand);
+    store_run_mask(f.removed_mask, s, n, remm);
+  }
 }
 
 // Fills one check segment when v is contiguous, 16-byte aligned and floating;
@@ -1276,10 +1509,18 @@ extern "C" int cs_wca_update(const cs_wca_update_args* u, void* stream) {
   } while (0)
   update_checks c{};
   int64_t blocks = 0;
-  const bool fused = check_segment(&u->cached_k, 1 << 20, c, 0, blocks) &&
-                     check_segment(&u->cached_v, 1 << 22, c, 1, blocks) &&
-                     check_segment(&u->recomputed_k, 1 << 21, c, 2, blocks) &&
-                     check_segment(&u->recomputed_v, 1 << 23, c, 3, blocks);
+  const bool rows_fused = fused_update_ok(u);
+  bool fused = check_segment(&u->cached_k, 1 << 20, c, 0, blocks) &&
+               check_segment(&u->cached_v, 1 << 22, c, 1, blocks);
+  if (fused && rows_fused) {
+    // the row pass checks the recomputed rows as it reads them (update_row)
+    const cs_view none{};
+    check_segment(&none, 1 << 21, c, 2, blocks);
+    check_segment(&none, 1 << 23, c, 3, blocks);
+  } else {
+    fused = fused && check_segment(&u->recomputed_k, 1 << 21, c, 2, blocks) &&
+            check_segment(&u->recomputed_v, 1 << 23, c, 3, blocks);
+  }
   if (fused) {
     c.first[4] = blocks;
     if (u->computed && u->a > 0) {
@@ -1290,7 +1531,7 @@ extern "C" int cs_wca_update(const cs_wca_update_args* u, void* stream) {
     }
     c.first[5] = blocks;
   }
-  if (fused && fused_update_ok(u)) {
+  if (fused && rows_fused) {
     // three launches: checks + rows, the one-workgroup finish, the promotion order
     update_rows r{};
     r.old_k = static_cast<const uint16_t*>(u->cached_k.data);
@@ -1347,11 +1588,19 @@ extern "C" int cs_wca_update(const cs_wca_update_args* u, void* stream) {
     fin.threshold = u->threshold;
     fin.flags = f;
     fin.abort_mask = u->abort_mask;
-    hipLaunchKernelGGL(update_finalize_kernel, dim3(1), dim3(kSelThreads), 0, s, fin);
+    fin.promoted = u->promoted;
+    const bool small = u->n <= kChunk;
+    if (small)
+      hipLaunchKernelGGL(update_finalize_small_kernel, dim3(1), dim3(kSelThreads), 0, s, fin);
+    else
+      hipLaunchKernelGGL(update_finalize_kernel, dim3(1), dim3(kSelThreads), 0, s, fin);
+    // promotions beyond what the small finish orders get their own launch
+    // (kmax bounds the device count)
     const int64_t kmax = u->budget < u->n ? (u->budget > 0 ? u->budget : 0) : u->n;
-    if (kmax > 0)
+    const int64_t done = small ? kRankMax : 0;
+    if (kmax > done)
       hipLaunchKernelGGL(wca_promote_order_kernel, dim3(ceil_div(kmax, 64)), dim3(64 * kOrderSlices), 0,
-                         s, u->scratch, u->n, u->counts + 1, u->promoted);
+                         s, u->scratch, u->n, u->counts + 1, u->promoted, done);
     CS_LAUNCH_CHECK("wca_update");
     return CS_OK;
   }
