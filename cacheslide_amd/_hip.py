@@ -85,6 +85,7 @@ class CsWcaUpdateArgs(ctypes.Structure):
         ("epsilon", ctypes.c_double), ("threshold", ctypes.c_double),
         ("clamp", ctypes.c_int32), ("previous_layer", ctypes.c_int32), ("gate", ctypes.c_int32),
         ("distance_mode", ctypes.c_int32), ("abort_mask", ctypes.c_int32),
+        ("clear_status", ctypes.c_int32), ("report", ctypes.c_void_p),
     ]
 
 
@@ -290,15 +291,13 @@ def view(tensor: torch.Tensor | None) -> CsView:
         return v
     if tensor.ndim > 6:
         raise ValueError("views have at most 6 dimensions")
+    nd = tensor.ndim
+    # an empty tensor keeps its shape for validation with its data absent
     v.data = tensor.data_ptr() if tensor.numel() else None
     v.dtype = dtype_code(tensor.dtype)
-    v.ndim = tensor.ndim
-    for i, (size, stride) in enumerate(zip(tensor.shape, tensor.stride())):
-        v.shape[i] = size
-        v.stride[i] = stride
-    if tensor.numel() == 0:
-        # keep shapes for validation while marking the data absent
-        v.data = None
+    v.ndim = nd
+    v.shape[:nd] = tensor.shape
+    v.stride[:nd] = tensor.stride()
     return v
 
 

@@ -1183,6 +1183,25 @@ __global__ void __launch_bounds__(256) update_fused_kernel(update_checks c, upda
 // commit (skipped when a registered check fired), the promotion's selection
 // and the next active rows -- the bodies of the separate launches, in their
 // order.
+// The status of an update for the host: the flags word and the three counts,
+// written by the thread that wrote the counts (after them, in its program
+// order), as plain stores into host-visible memory.
+__device__ inline void write_report(int64_t* report, const int32_t* flags, const int64_t* counts) {
+  report[0] = static_cast<int64_t>(static_cast<uint32_t>(*flags));
+  report[1] = counts[0];
+  report[2] = counts[1];
+  report[3] = counts[2];
+}
+
+__global__ void status_clear_kernel(int32_t* flags, int64_t* counts) {
+  if (threadIdx.x == 0) *flags = 0;
+  if (threadIdx.x < 3) counts[threadIdx.x] = 0;
+}
+
+__global__ void status_report_kernel(int64_t* report, const int32_t* flags, const int64_t* counts) {
+  if (threadIdx.x == 0) write_report(report, flags, counts);
+}
+
 struct update_final {
   double* alpha;
   const double* next;
@@ -1196,6 +1215,7 @@ struct update_final {
   int64_t* scratch;
   int64_t *removed, *active, *counts;
   int64_t* promoted;  // the small finish orders promotions of up to kRankMax tokens here
+  int64_t* report;    // NULL, or host-visible {flags word, counts[0..2]}
   int32_t gate, distance;
   double threshold;
   const int32_t* flags;
@@ -1224,6 +1244,7 @@ __global__ void __launch_bounds__(kSelThreads) update_finalize_kernel(update_fin
                 f.counts + 1, f.flags, f.abort_mask);
   __syncthreads();
   nonzero_block(f.selected, f.mandatory, f.n, f.active, f.counts + 2);
+  if (threadIdx.x == 0 && f.report) write_report(f.report, f.flags, f.counts);
 }
 
 // Stores the 16 bits of a run as bytes 0 / 1 (run_mask's inverse).
@@ -1446,6 +1467,7 @@ __global__ void __launch_bounds__(kSelThreads) update_finalize_small_kernel(upda
     store_run_mask(f.candidate, s, n, cand);
     store_run_mask(f.removed_mask, s, n, remm);
   }
+  if (tid == 0 && f.report) write_report(f.report, f.flags, f.counts);
 }
 
 // Fills one check segment when v is contiguous, 16-byte aligned and floating;
@@ -1502,6 +1524,10 @@ extern "C" int cs_wca_update(const cs_wca_update_args* u, void* stream) {
   CS_REQUIRE(u->a >= 0 && (!u->computed || u->a == 0 || u->rows), "null arguments");
   int32_t* f = u->flags;
   int st;
+  if (u->clear_status) {
+    hipLaunchKernelGGL(status_clear_kernel, dim3(1), dim3(64), 0, as_stream(stream), f, u->counts);
+    CS_LAUNCH_CHECK("wca_update status");
+  }
 #define CS_STEP(expr) \
   do {                \
     st = (expr);      \
@@ -1589,6 +1615,7 @@ extern "C" int cs_wca_update(const cs_wca_update_args* u, void* stream) {
     fin.flags = f;
     fin.abort_mask = u->abort_mask;
     fin.promoted = u->promoted;
+    fin.report = u->report;
     const bool small = u->n <= kChunk;
     if (small)
       hipLaunchKernelGGL(update_finalize_small_kernel, dim3(1), dim3(kSelThreads), 0, s, fin);
@@ -1636,5 +1663,9 @@ extern "C" int cs_wca_update(const cs_wca_update_args* u, void* stream) {
                          u->scratch, u->promoted, u->counts + 1, f, u->abort_mask, stream));
   CS_STEP(cs_mask_nonzero(u->selected, u->mandatory, u->n, u->active, u->counts + 2, stream));
 #undef CS_STEP
+  if (u->report) {
+    hipLaunchKernelGGL(status_report_kernel, dim3(1), dim3(64), 0, as_stream(stream), u->report, f, u->counts);
+    CS_LAUNCH_CHECK("wca_update report");
+  }
   return CS_OK;
 }

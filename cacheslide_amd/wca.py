@@ -106,6 +106,30 @@ def _alpha_steps(fl: _Flags) -> None:
 
 _COMPUTED_MESSAGE = "computed_indices must equal sorted active_indices"
 _BLEND_MESSAGE = "weighted K/V overflowed the cache dtype"
+_UPDATE_STEPS: dict = {}
+
+
+def _update_steps(computed: bool) -> tuple[list, int]:
+    """The one-call update's checks in the order its launches make them (the
+    reference's order of checks in WCAState.update), and their bits together
+    (the device commits nothing when one of them is set)."""
+    if computed not in _UPDATE_STEPS:
+        names = ["cached_k", "cached_v", None, "recomputed_k", "recomputed_v"]
+        steps = []
+        for name in names:
+            if name is None:
+                if computed:
+                    steps.append((64, ValueError, _COMPUTED_MESSAGE))
+                continue
+            steps.append((_NONFINITE_BIT[name], WCANumericalError, f"{name} must have finite values"))
+        steps.append((2 | 16, WCANumericalError, "adaptation weight overflowed float64"))
+        steps.append((4, WCANumericalError, "adaptation weight overflowed; inspect the K magnitudes"))
+        steps.append((8, WCANumericalError, _BLEND_MESSAGE))
+        mask = 0
+        for bits, _, _ in steps:
+            mask |= bits
+        _UPDATE_STEPS[computed] = (steps, mask)
+    return _UPDATE_STEPS[computed]
 
 
 def _matching(name: str, tensor: Tensor, reference_shape, reference: Tensor, fl: _Flags,
@@ -255,6 +279,7 @@ class WCAState:
     _work_f64: Tensor | None = field(default=None, repr=False, compare=False)
     _work_i64: Tensor | None = field(default=None, repr=False, compare=False)
     _update_args: object = field(default=None, repr=False, compare=False)
+    _status_block: object = field(default=None, repr=False, compare=False)
 
     @classmethod
     def initialize(
@@ -400,61 +425,75 @@ class WCAState:
         return all((t.shape, t.dtype, t.device) == (rows_shape, ref.dtype, ref.device)
                    for t, ref in ((recomputed_k, cached_k), (recomputed_v, cached_v)))
 
+    def _status(self, device) -> tuple:
+        """The one-call update's status: a device int64[4] block (flags word,
+        three counts) that cs_wca_update clears itself, its pinned host mirror
+        that the call's last kernel fills, and the launch stream."""
+        status = self._status_block
+        if status is None or status[0].device != device:
+            block = torch.zeros(4, dtype=torch.int64, device=device)
+            host = torch.zeros(4, dtype=torch.int64, pin_memory=True)
+            status = self._status_block = (block, host, _hip.stream_of(device),
+                                           torch.cuda.current_stream(device))
+        return status
+
     def _update_device(self, layer_index, device, cached_k, cached_v, recomputed_k, recomputed_v,
                        computed_indices) -> WCAUpdate:
         """The launches of _update_checked in one cs_wca_update call, with its checks registered."""
         indices = self.active_indices
         a, n = indices.numel(), self.selected_mask.numel()
-        fl = _Flags(device, 3)
+        block, host, stream, torch_stream = self._status(device)
         work, scratch = self._workspace()
-        rows_shape = (a, *cached_k.shape[1:])
-        used = torch.empty(a, dtype=torch.float64, device=device)
-        fused_k = torch.empty(rows_shape, dtype=cached_k.dtype, device=device)
-        fused_v = torch.empty(rows_shape, dtype=cached_v.dtype, device=device)
         gate = layer_index % self.config.gate_interval == 0 and a > 0
-        removed_buf = torch.empty(a, dtype=torch.long, device=device) if gate else None
-        promoted_buf = torch.empty(max(n, 1), dtype=torch.long, device=device)
-        active_buf = torch.empty(max(n, 1), dtype=torch.long, device=device)
+        # fresh outputs in two allocations: fused K and V; the index lists and the weights used
+        m = max(n, 1)
+        fused = torch.empty((2, a, *cached_k.shape[1:]), dtype=cached_k.dtype, device=device)
+        fused_k, fused_v = fused[0], fused[1]
+        ibuf = torch.empty(2 * m + 2 * a, dtype=torch.long, device=device)
+        promoted_buf, active_buf = ibuf[:m], ibuf[m:2 * m]
+        removed_buf = ibuf[2 * m:2 * m + a] if gate else None
+        used = ibuf[2 * m + a:].view(torch.float64)
         computed = computed_indices.contiguous() if computed_indices is not None else None
-        # the checks in the order the launches make them (the reference's order)
-        _finite_step("cached_k", fl)
-        _finite_step("cached_v", fl)
-        if computed is not None:
-            fl.step(64, ValueError, _COMPUTED_MESSAGE)
-        _finite_step("recomputed_k", fl)
-        _finite_step("recomputed_v", fl)
-        _alpha_steps(fl)
-        fl.step(8, WCANumericalError, _BLEND_MESSAGE)
+        steps, abort_mask = _update_steps(computed is not None)
         u = self._update_args
         if u is None:
             u = self._update_args = _hip.CsWcaUpdateArgs()
+            u.clear_status = 1
+        u.budget = self.budget
+        u.alpha, u.deviation = _raw(self.alpha), _raw(self.initial_deviation)
+        u.selected, u.candidate = _raw(self.selected_mask), _raw(self.candidate_mask)
+        u.removed_mask, u.mandatory = _raw(self.removed_mask), _raw(self.mandatory_mask)
+        config = self.config
+        u.epsilon, u.threshold = float(config.epsilon), float(config.convergence_threshold)
+        u.clamp = 1 if config.clamp_alpha else 0
+        u.previous_layer = 1 if config.weight_update == "previous_layer" else 0
+        u.distance_mode = 1 if config.convergence_mode == "distance_lt" else 0
         u.cached_k, u.cached_v = _hip.view(cached_k), _hip.view(cached_v)
         u.recomputed_k, u.recomputed_v = _hip.view(recomputed_k), _hip.view(recomputed_v)
         u.fused_k, u.fused_v = _hip.view(fused_k), _hip.view(fused_v)
         u.rows, u.computed = _raw(indices), _raw(computed)
-        u.a, u.n, u.budget = a, n, self.budget
-        u.alpha, u.deviation = _raw(self.alpha), _raw(self.initial_deviation)
-        u.selected, u.candidate = _raw(self.selected_mask), _raw(self.candidate_mask)
-        u.removed_mask, u.mandatory = _raw(self.removed_mask), _raw(self.mandatory_mask)
+        u.a, u.n = a, n
         base = work.data_ptr()
         u.err, u.norm, u.next_alpha, u.cosine = base, base + 8 * n, base + 16 * n, base + 24 * n
         u.used, u.removed = _raw(used), _raw(removed_buf)
         u.promoted, u.scratch, u.active = _raw(promoted_buf), _raw(scratch), _raw(active_buf)
-        u.flags, u.counts = fl.block.data_ptr(), fl.block.data_ptr() + 8
-        u.epsilon, u.threshold = float(self.config.epsilon), float(self.config.convergence_threshold)
-        u.clamp = 1 if self.config.clamp_alpha else 0
-        u.previous_layer = 1 if self.config.weight_update == "previous_layer" else 0
+        u.flags, u.counts = block.data_ptr(), block.data_ptr() + 8
+        u.report = host.data_ptr()
         u.gate = 1 if gate else 0
-        u.distance_mode = 1 if self.config.convergence_mode == "distance_lt" else 0
-        u.abort_mask = fl.abort_mask
-        call("cs_wca_update", ctypes.byref(u), fl.stream)
-        fl.finish(read=True)
-        return self._finish_update(layer_index, fl, indices, fused_k, fused_v, used, gate, removed_buf,
-                                   promoted_buf, active_buf)
+        u.abort_mask = abort_mask
+        call("cs_wca_update", ctypes.byref(u), stream)
+        torch_stream.synchronize()
+        words = host.tolist()
+        value = words[0] & 0xFFFFFFFF
+        for bits, exc, message in steps:
+            if value & bits:
+                raise exc(message)
+        return self._finish_update(layer_index, words[1:], indices, fused_k, fused_v, used, gate,
+                                   removed_buf, promoted_buf, active_buf)
 
-    def _finish_update(self, layer_index, fl, indices, fused_k, fused_v, used, gate, removed_buf,
+    def _finish_update(self, layer_index, counts, indices, fused_k, fused_v, used, gate, removed_buf,
                        promoted_buf, active_buf) -> WCAUpdate:
-        n_removed, n_promoted, n_active = fl.counts
+        n_removed, n_promoted, n_active = counts
         removed = removed_buf[:n_removed] if gate else indices[:0]
         promoted = promoted_buf[:n_promoted]
         next_indices = self._cache_active(active_buf, n_active)
@@ -539,5 +578,5 @@ class WCAState:
         call("cs_mask_nonzero", ptr(self.selected_mask), ptr(self.mandatory_mask), n, ptr(active_buf),
              fl.counter(2), fl.stream)
         fl.finish(read=True)
-        return self._finish_update(layer_index, fl, indices, fused_k, fused_v, used, gate, removed_buf,
-                                   promoted_buf, active_buf)
+        return self._finish_update(layer_index, fl.counts, indices, fused_k, fused_v, used, gate,
+                                   removed_buf, promoted_buf, active_buf)

@@ -487,6 +487,10 @@ typedef struct cs_wca_update_args {
   int64_t* counts;          /* [3] */
   double epsilon, threshold;
   int32_t clamp, previous_layer, gate, distance_mode, abort_mask;
+  int32_t clear_status;     /* nonzero: the call zeroes flags and counts[3] first */
+  int64_t* report;          /* NULL, or host-visible int64[4] that receives the flags
+                               word and counts[0..2] from the call's last kernel
+                               (read it after synchronizing the stream) */
 } cs_wca_update_args;
 
 int cs_wca_update(const cs_wca_update_args* u, void* stream);

@@ -81,7 +81,7 @@ def test_wca_update_checks_arguments_without_a_device():
     assert b"null" in lib.cs_last_error()
     args = _hip.CsWcaUpdateArgs()          # no status block
     assert lib.cs_wca_update(ctypes.byref(args), None) == _hip.CS_EINVAL
-    assert ctypes.sizeof(_hip.CsWcaUpdateArgs) == 888   # the C struct's size on x86-64
+    assert ctypes.sizeof(_hip.CsWcaUpdateArgs) == 896   # the C struct's size on x86-64
 
 
 def test_decode_refuses_a_small_workspace_without_a_device():
