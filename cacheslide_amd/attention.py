@@ -43,30 +43,43 @@ def _fixed_positions(fixed: tuple[int, ...]) -> Tensor:
     return tensor
 
 
+def _policy_tables(policy: "CanonicalPositionPolicy", device) -> tuple:
+    """Position -> profile row and position -> fixed ordinal tables on the
+    device (-1 where the position is not fixed; a fixed ordinal the profile
+    never traced maps to -2, a repeated one to its last row), with the
+    untraced flag, the profile's row count, the fixed count and the reason
+    profile.lookup would refuse the plan (None when it accepts it)."""
+    fixed = _fixed_positions(policy.plan.fixed_indices)
+    count = fixed.numel()
+    profile = policy.profile
+    traced = profile.query_positions.detach().to("cpu", torch.long).reshape(-1)
+    size = int(fixed.max()) + 1 if count else 1
+    rows_of = torch.full((count,), -2, dtype=torch.long)
+    inside = (traced >= 0) & (traced < count)
+    if count and bool(inside.any()):
+        rows_of.scatter_reduce_(0, traced[inside], torch.arange(traced.numel())[inside], reduce="amax",
+                                include_self=False)
+    q_table = torch.full((size,), -1, dtype=torch.long)
+    k_table = torch.full((size,), -1, dtype=torch.long)
+    if count:
+        q_table[fixed] = rows_of
+        k_table[fixed] = torch.arange(count)
+    chunks = tuple(ChunkIdentity(*entry) for entry in policy.plan.fixed_layout)
+    reason = profile.lookup_reason(chunks, None, None, policy.checkpoint_id, profile.trained_profile_version)
+    return (q_table.to(device), k_table.to(device), size, bool((rows_of == -2).any()),
+            int(torch.unique(traced).numel()), count, reason)
+
+
 class _LoweredCanonical:
     """Kernel inputs for one CanonicalPositionPolicy over one call's coordinates."""
 
     def __init__(self, policy: "CanonicalPositionPolicy", device, query_positions, key_positions):
-        fixed = _fixed_positions(policy.plan.fixed_indices)
-        count = fixed.numel()
-        profile = policy.profile
-        traced = profile.query_positions.detach().to("cpu", torch.long).reshape(-1)
-        size = int(fixed.max()) + 1 if count else 1
-        # profile row of each fixed ordinal, -2 when untraced (for a repeated
-        # ordinal, its last row)
-        rows_of = torch.full((count,), -2, dtype=torch.long)
-        inside = (traced >= 0) & (traced < count)
-        if count and bool(inside.any()):
-            rows_of.scatter_reduce_(0, traced[inside], torch.arange(traced.numel())[inside], reduce="amax",
-                                    include_self=False)
-        self.unknown = bool((rows_of == -2).any())
-        q_table = torch.full((size,), -1, dtype=torch.long)
-        k_table = torch.full((size,), -1, dtype=torch.long)
-        if count:
-            q_table[fixed] = rows_of
-            k_table[fixed] = torch.arange(count)
-        q_dev = q_table.to(device)
-        k_dev = k_table.to(device)
+        # the call-independent part (position -> profile row / fixed ordinal
+        # tables, the profile lookup's verdict) once per policy and device
+        tables = policy._device_cache.get(("tables", str(device)))
+        if tables is None:
+            tables = policy._device_cache[("tables", str(device))] = _policy_tables(policy, device)
+        q_dev, k_dev, size, self.unknown, self.profile_rows, self.fixed_count, self.reason = tables
         self.q_rows = torch.empty(query_positions.shape[0], dtype=torch.long, device=device)
         self.k_ord = torch.empty(key_positions.shape[0], dtype=torch.long, device=device)
         stream = _hip.stream_of(device)
@@ -76,12 +89,6 @@ class _LoweredCanonical:
              key_positions.shape[0], stream)
         self._tables = (q_dev, k_dev)
         self.canonical = policy._canonical_on(device)
-        self.profile_rows = int(torch.unique(traced).numel())
-        self.fixed_count = count
-        chunks = tuple(ChunkIdentity(*entry) for entry in policy.plan.fixed_layout)
-        self.reason = profile.lookup_reason(
-            chunks, None, None, policy.checkpoint_id, profile.trained_profile_version
-        )
 
     def fits(self, heads: int) -> bool:
         """The canonical tensor covers every (head, profile row, fixed ordinal) the kernel reads."""
@@ -187,7 +194,10 @@ class SelectedAssociationPolicy:
     def _sets(self, device) -> tuple[Tensor, Tensor]:
         """Fixed and selected positions on the device, each sorted ascending
         (the kernels test membership by binary search)."""
-        fixed = _fixed_positions(tuple(self.fixed_indices)).to(device)
+        fixed_indices = self.fixed_indices
+        if not isinstance(fixed_indices, tuple):
+            fixed_indices = tuple(fixed_indices)
+        fixed = _fixed_positions(fixed_indices).to(device)
         fixed = torch.sort(fixed).values
         selected = self.selected_indices.to(device=device, dtype=torch.long).reshape(-1)
         return fixed, torch.sort(selected).values

@@ -116,21 +116,35 @@ class RequestPlan:
     def _tokens_of(self, role: str) -> list[int]:
         return [t for chunk in self.chunks if chunk.role == role for t in range(chunk.start, chunk.end)]
 
+    def _memo(self, name: str, compute):
+        """Derived values of this immutable plan, computed once: the runtime
+        asks for them on every layer, and the attention policies key their
+        device caches on the returned objects."""
+        memo = self.__dict__.get("_derived")
+        if memo is None:
+            memo = {}
+            object.__setattr__(self, "_derived", memo)
+        if name not in memo:
+            memo[name] = compute()
+        return memo[name]
+
     @property
     def fixed_indices(self) -> tuple[int, ...]:
         """Token indices of the reused chunks, ascending."""
-        return tuple(self._tokens_of("reuse"))
+        return self._memo("fixed_indices", lambda: tuple(self._tokens_of("reuse")))
 
     @property
     def mandatory_indices(self) -> tuple[int, ...]:
         """Recomputed tokens plus the last prompt token, ascending."""
-        return tuple(sorted(set(self._tokens_of("recompute")) | {len(self.token_ids) - 1}))
+        return self._memo("mandatory_indices", lambda: tuple(
+            sorted(set(self._tokens_of("recompute")) | {len(self.token_ids) - 1})))
 
     @property
     def fixed_layout(self) -> tuple[tuple[str, str, int], ...]:
         """(chunk id, digest of its token ids, length) of each reused chunk, in order."""
-        return tuple((c.chunk_id, digest(self.token_ids[c.start:c.end]), c.length)
-                     for c in self.chunks if c.role == "reuse")
+        return self._memo("fixed_layout", lambda: tuple(
+            (c.chunk_id, digest(self.token_ids[c.start:c.end]), c.length)
+            for c in self.chunks if c.role == "reuse"))
 
     def cache_key(self, model_identity: str, layer: int) -> str:
         """KV identity: model, namespace, task, the whole ordered fixed layout

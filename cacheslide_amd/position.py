@@ -47,8 +47,11 @@ class _Checks:
     def device_step(self, bits: int, exc: type, message: str) -> None:
         self.steps.append((bits, exc, message))
 
-    def finish(self, pending: BaseException | None = None) -> None:
-        value = _hip.read_flags(self.flags)[0] if self.steps else 0
+    def finish(self, pending: BaseException | None = None, value: int | None = None) -> None:
+        """Raise the first registered device check that fired, then ``pending``;
+        ``value``: the flags word already read after the last launch."""
+        if value is None:
+            value = _hip.read_flags(self.flags)[0] if self.steps else 0
         for bits, exc, message in self.steps:
             if value & bits:
                 raise exc(message)
@@ -622,17 +625,29 @@ def cope_attention(
         keep += [sel_rows, fixed_keys]
         args.sel_rows = ptr(sel_rows)
         args.fixed_keys = ptr(fixed_keys)
-    if not (selected is not None and default_keys
+    # The MFMA reuse-call path; the flags word it leaves is read once here and
+    # serves every check below (one wait for the device per call).
+    flags_value = None
+    if (selected is not None and default_keys
             and _policy_fast_ok(query, key, value, e, cope, amask, visibility_mask, fixed_positions,
                                 return_positions, lowered if canonical is not None else None)
-            and _policy_prefill(args, query, key, chunk_flags, ck)):
+            and _policy_prefill(args, query, key, ck)):
+        flags_value = _hip.read_flags(ck.flags)[0]
+        if flags_value & _hip.FLAG_POLICY_GENERIC:
+            # a fixed query row that is not selected: the generic kernel runs the call
+            ck.flags.bitwise_and_(~_hip.FLAG_POLICY_GENERIC)
+            if chunk_flags is not None:
+                chunk_flags.zero_()
+            flags_value = None
+            call("cs_ccpe_attention", args, ck.stream)
+    else:
         call("cs_ccpe_attention", args, ck.stream)
     ck.device_step(_hip.FLAG_LOGIT_NONFINITE, ValueError, "attention logits overflowed the accumulation dtype")
     ck.device_step(_hip.FLAG_POS_INVALID, ValueError, "positions must be bounded query-dependent [head,query,key]")
     ck.device_step(_hip.FLAG_SCORE_NONFINITE, ValueError, "contextual attention logits are not finite")
     if chunk_flags is not None:
-        _raise_policy_errors(ck, chunk_flags, lowered)
-    ck.finish()
+        _raise_policy_errors(ck, chunk_flags, lowered, flags_value)
+    ck.finish(value=flags_value)
     if return_positions:
         return output, trace
     return output
@@ -642,13 +657,13 @@ _TRANSFORM_BOUNDS_MESSAGE = ("positions_transform must return bounded finite pos
                              "with the contextual shape, dtype and device")
 
 
-def _raise_policy_errors(ck: _Checks, chunk_flags: Tensor, lowered) -> None:
+def _raise_policy_errors(ck: _Checks, chunk_flags: Tensor, lowered, flags_value: int | None = None) -> None:
     """In chunk order, the first chunk holding a fixed query row that fails:
     profile lookup, then the strict path checks, then the bounds of the
     substituted positions (position.py:485-516 with attention.py:32-57)."""
     from .attention import CHUNK_CANON_OUT_OF_RANGE, CHUNK_HAS_FIXED_ROW
 
-    ck.finish()
+    ck.finish(value=flags_value)
     values = _hip.read_flags(chunk_flags)
     for value in values:
         if not value & CHUNK_HAS_FIXED_ROW:
@@ -671,10 +686,10 @@ def _policy_fast_ok(query, key, value, e, cope, amask, visibility_mask, fixed_po
     return lowered is None or lowered.canonical.dtype == torch.float32
 
 
-def _policy_prefill(args, query: Tensor, key: Tensor, chunk_flags: Tensor | None, ck: _Checks) -> bool:
-    """cs_ccpe_prefill_policy_bf16 into args.out; False when the call needs the
-    generic kernel (an unsupported layout, or a fixed query row that is not
-    selected: its flag is cleared and the chunk flags reset for that run)."""
+def _policy_prefill(args, query: Tensor, key: Tensor, ck: _Checks) -> bool:
+    """Launch cs_ccpe_prefill_policy_bf16 into args.out; False (nothing
+    launched) for a layout it does not take.  A fixed query row that is not
+    selected sets FLAG_POLICY_GENERIC: the caller then runs the generic kernel."""
     device = ck.device
     lib = _hip.load()
     nq, hq, nk = query.shape[0], query.shape[1], key.shape[0]
@@ -690,12 +705,7 @@ def _policy_prefill(args, query: Tensor, key: Tensor, chunk_flags: Tensor | None
     if status == _hip.CS_EUNSUPPORTED:
         return False
     _hip.check(status, "cs_ccpe_prefill_policy_bf16")
-    if not _hip.read_flags(ck.flags)[0] & _hip.FLAG_POLICY_GENERIC:
-        return True
-    ck.flags.bitwise_and_(~_hip.FLAG_POLICY_GENERIC)
-    if chunk_flags is not None:
-        chunk_flags.zero_()
-    return False
+    return True
 
 
 def _fast_path_ok(query, key, value, e, cope, amask, visibility_mask, fixed_positions, canonical,
