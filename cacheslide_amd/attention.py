@@ -43,6 +43,19 @@ def _fixed_positions(fixed: tuple[int, ...]) -> Tensor:
     return tensor
 
 
+def _memo_of(profile, fallback: dict) -> dict:
+    """A memo dict kept on the profile object (immutable calibration data),
+    or ``fallback`` for a profile that takes no attributes."""
+    memo = getattr(profile, "__dict__", {}).get("_lowering_memo")
+    if memo is None:
+        memo = {}
+        try:
+            object.__setattr__(profile, "_lowering_memo", memo)
+        except (AttributeError, TypeError):
+            return fallback
+    return memo
+
+
 def _policy_tables(policy: "CanonicalPositionPolicy", device) -> tuple:
     """Position -> profile row and position -> fixed ordinal tables on the
     device (-1 where the position is not fixed; a fixed ordinal the profile
@@ -75,11 +88,16 @@ class _LoweredCanonical:
 
     def __init__(self, policy: "CanonicalPositionPolicy", device, query_positions, key_positions):
         # the call-independent part (position -> profile row / fixed ordinal
-        # tables, the profile lookup's verdict) once per policy and device
-        tables = policy._device_cache.get(("tables", str(device)))
-        if tables is None:
-            tables = policy._device_cache[("tables", str(device))] = _policy_tables(policy, device)
-        q_dev, k_dev, size, self.unknown, self.profile_rows, self.fixed_count, self.reason = tables
+        # tables, the profile lookup's verdict) once per profile, plan and
+        # device: the runtime builds a new policy per call around the same
+        # profile and plan
+        fixed = policy.plan.fixed_indices
+        cache = _memo_of(policy.profile, policy._device_cache)
+        key = ("tables", id(fixed), policy.checkpoint_id, str(device))
+        hit = cache.get(key)
+        if hit is None or hit[0] is not fixed:
+            hit = cache[key] = (fixed, _policy_tables(policy, device))
+        q_dev, k_dev, size, self.unknown, self.profile_rows, self.fixed_count, self.reason = hit[1]
         self.q_rows = torch.empty(query_positions.shape[0], dtype=torch.long, device=device)
         self.k_ord = torch.empty(key_positions.shape[0], dtype=torch.long, device=device)
         stream = _hip.stream_of(device)
@@ -140,10 +158,11 @@ class CanonicalPositionPolicy:
             raise ValueError("unknown CCPE position policy")
 
     def _canonical_on(self, device) -> Tensor:
-        key = str(device)
-        if key not in self._device_cache:
-            self._device_cache[key] = self.profile.canonical_positions.to(device)
-        return self._device_cache[key]
+        cache = _memo_of(self.profile, self._device_cache)
+        key = ("canonical", str(device))
+        if key not in cache:
+            cache[key] = self.profile.canonical_positions.to(device)
+        return cache[key]
 
     def _lower(self, device, query_positions: Tensor, key_positions: Tensor) -> _LoweredCanonical:
         return _LoweredCanonical(self, device, query_positions, key_positions)
