@@ -88,16 +88,21 @@ __global__ void __launch_bounds__(64 * kWaves) policy_check_kernel(policy_check_
   // Right to left over blocks of 256 keys, lane l holding keys 4l .. 4l+3 of
   // a block: the right-hand neighbour of its last key is the next lane's
   // first, and that of lane 63's last key the first key of the block to the
-  // right.  Blocks past the query need only the bounds check.
+  // right.  Blocks past the query need only the bounds check.  Blocks go in
+  // groups of kGroup, all of a group's canonical cells loaded together, the
+  // codes of the next group in flight while a group is checked.
+  constexpr int kGroup = 4;
   int bits = 0;
   bool out_of_range = false;
   float prev_p = 0.f;
   bool prev_known = false, prev_fixed = false;
   const float atol = static_cast<float>(1e-6);
-  for (int64_t t = (a.nk + 255) / 256 - 1; t >= 0; --t) {
+  auto load_codes = [&](int64_t t, int32_t* code) {
     const int64_t j0 = t * 256 + 4 * lane;
-    int32_t code[4];
-    if (j0 + 3 < a.nk) {
+    if (t < 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) code[i] = -1;
+    } else if (j0 + 3 < a.nk) {
       const int4 c4 = *reinterpret_cast<const int4*>(a.code + j0);
       code[0] = c4.x;
       code[1] = c4.y;
@@ -107,19 +112,19 @@ __global__ void __launch_bounds__(64 * kWaves) policy_check_kernel(policy_check_
 #pragma unroll
       for (int i = 0; i < 4; ++i) code[i] = j0 + i < a.nk ? a.code[j0 + i] : -1;
     }
+  };
+  auto check_block = [&](int64_t t, const int32_t* code, const float* pcell) {
+    const int64_t j0 = t * 256 + 4 * lane;
     float pv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      pv[i] = 0.f;
-      if (code[i] >= 0) {
-        pv[i] = crow[static_cast<int64_t>(code[i]) * a.c_s2];
-        if (!(pv[i] >= 0.f && pv[i] <= top)) out_of_range = true;  // NaN included
-      }
+      pv[i] = pcell[i];
+      if (code[i] >= 0 && !(pv[i] >= 0.f && pv[i] <= top)) out_of_range = true;  // NaN included
     }
-    if (!a.strict) continue;
+    if (!a.strict) return;
     if (t * 256 >= kend) {  // no causal key in the block
       prev_known = false;
-      continue;
+      return;
     }
     bool known[4], fixed[4];
 #pragma unroll
@@ -148,6 +153,28 @@ __global__ void __launch_bounds__(64 * kWaves) policy_check_kernel(policy_check_
     prev_p = __shfl(pv[0], 0, 64);
     prev_known = __shfl(known[0] ? 1 : 0, 0, 64) != 0;
     prev_fixed = __shfl(fixed[0] ? 1 : 0, 0, 64) != 0;
+  };
+  const int64_t last = (a.nk + 255) / 256 - 1;
+  int32_t codes[kGroup][4];
+#pragma unroll
+  for (int g = 0; g < kGroup; ++g) load_codes(last - g, codes[g]);
+  for (int64_t t0 = last; t0 >= 0; t0 -= kGroup) {
+    float cells[kGroup][4];
+#pragma unroll
+    for (int g = 0; g < kGroup; ++g)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        cells[g][i] = codes[g][i] >= 0 ? crow[static_cast<int64_t>(codes[g][i]) * a.c_s2] : 0.f;
+    int32_t next[kGroup][4];
+#pragma unroll
+    for (int g = 0; g < kGroup; ++g) load_codes(t0 - kGroup - g, next[g]);
+#pragma unroll
+    for (int g = 0; g < kGroup; ++g)
+      if (t0 - g >= 0) check_block(t0 - g, codes[g], cells[g]);
+#pragma unroll
+    for (int g = 0; g < kGroup; ++g)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) codes[g][i] = next[g][i];
   }
   for (int off = 32; off > 0; off >>= 1) bits |= __shfl_xor(bits, off, 64);
   const bool any_oob = __any(out_of_range);
