@@ -198,12 +198,13 @@ struct stage_t {
   uint4 v[kStageSlots];
 };
 
-// WAVES wavefronts of 32 columns each; two wavefronts per SIMD.  POLICY (dense
+// WAVES wavefronts of 32 columns each (2, 4 or 8); registers for two
+// wavefronts per SIMD.  POLICY (dense
 // K/V only): SelectedAssociationPolicy visibility and the canonical position
 // of each selected fixed row's own key, for calls in which every fixed query
 // row is selected (its only visible fixed key is then itself).
 template <int MODE, int WAVES, bool POLICY = false>
-__global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(prefill_params p) {
+__global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2))) ccpe_prefill_kernel(prefill_params p) {
   constexpr bool PAGED = MODE != 0;
   constexpr bool SLOTS = MODE == 2;
   constexpr int kThreads = 64 * WAVES;
@@ -796,6 +797,18 @@ __global__ void __launch_bounds__(64 * WAVES, 8 / WAVES) ccpe_prefill_kernel(pre
 using namespace cs;
 
 namespace {
+// Compute units of the current device (cached per device).
+int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int v = 0;
+    cus[dev] = hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0 ? v : 256;
+  }
+  return cus[dev];
+}
+
 int fill_kv(const cs_kv_source* kv, cs::kv_addr* a) {
   CS_REQUIRE(kv != nullptr, "null kv source");
   cs::kv_addr r{};
@@ -915,7 +928,12 @@ int prepare_prefill(const void* q, int64_t q_s_batch, int64_t q_s_tok, int64_t q
   int tab_stride = (max_positions + 1) / 2 * 2 + 2;
   if ((tab_stride / 2) % 2 == 0) tab_stride += 2;
   const size_t tab4 = 2 * 4 * kCols * static_cast<size_t>(tab_stride);
-  const int waves = 2 * (tab4 + kStaticLds) <= kLdsLimit ? 4 : 8;
+  int waves = 2 * (tab4 + kStaticLds) <= kLdsLimit ? 4 : 8;
+  // A launch of fewer 4-wave workgroups than two per CU (a selective call's
+  // few hundred rows) runs 2-wave workgroups: twice as many workgroups share
+  // the longest key walks.
+  if (waves == 4 && static_cast<int64_t>(batch) * hkv * ceil_div(nq, kCols * 4 / group) < 2 * device_cus())
+    waves = 2;
   p.rows_per_wg = kCols * waves / group;
   p.row_blocks = static_cast<int32_t>(ceil_div(nq, p.rows_per_wg));
   p.nk = nk;
@@ -1064,14 +1082,20 @@ extern "C" int cs_ccpe_prefill_bf16(const void* q, int64_t q_s_batch, int64_t q_
   const int mode = p.kv.slots ? 2 : (p.kv.block_table ? 1 : 0);
   if (mode == 2 && waves == 8)
     hipLaunchKernelGGL((ccpe_prefill_kernel<2, 8>), grid, block, smem, s, p);
+  else if (mode == 2 && waves == 2)
+    hipLaunchKernelGGL((ccpe_prefill_kernel<2, 2>), grid, block, smem, s, p);
   else if (mode == 2)
     hipLaunchKernelGGL((ccpe_prefill_kernel<2, 4>), grid, block, smem, s, p);
   else if (mode == 1 && waves == 8)
     hipLaunchKernelGGL((ccpe_prefill_kernel<1, 8>), grid, block, smem, s, p);
+  else if (mode == 1 && waves == 2)
+    hipLaunchKernelGGL((ccpe_prefill_kernel<1, 2>), grid, block, smem, s, p);
   else if (mode == 1)
     hipLaunchKernelGGL((ccpe_prefill_kernel<1, 4>), grid, block, smem, s, p);
   else if (waves == 8)
     hipLaunchKernelGGL((ccpe_prefill_kernel<0, 8>), grid, block, smem, s, p);
+  else if (waves == 2)
+    hipLaunchKernelGGL((ccpe_prefill_kernel<0, 2>), grid, block, smem, s, p);
   else
     hipLaunchKernelGGL((ccpe_prefill_kernel<0, 4>), grid, block, smem, s, p);
   CS_LAUNCH_CHECK("ccpe_prefill");
@@ -1160,6 +1184,8 @@ extern "C" int cs_ccpe_prefill_policy_bf16(const cs_ccpe_args* a, void* workspac
   const dim3 grid(p.total_wg), block(64 * waves);
   if (waves == 8)
     hipLaunchKernelGGL((ccpe_prefill_kernel<0, 8, true>), grid, block, smem, s, p);
+  else if (waves == 2)
+    hipLaunchKernelGGL((ccpe_prefill_kernel<0, 2, true>), grid, block, smem, s, p);
   else
     hipLaunchKernelGGL((ccpe_prefill_kernel<0, 4, true>), grid, block, smem, s, p);
   CS_LAUNCH_CHECK("ccpe_prefill_policy");
