@@ -99,6 +99,7 @@ struct policy_check_args {
   int64_t c_s0, c_s1, c_s2;
   const int64_t* q_ord;
   const int32_t* code;       // per key: fixed ordinal (>= 0), -2 - s (boundary slot s), -1
+  const int32_t* blk;        // per block of 256 keys: offset o (code = key - o), -1 (all -1), -2 (read code)
   const int32_t* bnd_count;  // dynamic keys beside a fixed key: count
   const int32_t* bnd_keys;   // and the keys, ascending
   int32_t npos, strict, chunk_rows;

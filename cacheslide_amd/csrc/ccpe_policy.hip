@@ -90,7 +90,11 @@ __global__ void __launch_bounds__(64 * kWaves) policy_check_kernel(policy_check_
   // first, and that of lane 63's last key the first key of the block to the
   // right.  Blocks past the query need only the bounds check.  Blocks go in
   // groups of kGroup, all of a group's canonical cells loaded together, the
-  // codes of the next group in flight while a group is checked.
+  // codes of the next group in flight while a group is checked.  A block
+  // whose keys are all fixed with consecutive ordinals (descriptor o >= 0:
+  // code = key - o) computes its codes and, on a contiguous profile row,
+  // reads each lane's 4 cells as one 16-byte load; a block of plain dynamic
+  // keys (-1) reads nothing; only the other blocks (-2) read their codes.
   constexpr int kGroup = 4;
   int bits = 0;
   bool out_of_range = false;
@@ -154,27 +158,56 @@ __global__ void __launch_bounds__(64 * kWaves) policy_check_kernel(policy_check_
     prev_known = __shfl(known[0] ? 1 : 0, 0, 64) != 0;
     prev_fixed = __shfl(fixed[0] ? 1 : 0, 0, 64) != 0;
   };
-  const int64_t last = (a.nk + 255) / 256 - 1;
-  int32_t codes[kGroup][4];
+  auto fetch = [&](int64_t t, int32_t& d, int32_t* code) {
+    if (t < 0) {
+      d = -1;
+    } else {
+      d = a.blk[t];  // wave-uniform
+    }
+    const int64_t j0 = t * 256 + 4 * lane;
+    if (d >= 0) {
 #pragma unroll
-  for (int g = 0; g < kGroup; ++g) load_codes(last - g, codes[g]);
+      for (int i = 0; i < 4; ++i) code[i] = static_cast<int32_t>(j0 + i - d);
+    } else if (d == -1) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) code[i] = -1;
+    } else {
+      load_codes(t, code);
+    }
+  };
+  const bool row16 = a.c_s2 == 1 && (reinterpret_cast<uintptr_t>(crow) & 15) == 0;
+  const int64_t last = (a.nk + 255) / 256 - 1;
+  int32_t desc[kGroup], codes[kGroup][4];
+#pragma unroll
+  for (int g = 0; g < kGroup; ++g) fetch(last - g, desc[g], codes[g]);
   for (int64_t t0 = last; t0 >= 0; t0 -= kGroup) {
     float cells[kGroup][4];
 #pragma unroll
-    for (int g = 0; g < kGroup; ++g)
+    for (int g = 0; g < kGroup; ++g) {
+      if (desc[g] >= 0 && row16 && (desc[g] & 3) == 0) {
+        const float4 v4 = *reinterpret_cast<const float4*>(crow + codes[g][0]);
+        cells[g][0] = v4.x;
+        cells[g][1] = v4.y;
+        cells[g][2] = v4.z;
+        cells[g][3] = v4.w;
+      } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        cells[g][i] = codes[g][i] >= 0 ? crow[static_cast<int64_t>(codes[g][i]) * a.c_s2] : 0.f;
-    int32_t next[kGroup][4];
+        for (int i = 0; i < 4; ++i)
+          cells[g][i] = codes[g][i] >= 0 ? crow[static_cast<int64_t>(codes[g][i]) * a.c_s2] : 0.f;
+      }
+    }
+    int32_t ndesc[kGroup], next[kGroup][4];
 #pragma unroll
-    for (int g = 0; g < kGroup; ++g) load_codes(t0 - kGroup - g, next[g]);
+    for (int g = 0; g < kGroup; ++g) fetch(t0 - kGroup - g, ndesc[g], next[g]);
 #pragma unroll
     for (int g = 0; g < kGroup; ++g)
       if (t0 - g >= 0) check_block(t0 - g, codes[g], cells[g]);
 #pragma unroll
-    for (int g = 0; g < kGroup; ++g)
+    for (int g = 0; g < kGroup; ++g) {
+      desc[g] = ndesc[g];
 #pragma unroll
       for (int i = 0; i < 4; ++i) codes[g][i] = next[g][i];
+    }
   }
   for (int off = 32; off > 0; off >>= 1) bits |= __shfl_xor(bits, off, 64);
   const bool any_oob = __any(out_of_range);

@@ -1014,6 +1014,33 @@ __global__ void __launch_bounds__(kPackThreads) policy_pack_kernel(const uint8_t
   if (tid == 0) bnd_count[0] = running < kMaxBoundary ? running : kMaxBoundary;
 }
 
+// Per block of 256 keys, for the checker: the offset o when every key j of
+// the block is fixed with ordinal j - o, -1 when every key is a dynamic key
+// with no fixed neighbour (or past the end), -2 otherwise (the checker then
+// reads the block's codes).  One wave per block.
+__global__ void __launch_bounds__(256) policy_blocks_kernel(const int32_t* code, int64_t nk, int32_t* blk) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t nb = (nk + 255) / 256;
+  if (t >= nb) return;
+  const int64_t j0 = t * 256 + 4 * lane;
+  int32_t c[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) c[i] = j0 + i < nk ? code[j0 + i] : -1;
+  const int64_t first = code[t * 256];
+  const int64_t off = t * 256 - first;
+  bool affine = first >= 0 && t * 256 + 255 < nk;
+  bool plain = true;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    affine = affine && c[i] == j0 + i - off;
+    plain = plain && c[i] == -1;
+  }
+  affine = __all(affine);
+  plain = __all(plain);
+  if (lane == 0) blk[t] = affine ? static_cast<int32_t>(off) : (plain ? -1 : -2);
+}
+
 // Canonical position of each (head, row)'s own key, NaN when the row is not a
 // fixed row the profile covers: canonical[h][q_ord[row]][k_ord[qpos[row]]].
 __global__ void policy_self_kernel(const float* canon, int64_t c_s0, int64_t c_s1, int64_t c_s2,
@@ -1040,6 +1067,7 @@ struct policy_ws {
   int32_t* bnd_count;
   int32_t* bnd_keys;
   int32_t* code;
+  int32_t* blk;
   float* canon_self;
   int64_t bytes;
 };
@@ -1057,6 +1085,7 @@ policy_ws carve_policy(char* base, int32_t nq, int32_t hq, int64_t nk) {
   w.bnd_count = reinterpret_cast<int32_t*>(take(16));
   w.bnd_keys = reinterpret_cast<int32_t*>(take(4 * kMaxBoundary));
   w.code = reinterpret_cast<int32_t*>(take(4 * nk));
+  w.blk = reinterpret_cast<int32_t*>(take(4 * ((nk + 255) / 256)));
   w.canon_self = reinterpret_cast<float*>(take(4 * static_cast<int64_t>(nq) * hq));
   w.bytes = off;
   return w;
@@ -1208,12 +1237,17 @@ extern "C" int cs_ccpe_prefill_policy_bf16(const cs_ccpe_args* a, void* workspac
     c.c_s2 = a->canonical.stride[2];
     c.q_ord = a->q_ord;
     c.code = w.code;
+    c.blk = w.blk;
     c.bnd_count = w.bnd_count;
     c.bnd_keys = w.bnd_keys;
     c.npos = static_cast<int32_t>(ev.shape[1]);
     c.strict = a->strict;
     c.chunk_rows = a->chunk_rows;
     c.chunk_flags = a->chunk_flags;
+    const int64_t nb = (static_cast<int64_t>(nk) + 255) / 256;
+    if (nb > 0)
+      hipLaunchKernelGGL(policy_blocks_kernel, dim3(static_cast<uint32_t>((nb + 3) / 4)), dim3(256), 0, s, w.code,
+                         static_cast<int64_t>(nk), w.blk);
     const int cst = cs::launch_policy_check(c, s);
     if (cst) return cst;
   }
