@@ -1185,12 +1185,21 @@ __global__ void __launch_bounds__(256) update_fused_kernel(update_checks c, upda
 // order.
 // The status of an update for the host: the flags word and the three counts,
 // written by the thread that wrote the counts (after them, in its program
-// order), as plain stores into host-visible memory.
-__device__ inline void write_report(int64_t* report, const int32_t* flags, const int64_t* counts) {
+// order), as plain stores into host-visible memory.  With clear set the same
+// thread then zeroes the status block for the next call (every other write
+// to it in this call is ordered before: the flags' atomics by the kernel
+// boundary, the counts by the thread's own program order).
+__device__ inline void write_report(int64_t* report, int32_t* flags, int64_t* counts, bool clear) {
   report[0] = static_cast<int64_t>(static_cast<uint32_t>(*flags));
   report[1] = counts[0];
   report[2] = counts[1];
   report[3] = counts[2];
+  if (clear) {
+    *flags = 0;
+    counts[0] = 0;
+    counts[1] = 0;
+    counts[2] = 0;
+  }
 }
 
 __global__ void status_clear_kernel(int32_t* flags, int64_t* counts) {
@@ -1198,8 +1207,8 @@ __global__ void status_clear_kernel(int32_t* flags, int64_t* counts) {
   if (threadIdx.x < 3) counts[threadIdx.x] = 0;
 }
 
-__global__ void status_report_kernel(int64_t* report, const int32_t* flags, const int64_t* counts) {
-  if (threadIdx.x == 0) write_report(report, flags, counts);
+__global__ void status_report_kernel(int64_t* report, int32_t* flags, int64_t* counts, int32_t clear) {
+  if (threadIdx.x == 0) write_report(report, flags, counts, clear != 0);
 }
 
 struct update_final {
@@ -1218,8 +1227,9 @@ struct update_final {
   int64_t* report;    // NULL, or host-visible {flags word, counts[0..2]}
   int32_t gate, distance;
   double threshold;
-  const int32_t* flags;
+  int32_t* flags;
   int32_t abort_mask;
+  int32_t clear_after;  // zero the status block once the report is written
 };
 
 __global__ void __launch_bounds__(kSelThreads) update_finalize_kernel(update_final f) {
@@ -1244,7 +1254,7 @@ __global__ void __launch_bounds__(kSelThreads) update_finalize_kernel(update_fin
                 f.counts + 1, f.flags, f.abort_mask);
   __syncthreads();
   nonzero_block(f.selected, f.mandatory, f.n, f.active, f.counts + 2);
-  if (threadIdx.x == 0 && f.report) write_report(f.report, f.flags, f.counts);
+  if (threadIdx.x == 0 && f.report) write_report(f.report, f.flags, f.counts, f.clear_after != 0);
 }
 
 // Stores the 16 bits of a run as bytes 0 / 1 (run_mask's inverse).
@@ -1467,7 +1477,7 @@ __global__ void __launch_bounds__(kSelThreads) update_finalize_small_kernel(upda
     store_run_mask(f.candidate, s, n, cand);
     store_run_mask(f.removed_mask, s, n, remm);
   }
-  if (tid == 0 && f.report) write_report(f.report, f.flags, f.counts);
+  if (tid == 0 && f.report) write_report(f.report, f.flags, f.counts, f.clear_after != 0);
 }
 
 // Fills one check segment when v is contiguous, 16-byte aligned and floating;
@@ -1522,9 +1532,10 @@ bool fused_update_ok(const cs_wca_update_args* u) {
 extern "C" int cs_wca_update(const cs_wca_update_args* u, void* stream) {
   CS_REQUIRE(u && u->flags && u->counts, "null arguments");
   CS_REQUIRE(u->a >= 0 && (!u->computed || u->a == 0 || u->rows), "null arguments");
+  CS_REQUIRE(!(u->clear_status & 2) || u->report, "clearing the status at the end needs a report");
   int32_t* f = u->flags;
   int st;
-  if (u->clear_status) {
+  if (u->clear_status & 1) {
     hipLaunchKernelGGL(status_clear_kernel, dim3(1), dim3(64), 0, as_stream(stream), f, u->counts);
     CS_LAUNCH_CHECK("wca_update status");
   }
@@ -1617,17 +1628,22 @@ extern "C" int cs_wca_update(const cs_wca_update_args* u, void* stream) {
     fin.promoted = u->promoted;
     fin.report = u->report;
     const bool small = u->n <= kChunk;
+    // promotions beyond what the small finish orders get their own launch
+    // (kmax bounds the device count); it reads counts[1], so the status is
+    // then cleared by a launch of its own behind it
+    const int64_t kmax = u->budget < u->n ? (u->budget > 0 ? u->budget : 0) : u->n;
+    const int64_t done = small ? kRankMax : 0;
+    const bool order = kmax > done;
+    fin.clear_after = (u->clear_status & 2) && !order;
     if (small)
       hipLaunchKernelGGL(update_finalize_small_kernel, dim3(1), dim3(kSelThreads), 0, s, fin);
     else
       hipLaunchKernelGGL(update_finalize_kernel, dim3(1), dim3(kSelThreads), 0, s, fin);
-    // promotions beyond what the small finish orders get their own launch
-    // (kmax bounds the device count)
-    const int64_t kmax = u->budget < u->n ? (u->budget > 0 ? u->budget : 0) : u->n;
-    const int64_t done = small ? kRankMax : 0;
-    if (kmax > done)
+    if (order) {
       hipLaunchKernelGGL(wca_promote_order_kernel, dim3(ceil_div(kmax, 64)), dim3(64 * kOrderSlices), 0,
                          s, u->scratch, u->n, u->counts + 1, u->promoted, done);
+      if (u->clear_status & 2) hipLaunchKernelGGL(status_clear_kernel, dim3(1), dim3(64), 0, s, f, u->counts);
+    }
     CS_LAUNCH_CHECK("wca_update");
     return CS_OK;
   }
@@ -1664,7 +1680,8 @@ extern "C" int cs_wca_update(const cs_wca_update_args* u, void* stream) {
   CS_STEP(cs_mask_nonzero(u->selected, u->mandatory, u->n, u->active, u->counts + 2, stream));
 #undef CS_STEP
   if (u->report) {
-    hipLaunchKernelGGL(status_report_kernel, dim3(1), dim3(64), 0, as_stream(stream), u->report, f, u->counts);
+    hipLaunchKernelGGL(status_report_kernel, dim3(1), dim3(64), 0, as_stream(stream), u->report, f, u->counts,
+                       u->clear_status & 2);
     CS_LAUNCH_CHECK("wca_update report");
   }
   return CS_OK;

@@ -280,6 +280,7 @@ class WCAState:
     _work_i64: Tensor | None = field(default=None, repr=False, compare=False)
     _update_args: object = field(default=None, repr=False, compare=False)
     _status_block: object = field(default=None, repr=False, compare=False)
+    _status_dirty: bool = field(default=True, repr=False, compare=False)
 
     @classmethod
     def initialize(
@@ -427,14 +428,15 @@ class WCAState:
 
     def _status(self, device) -> tuple:
         """The one-call update's status: a device int64[4] block (flags word,
-        three counts) that cs_wca_update clears itself, its pinned host mirror
-        that the call's last kernel fills, and the launch stream."""
+        three counts) that cs_wca_update zeroes again after its last kernel
+        has copied it into the pinned host mirror, and the launch stream."""
         status = self._status_block
         if status is None or status[0].device != device:
             block = torch.zeros(4, dtype=torch.int64, device=device)
             host = torch.zeros(4, dtype=torch.int64, pin_memory=True)
             status = self._status_block = (block, host, _hip.stream_of(device),
                                            torch.cuda.current_stream(device))
+            self._status_dirty = True
         return status
 
     def _update_device(self, layer_index, device, cached_k, cached_v, recomputed_k, recomputed_v,
@@ -449,16 +451,16 @@ class WCAState:
         m = max(n, 1)
         fused = torch.empty((2, a, *cached_k.shape[1:]), dtype=cached_k.dtype, device=device)
         fused_k, fused_v = fused[0], fused[1]
+        # int64 [used (fp64 bits) a | promoted m | active m | removed a]
         ibuf = torch.empty(2 * m + 2 * a, dtype=torch.long, device=device)
-        promoted_buf, active_buf = ibuf[:m], ibuf[m:2 * m]
-        removed_buf = ibuf[2 * m:2 * m + a] if gate else None
-        used = ibuf[2 * m + a:].view(torch.float64)
+        ib = ibuf.data_ptr()
         computed = computed_indices.contiguous() if computed_indices is not None else None
         steps, abort_mask = _update_steps(computed is not None)
         u = self._update_args
         if u is None:
             u = self._update_args = _hip.CsWcaUpdateArgs()
-            u.clear_status = 1
+        # bit 1: the call leaves the block zeroed; bit 0 also zeroes it first
+        u.clear_status = 3 if self._status_dirty else 2
         u.budget = self.budget
         u.alpha, u.deviation = _raw(self.alpha), _raw(self.initial_deviation)
         u.selected, u.candidate = _raw(self.selected_mask), _raw(self.candidate_mask)
@@ -470,33 +472,43 @@ class WCAState:
         u.distance_mode = 1 if config.convergence_mode == "distance_lt" else 0
         u.cached_k, u.cached_v = _hip.view(cached_k), _hip.view(cached_v)
         u.recomputed_k, u.recomputed_v = _hip.view(recomputed_k), _hip.view(recomputed_v)
-        u.fused_k, u.fused_v = _hip.view(fused_k), _hip.view(fused_v)
+        fk = _hip.view(fused_k)  # fused_v differs from it in the data pointer only
+        u.fused_k = fk
+        if a:
+            fk.data = fused_v.data_ptr()
+        u.fused_v = fk
         u.rows, u.computed = _raw(indices), _raw(computed)
         u.a, u.n = a, n
         base = work.data_ptr()
         u.err, u.norm, u.next_alpha, u.cosine = base, base + 8 * n, base + 16 * n, base + 24 * n
-        u.used, u.removed = _raw(used), _raw(removed_buf)
-        u.promoted, u.scratch, u.active = _raw(promoted_buf), _raw(scratch), _raw(active_buf)
+        u.used, u.promoted, u.active = ib, ib + 8 * a, ib + 8 * (a + m)
+        u.removed = ib + 8 * (a + 2 * m) if gate else None
+        u.scratch = _raw(scratch)
         u.flags, u.counts = block.data_ptr(), block.data_ptr() + 8
         u.report = host.data_ptr()
         u.gate = 1 if gate else 0
         u.abort_mask = abort_mask
+        self._status_dirty = True
         call("cs_wca_update", ctypes.byref(u), stream)
+        self._status_dirty = False
         torch_stream.synchronize()
         words = host.tolist()
         value = words[0] & 0xFFFFFFFF
         for bits, exc, message in steps:
             if value & bits:
                 raise exc(message)
-        return self._finish_update(layer_index, words[1:], indices, fused_k, fused_v, used, gate,
-                                   removed_buf, promoted_buf, active_buf)
+        n_removed, n_promoted, n_active = words[1:]
+        used = ibuf[:a].view(torch.float64)
+        promoted = ibuf[a:a + n_promoted]
+        active = ibuf[a + m:a + m + n_active]
+        removed = ibuf[a + 2 * m:a + 2 * m + n_removed] if gate else indices[:0]
+        return self._finish_update(layer_index, indices, fused_k, fused_v, used, removed, promoted,
+                                   active)
 
-    def _finish_update(self, layer_index, counts, indices, fused_k, fused_v, used, gate, removed_buf,
-                       promoted_buf, active_buf) -> WCAUpdate:
-        n_removed, n_promoted, n_active = counts
-        removed = removed_buf[:n_removed] if gate else indices[:0]
-        promoted = promoted_buf[:n_promoted]
-        next_indices = self._cache_active(active_buf, n_active)
+    def _finish_update(self, layer_index, indices, fused_k, fused_v, used, removed, promoted,
+                       next_indices) -> WCAUpdate:
+        self._active = next_indices
+        self._active_key = self._mask_key() + (next_indices._version,)
         self.last_layer = layer_index
         return WCAUpdate(
             indices=indices,
@@ -578,5 +590,7 @@ class WCAState:
         call("cs_mask_nonzero", ptr(self.selected_mask), ptr(self.mandatory_mask), n, ptr(active_buf),
              fl.counter(2), fl.stream)
         fl.finish(read=True)
-        return self._finish_update(layer_index, fl.counts, indices, fused_k, fused_v, used, gate,
-                                   removed_buf, promoted_buf, active_buf)
+        n_removed, n_promoted, n_active = fl.counts
+        removed = removed_buf[:n_removed] if gate else indices[:0]
+        return self._finish_update(layer_index, indices, fused_k, fused_v, used, removed,
+                                   promoted_buf[:n_promoted], active_buf[:n_active])

@@ -487,7 +487,11 @@ typedef struct cs_wca_update_args {
   int64_t* counts;          /* [3] */
   double epsilon, threshold;
   int32_t clamp, previous_layer, gate, distance_mode, abort_mask;
-  int32_t clear_status;     /* nonzero: the call zeroes flags and counts[3] first */
+  int32_t clear_status;     /* bit 0: the call zeroes flags and counts[3] first;
+                               bit 1 (needs report): once the report is written the
+                               call zeroes them again, so a caller that keeps one
+                               block for consecutive calls sets bit 0 only on its
+                               first call and after a call that returned an error */
   int64_t* report;          /* NULL, or host-visible int64[4] that receives the flags
                                word and counts[0..2] from the call's last kernel
                                (read it after synchronizing the stream) */
