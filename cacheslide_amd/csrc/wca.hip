@@ -203,6 +203,29 @@ __device__ inline int block_scan(int v, int* wave_tot, int& excl) {
   return total;
 }
 
+// block_scan over int64 (several counts packed in fields of one word).
+__device__ inline int64_t block_scan64(int64_t v, int64_t* wave_tot, int64_t& excl) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int64_t incl = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int64_t t = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += t;
+  }
+  if (lane == 63) wave_tot[w] = incl;
+  __syncthreads();
+  int64_t before = 0, total = 0;
+#pragma unroll
+  for (int i = 0; i < kSelWaves; ++i) {
+    const int64_t t = wave_tot[i];
+    before += i < w ? t : 0;
+    total += t;
+  }
+  __syncthreads();
+  excl = before + incl - v;
+  return total;
+}
+
 // Bit j set when p[start + j] != 0 (j < kRun, start + j < n).
 __device__ inline uint32_t run_mask(const uint8_t* p, int64_t start, int64_t n) {
   uint32_t m = 0;
@@ -1287,6 +1310,7 @@ __global__ void __launch_bounds__(kSelThreads) update_finalize_small_kernel(upda
   __shared__ uint32_t sel_run[kSelThreads];
   __shared__ uint32_t rm_run[kSelThreads];
   __shared__ int wave_tot[kSelWaves];
+  __shared__ int64_t wave_tot64[kSelWaves];
   __shared__ int hist[256];
   __shared__ uint64_t s_prefix, s_mask;
   __shared__ int64_t s_remaining;
@@ -1301,31 +1325,46 @@ __global__ void __launch_bounds__(kSelThreads) update_finalize_small_kernel(upda
   uint32_t remm = run_mask(f.removed_mask, s, n);
   const uint32_t mand = f.mandatory ? run_mask(f.mandatory, s, n) : 0u;
   const bool abort = (*f.flags & f.abort_mask) != 0;
-  // commit of the next weights, first (nothing below reads alpha): the
-  // loads of a thread go out with the mask loads, the stores once the flags
-  // have arrived
-  for (int64_t i0 = 0; i0 < a; i0 += 4 * kSelThreads) {
-    int64_t r4[4];
-    double n4[4];
+  // commit of the next weights (nothing below reads alpha): the first
+  // 4 * kSelThreads entries are loaded with the masks and stored before the
+  // gate on gate layers, else after the counting scan, so that without a
+  // gate or a promotion no barrier waits for their stores; entries past
+  // them are committed here
+  int64_t r4[4];
+  double n4[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int64_t i = u * kSelThreads + tid;
+    r4[u] = i < a ? f.rows[i] : -1;
+    n4[u] = i < a ? f.next[i] : 0.0;
+  }
+  for (int64_t i0 = 4 * kSelThreads; i0 < a; i0 += 4 * kSelThreads) {
+    int64_t rr[4];
+    double nr[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int64_t i = i0 + u * kSelThreads + tid;
-      r4[u] = i < a ? f.rows[i] : -1;
-      n4[u] = i < a ? f.next[i] : 0.0;
+      rr[u] = i < a ? f.rows[i] : -1;
+      nr[u] = i < a ? f.next[i] : 0.0;
     }
+    if (!abort) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (rr[u] >= 0) f.alpha[rr[u]] = nr[u];
+    }
+  }
+
+  // gate (gate_block): the selected rows whose metric is below the threshold
+  int64_t nrem = 0;
+  if (f.gate) {
     if (!abort) {
 #pragma unroll
       for (int u = 0; u < 4; ++u)
         if (r4[u] >= 0) f.alpha[r4[u]] = n4[u];
     }
-  }
-  sel_run[tid] = sel;
-  rm_run[tid] = 0;
-  __syncthreads();
-
-  // gate (gate_block): the selected rows whose metric is below the threshold
-  int64_t nrem = 0;
-  if (f.gate) {
+    sel_run[tid] = sel;
+    rm_run[tid] = 0;
+    __syncthreads();
     for (int64_t c0 = 0; c0 < a; c0 += kChunk) {
       const int64_t s2 = c0 + s;
       uint32_t fl = 0;
@@ -1346,34 +1385,51 @@ __global__ void __launch_bounds__(kSelThreads) update_finalize_small_kernel(upda
       }
       nrem += tot;
     }
+    __syncthreads();
+    if (!abort) {
+      const uint32_t r = rm_run[tid];
+      sel &= ~r;
+      cand &= ~r;
+      remm |= r;
+    }
   }
   if (tid == 0) f.counts[0] = nrem;
-  __syncthreads();
-  if (!abort) {
-    const uint32_t r = rm_run[tid];
-    sel &= ~r;
-    cand &= ~r;
-    remm |= r;
-  }
 
   // promotion (promote_block, one chunk): slots = max(0, budget - #selected),
   // available = candidate & ~selected & ~removed, the k largest keys taken
+  // one scan for three counts in 16-bit fields (each total is at most
+  // kChunk = 2^14): selected, available, and selected | mandatory -- the
+  // next active rows' positions when nothing gets promoted
   const uint32_t av = cand & ~sel & ~remm;
-  int ex;
-  const int total_sel = block_scan(__popc(sel), wave_tot, ex);
-  const int total_av = block_scan(__popc(av), wave_tot, ex);
+  int64_t ex;
+  const int64_t packed = block_scan64(static_cast<int64_t>(__popc(sel)) |
+                                          (static_cast<int64_t>(__popc(av)) << 16) |
+                                          (static_cast<int64_t>(__popc(sel | mand)) << 32),
+                                      wave_tot64, ex);
+  const int total_sel = static_cast<int>(packed & 0xffff);
+  const int total_av = static_cast<int>((packed >> 16) & 0xffff);
   int64_t slots = f.budget - total_sel;
   if (slots < 0) slots = 0;
-  const int64_t k = abort ? 0 : (slots < total_av ? slots : total_av);
-  if (tid == 0) {
-    s_prefix = 0;
-    s_mask = 0;
-    s_remaining = k;
-    s_done = k == total_av;
-    f.counts[1] = k;
+  // the same on every lane (at most kChunk); read from one lane so the
+  // branches below are uniform and their values do not stay live across
+  // each other
+  const int64_t k = __builtin_amdgcn_readfirstlane(
+      static_cast<int>(abort ? 0 : (slots < total_av ? slots : total_av)));
+  if (tid == 0) f.counts[1] = k;
+  if (!abort && !f.gate) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (r4[u] >= 0) f.alpha[r4[u]] = n4[u];
   }
-  __syncthreads();
+  int nz_pos, nz_tot;  // positions of the next active rows
   if (k > 0) {
+    if (tid == 0) {
+      s_prefix = 0;
+      s_mask = 0;
+      s_remaining = k;
+      s_done = k == total_av;
+    }
+    __syncthreads();
     uint64_t kb[kRun] = {};
     if (s < n) load_key_run(f.deviation, s, n, kb);
     for (int pass = 0; pass < 8 && !s_done; ++pass) {
@@ -1462,15 +1518,17 @@ __global__ void __launch_bounds__(kSelThreads) update_finalize_small_kernel(upda
         f.promoted[rank] = p_tok[e];
       }
     }
+    nz_tot = block_scan(__popc(sel | mand), wave_tot, nz_pos);
+  } else {
+    nz_pos = static_cast<int>(ex >> 32);
+    nz_tot = static_cast<int>(packed >> 32);
   }
 
   // next active rows (nonzero_block): ascending tokens of selected | mandatory
   {
-    uint32_t m = sel | mand;
-    int pos;
-    const int tot = block_scan(__popc(m), wave_tot, pos);
-    for (; m; m &= m - 1) f.active[pos++] = s + (__ffs(m) - 1);
-    if (tid == 0) f.counts[2] = tot;
+    int pos = nz_pos;
+    for (uint32_t m = sel | mand; m; m &= m - 1) f.active[pos++] = s + (__ffs(m) - 1);
+    if (tid == 0) f.counts[2] = nz_tot;
   }
   if (s < n) {
     store_run_mask(f.selected, s, n, sel);
@@ -1504,7 +1562,7 @@ bool check_segment(const cs_view* v, int32_t bit, update_checks& c, int seg, int
   c.p[seg] = static_cast<const uint4*>(v->data);
   c.words[seg] = bytes / 16;
   c.kind[seg] = v->dtype == CS_BF16 ? 0 : v->dtype == CS_F16 ? 1 : v->dtype == CS_F32 ? 2 : 3;
-  blocks += std::min<int64_t>(ceil_div(c.words[seg], 256 * 4), 4096);
+  blocks += std::min<int64_t>(ceil_div(c.words[seg], 256 * 8), 4096);
   return true;
 }
 }  // namespace

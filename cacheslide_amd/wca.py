@@ -497,7 +497,7 @@ class WCAState:
         for bits, exc, message in steps:
             if value & bits:
                 raise exc(message)
-        n_removed, n_promoted, n_active = words[1:]
+        n_removed, n_promoted, n_active = words[1:4]
         used = ibuf[:a].view(torch.float64)
         promoted = ibuf[a:a + n_promoted]
         active = ibuf[a + m:a + m + n_active]
