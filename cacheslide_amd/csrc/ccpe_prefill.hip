@@ -54,6 +54,8 @@
 // in consecutive offsets takes the scalar-base form; other loads address each
 // lane's record.
 
+#include <mutex>
+
 #include "common.h"
 #include "ccpe_path.h"
 
@@ -797,6 +799,40 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
 using namespace cs;
 
 namespace {
+// A second stream per device for the policy checker, so that the check runs
+// beside the attention kernel: an event forks it from the caller's stream
+// once the shared inputs are staged, and the caller's stream waits for its
+// end event.  Default priority; created on first use, kept until the
+// process ends.  The mutex covers the fork, the launches and the join.
+struct side_lane {
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+constexpr int kSideDevices = 64;
+std::mutex g_side_mutex;
+side_lane g_side[kSideDevices];
+
+int side_lane_of_current(side_lane** out) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) {
+    set_error("hipGetDevice: %s", hipGetErrorString(err));
+    return CS_ELAUNCH;
+  }
+  CS_REQUIRE(dev >= 0 && dev < kSideDevices, "device ordinal %d out of range", dev);
+  side_lane& l = g_side[dev];
+  if (l.stream == nullptr) {
+    if ((err = hipStreamCreateWithFlags(&l.stream, hipStreamNonBlocking)) != hipSuccess ||
+        (err = hipEventCreateWithFlags(&l.fork, hipEventDisableTiming)) != hipSuccess ||
+        (err = hipEventCreateWithFlags(&l.join, hipEventDisableTiming)) != hipSuccess) {
+      set_error("policy check stream: %s", hipGetErrorString(err));
+      return CS_ELAUNCH;
+    }
+  }
+  *out = &l;
+  return CS_OK;
+}
+
 // Compute units of the current device (cached per device).
 int device_cus() {
   static int cus[64] = {};
@@ -1210,15 +1246,18 @@ extern "C" int cs_ccpe_prefill_policy_bf16(const cs_ccpe_args* a, void* workspac
     p.canon_self = w.canon_self;
     p.q_ord = a->q_ord;
   }
-  const dim3 grid(p.total_wg), block(64 * waves);
-  if (waves == 8)
-    hipLaunchKernelGGL((ccpe_prefill_kernel<0, 8, true>), grid, block, smem, s, p);
-  else if (waves == 2)
-    hipLaunchKernelGGL((ccpe_prefill_kernel<0, 2, true>), grid, block, smem, s, p);
-  else
-    hipLaunchKernelGGL((ccpe_prefill_kernel<0, 4, true>), grid, block, smem, s, p);
-  CS_LAUNCH_CHECK("ccpe_prefill_policy");
+  std::unique_lock<std::mutex> side_lock(g_side_mutex, std::defer_lock);
+  side_lane* side = nullptr;
   if (canon) {
+    side_lock.lock();
+    const int sst = side_lane_of_current(&side);
+    if (sst) return sst;
+    hipError_t err = hipEventRecord(side->fork, s);
+    if (err == hipSuccess) err = hipStreamWaitEvent(side->stream, side->fork, 0);
+    if (err != hipSuccess) {
+      set_error("policy check fork: %s", hipGetErrorString(err));
+      return CS_ELAUNCH;
+    }
     cs::policy_check_args c{};
     c.q = static_cast<const uint16_t*>(qv.data);
     c.q_s_tok = qv.stride[0];
@@ -1246,10 +1285,30 @@ extern "C" int cs_ccpe_prefill_policy_bf16(const cs_ccpe_args* a, void* workspac
     c.chunk_flags = a->chunk_flags;
     const int64_t nb = (static_cast<int64_t>(nk) + 255) / 256;
     if (nb > 0)
-      hipLaunchKernelGGL(policy_blocks_kernel, dim3(static_cast<uint32_t>((nb + 3) / 4)), dim3(256), 0, s, w.code,
-                         static_cast<int64_t>(nk), w.blk);
-    const int cst = cs::launch_policy_check(c, s);
+      hipLaunchKernelGGL(policy_blocks_kernel, dim3(static_cast<uint32_t>((nb + 3) / 4)), dim3(256), 0,
+                         side->stream, w.code, static_cast<int64_t>(nk), w.blk);
+    const int cst = cs::launch_policy_check(c, side->stream);
     if (cst) return cst;
+    err = hipEventRecord(side->join, side->stream);
+    if (err != hipSuccess) {
+      set_error("policy check join: %s", hipGetErrorString(err));
+      return CS_ELAUNCH;
+    }
+  }
+  const dim3 grid(p.total_wg), block(64 * waves);
+  if (waves == 8)
+    hipLaunchKernelGGL((ccpe_prefill_kernel<0, 8, true>), grid, block, smem, s, p);
+  else if (waves == 2)
+    hipLaunchKernelGGL((ccpe_prefill_kernel<0, 2, true>), grid, block, smem, s, p);
+  else
+    hipLaunchKernelGGL((ccpe_prefill_kernel<0, 4, true>), grid, block, smem, s, p);
+  CS_LAUNCH_CHECK("ccpe_prefill_policy");
+  if (side) {
+    const hipError_t err = hipStreamWaitEvent(s, side->join, 0);
+    if (err != hipSuccess) {
+      set_error("policy check join: %s", hipGetErrorString(err));
+      return CS_ELAUNCH;
+    }
   }
   return CS_OK;
 }
