@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import struct
 from pathlib import Path
 
 import torch
@@ -87,6 +88,12 @@ class CsWcaUpdateArgs(ctypes.Structure):
         ("distance_mode", ctypes.c_int32), ("abort_mask", ctypes.c_int32),
         ("clear_status", ctypes.c_int32), ("report", ctypes.c_void_p),
     ]
+
+
+# cs_wca_update_args from ``rows`` to ``report`` as bytes: two pointers, a, n,
+# budget, seventeen pointers, epsilon, threshold, six int32 fields, report
+WCA_UPDATE_TAIL = struct.Struct("<2q3q17q2d6iq")
+assert WCA_UPDATE_TAIL.size == ctypes.sizeof(CsWcaUpdateArgs) - CsWcaUpdateArgs.rows.offset
 
 
 class CsCcpeArgs(ctypes.Structure):
@@ -299,6 +306,20 @@ def view(tensor: torch.Tensor | None) -> CsView:
     v.shape[:nd] = tensor.shape
     v.stride[:nd] = tensor.stride()
     return v
+
+
+# CsView as bytes: data, dtype, ndim, shape[6], stride[6]
+_VIEW = struct.Struct("<qii6q6q")
+assert _VIEW.size == ctypes.sizeof(CsView)
+
+
+def pack_view3(target, offset: int, tensor: torch.Tensor) -> None:
+    """Write view(tensor) of a 3-d tensor into the CsView field of a ctypes
+    structure at byte ``offset`` (one pack, for per-call argument blocks)."""
+    s0, s1, s2 = tensor.shape
+    r0, r1, r2 = tensor.stride()
+    _VIEW.pack_into(target, offset, tensor.data_ptr() if s0 * s1 * s2 else 0, dtype_code(tensor.dtype), 3,
+                    s0, s1, s2, 0, 0, 0, r0, r1, r2, 0, 0, 0)
 
 
 def vref(tensor: torch.Tensor | None):

@@ -90,11 +90,6 @@ def _kv(name: str, tensor: Tensor, fl: _Flags, view=None) -> None:
     _finite_step(name, fl)
 
 
-def _raw(tensor: Tensor | None):
-    """Address for a struct field, None (NULL) for an absent or empty tensor, as ``ptr``."""
-    return tensor.data_ptr() if tensor is not None and tensor.numel() else None
-
-
 def _finite_step(name: str, fl: _Flags) -> None:
     fl.step(_NONFINITE_BIT[name], WCANumericalError, f"{name} must have finite values")
 
@@ -130,6 +125,12 @@ def _update_steps(computed: bool) -> tuple[list, int]:
             mask |= bits
         _UPDATE_STEPS[computed] = (steps, mask)
     return _UPDATE_STEPS[computed]
+
+
+# byte offsets of the per-call fields of cs_wca_update_args
+_CK, _CV, _RK, _RV, _FK, _FV = (getattr(_hip.CsWcaUpdateArgs, f).offset for f in (
+    "cached_k", "cached_v", "recomputed_k", "recomputed_v", "fused_k", "fused_v"))
+_TAIL = _hip.CsWcaUpdateArgs.rows.offset
 
 
 def _matching(name: str, tensor: Tensor, reference_shape, reference: Tensor, fl: _Flags,
@@ -459,38 +460,30 @@ class WCAState:
         u = self._update_args
         if u is None:
             u = self._update_args = _hip.CsWcaUpdateArgs()
-        # bit 1: the call leaves the block zeroed; bit 0 also zeroes it first
-        u.clear_status = 3 if self._status_dirty else 2
-        u.budget = self.budget
-        u.alpha, u.deviation = _raw(self.alpha), _raw(self.initial_deviation)
-        u.selected, u.candidate = _raw(self.selected_mask), _raw(self.candidate_mask)
-        u.removed_mask, u.mandatory = _raw(self.removed_mask), _raw(self.mandatory_mask)
+        # the six views, then every field from rows to report in one pack
+        for field, tensor in ((_CK, cached_k), (_CV, cached_v), (_RK, recomputed_k), (_RV, recomputed_v),
+                              (_FK, fused_k), (_FV, fused_v)):
+            _hip.pack_view3(u, field, tensor)
         config = self.config
-        u.epsilon, u.threshold = float(config.epsilon), float(config.convergence_threshold)
-        u.clamp = 1 if config.clamp_alpha else 0
-        u.previous_layer = 1 if config.weight_update == "previous_layer" else 0
-        u.distance_mode = 1 if config.convergence_mode == "distance_lt" else 0
-        u.cached_k, u.cached_v = _hip.view(cached_k), _hip.view(cached_v)
-        u.recomputed_k, u.recomputed_v = _hip.view(recomputed_k), _hip.view(recomputed_v)
-        fk = _hip.view(fused_k)  # fused_v differs from it in the data pointer only
-        u.fused_k = fk
-        if a:
-            fk.data = fused_v.data_ptr()
-        u.fused_v = fk
-        u.rows, u.computed = _raw(indices), _raw(computed)
-        u.a, u.n = a, n
         base = work.data_ptr()
-        u.err, u.norm, u.next_alpha, u.cosine = base, base + 8 * n, base + 16 * n, base + 24 * n
-        u.used, u.promoted, u.active = ib, ib + 8 * a, ib + 8 * (a + m)
-        u.removed = ib + 8 * (a + 2 * m) if gate else None
-        u.scratch = _raw(scratch)
-        u.flags, u.counts = block.data_ptr(), block.data_ptr() + 8
-        u.report = host.data_ptr()
-        u.gate = 1 if gate else 0
-        u.abort_mask = abort_mask
+        flags = block.data_ptr()
+        # the per-token state (NULL for a request without tokens)
+        state = (self.alpha.data_ptr(), self.initial_deviation.data_ptr(), self.selected_mask.data_ptr(),
+                 self.candidate_mask.data_ptr(), self.removed_mask.data_ptr(),
+                 self.mandatory_mask.data_ptr(), scratch.data_ptr()) if n else (0,) * 7
+        # clear_status bit 1: the call leaves the block zeroed; bit 0 also zeroes it first
+        _hip.WCA_UPDATE_TAIL.pack_into(
+            u, _TAIL, indices.data_ptr() if a else 0, computed.data_ptr() if computed is not None and a else 0,
+            a, n, self.budget, *state[:6], base, base + 8 * n, base + 16 * n, base + 24 * n,
+            ib, ib + 8 * (a + 2 * m) if gate else 0, ib + 8 * a, state[6], ib + 8 * (a + m),
+            flags, flags + 8, float(config.epsilon), float(config.convergence_threshold),
+            1 if config.clamp_alpha else 0, 1 if config.weight_update == "previous_layer" else 0,
+            1 if gate else 0, 1 if config.convergence_mode == "distance_lt" else 0, abort_mask,
+            3 if self._status_dirty else 2, host.data_ptr())
         self._status_dirty = True
         call("cs_wca_update", ctypes.byref(u), stream)
         self._status_dirty = False
+        used = ibuf[:a].view(torch.float64)  # while the device works
         torch_stream.synchronize()
         words = host.tolist()
         value = words[0] & 0xFFFFFFFF
@@ -498,7 +491,6 @@ class WCAState:
             if value & bits:
                 raise exc(message)
         n_removed, n_promoted, n_active = words[1:4]
-        used = ibuf[:a].view(torch.float64)
         promoted = ibuf[a:a + n_promoted]
         active = ibuf[a + m:a + m + n_active]
         removed = ibuf[a + 2 * m:a + 2 * m + n_removed] if gate else indices[:0]
