@@ -7,6 +7,8 @@ import ctypes
 import re
 from pathlib import Path
 
+import torch
+
 from cacheslide_amd import _hip
 
 HEADER = Path(__file__).resolve().parents[1] / "include" / "cacheslide_hip.h"
@@ -82,6 +84,36 @@ def test_wca_update_checks_arguments_without_a_device():
     args = _hip.CsWcaUpdateArgs()          # no status block
     assert lib.cs_wca_update(ctypes.byref(args), None) == _hip.CS_EINVAL
     assert ctypes.sizeof(_hip.CsWcaUpdateArgs) == 896   # the C struct's size on x86-64
+    # clearing the status at the end (bit 1) needs a report word; refused
+    # before any launch (host buffers stand in for the status block)
+    block = (ctypes.c_int64 * 4)()
+    args.flags, args.counts = ctypes.addressof(block), ctypes.addressof(block) + 8
+    args.clear_status = 2
+    assert lib.cs_wca_update(ctypes.byref(args), None) == _hip.CS_EINVAL
+    assert b"report" in lib.cs_last_error()
+
+
+def test_wca_update_argument_packs_match_the_ctypes_fields():
+    """The update's per-call argument block is written by two struct packs;
+    they must land exactly where the ctypes fields (the C layout) are."""
+    t = torch.empty((5, 3, 16), dtype=torch.bfloat16)[:, 1:, :]  # strided view
+    packed = _hip.CsWcaUpdateArgs()
+    _hip.pack_view3(packed, _hip.CsWcaUpdateArgs.recomputed_v.offset, t)
+    ref = _hip.view(t)
+    got = packed.recomputed_v
+    assert (got.data, got.dtype, got.ndim) == (ref.data, ref.dtype, ref.ndim)
+    assert list(got.shape) == list(ref.shape) and list(got.stride) == list(ref.stride)
+    empty = torch.empty((0, 2, 16), dtype=torch.float32)
+    _hip.pack_view3(packed, _hip.CsWcaUpdateArgs.fused_k.offset, empty)
+    assert packed.fused_k.data is None and list(packed.fused_k.shape[:3]) == [0, 2, 16]
+    names = [name for name, _ in _hip.CsWcaUpdateArgs._fields_]
+    tail = names[names.index("rows"):]
+    values = list(range(1, len(tail) + 1))
+    values[tail.index("epsilon")] = 0.25
+    values[tail.index("threshold")] = 0.5
+    _hip.WCA_UPDATE_TAIL.pack_into(packed, _hip.CsWcaUpdateArgs.rows.offset, *values)
+    for name, value in zip(tail, values):
+        assert getattr(packed, name) == value, name
 
 
 def test_decode_refuses_a_small_workspace_without_a_device():
