@@ -284,6 +284,127 @@ __device__ inline void hist_add(int* hist, int bin) {
   if (pending) atomicAdd(&hist[bin], 1);
 }
 
+// One pass of the radix select (8-bit digit at bit `shift`) over keys held
+// in registers: histogram of the available keys under the current prefix
+// (one private copy per wavefront, so waves never contend for a bin, then
+// summed), then the bin where the count from the top reaches the number
+// still needed.
+__device__ inline void radix_pass_regs(const uint64_t kb[kRun], uint32_t av, int shift, int* hist,
+                                       uint64_t& s_prefix, uint64_t& s_mask, int64_t& s_remaining,
+                                       int& s_done) {
+  __shared__ int hw[kSelWaves * 256];
+  const int tid = threadIdx.x, lane = tid & 63;
+  for (int i = tid; i < kSelWaves * 256; i += kSelThreads) hw[i] = 0;
+  __syncthreads();
+  const uint64_t prefix = s_prefix, mask = s_mask;
+  int* mine_hist = hw + (tid >> 6) * 256;
+#pragma unroll
+  for (int j = 0; j < kRun; ++j) {
+    const bool in = ((av >> j) & 1u) && (kb[j] & mask) == prefix;
+    if (in) atomicAdd(&mine_hist[static_cast<int>((kb[j] >> shift) & 255)], 1);
+  }
+  __syncthreads();
+  for (int i = tid; i < 256; i += kSelThreads) {
+    int t = 0;
+#pragma unroll
+    for (int w = 0; w < kSelWaves; ++w) t += hw[w * 256 + i];
+    hist[i] = t;
+  }
+  __syncthreads();
+  if (tid < 64) {
+    // Bins 4*lane .. 4*lane+3; find the bin where the count from the top reaches need.
+    int hb[4], mine = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      hb[q] = hist[4 * lane + q];
+      mine += hb[q];
+    }
+    int above = mine;  // inclusive suffix sum over lanes >= lane
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int t = __shfl_down(above, d, 64);
+      if (lane + d < 64) above += t;
+    }
+    above -= mine;  // lanes strictly above
+    const int64_t need = s_remaining;
+    if (above < need && above + mine >= need) {
+      int64_t cum = above;
+      for (int q = 3; q >= 0; --q) {
+        if (cum + hb[q] >= need) {
+          const int bin = 4 * lane + q;
+          s_remaining = need - cum;
+          s_prefix = prefix | (static_cast<uint64_t>(bin) << shift);
+          s_mask = mask | (255ull << shift);
+          s_done = (need - cum) == hb[q];
+          break;
+        }
+        cum += hb[q];
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// Radix select of the k-th largest key over keys held in registers (one
+// chunk: kb[j] of the tokens with bit j of av set), with s_prefix = s_mask
+// = 0, s_remaining = k and s_done set by the caller and visible.  The bits
+// above the highest bit in which the available keys differ are common to
+// all of them: they enter the prefix at once (one min/max reduction), and
+// the 8-bit passes start below them; the last pass takes bits 0..7.  The
+// result -- threshold under the final mask and the number of keys equal to
+// it still to take -- is the byte-aligned passes' result.
+__device__ inline void radix_select_regs(const uint64_t kb[kRun], uint32_t av, int* hist, uint64_t* wred,
+                                         uint64_t& s_prefix, uint64_t& s_mask, int64_t& s_remaining,
+                                         int& s_done, int& s_start) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  if (s_done) return;
+  uint64_t lo = ~0ull, hi = 0;
+#pragma unroll
+  for (int j = 0; j < kRun; ++j) {
+    if ((av >> j) & 1u) {
+      lo = kb[j] < lo ? kb[j] : lo;
+      hi = kb[j] > hi ? kb[j] : hi;
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const uint64_t l2 = __shfl_xor(lo, off, 64), h2 = __shfl_xor(hi, off, 64);
+    lo = l2 < lo ? l2 : lo;
+    hi = h2 > hi ? h2 : hi;
+  }
+  if (lane == 0) {
+    wred[w] = lo;
+    wred[kSelWaves + w] = hi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    uint64_t a = ~0ull, b = 0;
+    for (int i = 0; i < kSelWaves; ++i) {
+      a = wred[i] < a ? wred[i] : a;
+      b = wred[kSelWaves + i] > b ? wred[kSelWaves + i] : b;
+    }
+    const uint64_t diff = a ^ b;
+    if (diff == 0) {  // every available key is equal: take the lowest-index k
+      s_prefix = b;
+      s_mask = ~0ull;
+      s_done = 1;
+      s_start = 0;
+    } else {
+      const int top = 63 - __clzll(static_cast<long long>(diff));
+      const uint64_t common = top == 63 ? 0ull : ~0ull << (top + 1);
+      s_prefix = b & common;
+      s_mask = common;
+      s_start = top - 7;
+    }
+  }
+  __syncthreads();
+  for (int shift = s_start; !s_done; shift -= 8) {
+    const int sh = shift > 0 ? shift : 0;
+    radix_pass_regs(kb, av, sh, hist, s_prefix, s_mask, s_remaining, s_done);
+    if (sh == 0) break;
+  }
+}
+
 // WCAState._promote, first half: radix select of the k-th largest available
 // key (8-bit digits, most significant first, stopping once the chosen digit's
 // bucket is taken whole), then one pass that marks the taken tokens selected
@@ -297,9 +418,10 @@ __device__ void promote_block(
     const int32_t* abort_flags, int32_t abort_mask) {
   __shared__ int hist[256];
   __shared__ int wave_tot[kSelWaves];
+  __shared__ uint64_t wred[2 * kSelWaves];
   __shared__ uint64_t s_prefix, s_mask;
   __shared__ int64_t s_remaining;
-  __shared__ int s_done;
+  __shared__ int s_done, s_start;
   const int tid = threadIdx.x, lane = tid & 63;
   if (abort_flags && (*abort_flags & abort_mask)) {
     if (tid == 0) *count_out = 0;
@@ -339,8 +461,9 @@ __device__ void promote_block(
     const int64_t s = static_cast<int64_t>(tid) * kRun;
     av = run_mask(candidate, s, n) & ~run_mask(selected, s, n) & ~run_mask(removed, s, n);
     if (s < n) load_key_run(key, s, n, kb);
+    radix_select_regs(kb, av, hist, wred, s_prefix, s_mask, s_remaining, s_done, s_start);
   }
-  for (int pass = 0; pass < 8 && !s_done; ++pass) {
+  for (int pass = 0; pass < 8 && !single && !s_done; ++pass) {
     const int shift = 56 - 8 * pass;
     for (int i = tid; i < 256; i += kSelThreads) hist[i] = 0;
     __syncthreads();
@@ -1312,9 +1435,10 @@ __global__ void __launch_bounds__(kSelThreads) update_finalize_small_kernel(upda
   __shared__ int wave_tot[kSelWaves];
   __shared__ int64_t wave_tot64[kSelWaves];
   __shared__ int hist[256];
+  __shared__ uint64_t wred[2 * kSelWaves];
   __shared__ uint64_t s_prefix, s_mask;
   __shared__ int64_t s_remaining;
-  __shared__ int s_done;
+  __shared__ int s_done, s_start;
   __shared__ uint64_t p_key[kRankMax];  // promoted tokens in index order and their key bits
   __shared__ int32_t p_tok[kRankMax];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1432,49 +1556,7 @@ __global__ void __launch_bounds__(kSelThreads) update_finalize_small_kernel(upda
     __syncthreads();
     uint64_t kb[kRun] = {};
     if (s < n) load_key_run(f.deviation, s, n, kb);
-    for (int pass = 0; pass < 8 && !s_done; ++pass) {
-      const int shift = 56 - 8 * pass;
-      for (int i = tid; i < 256; i += kSelThreads) hist[i] = 0;
-      __syncthreads();
-      const uint64_t prefix = s_prefix, mask = s_mask;
-#pragma unroll
-      for (int j = 0; j < kRun; ++j) {
-        const bool in = ((av >> j) & 1u) && (kb[j] & mask) == prefix;
-        hist_add(hist, in ? static_cast<int>((kb[j] >> shift) & 255) : -1);
-      }
-      __syncthreads();
-      if (tid < 64) {
-        int hb[4], mine = 0;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          hb[q] = hist[4 * lane + q];
-          mine += hb[q];
-        }
-        int above = mine;
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-          const int t = __shfl_down(above, d, 64);
-          if (lane + d < 64) above += t;
-        }
-        above -= mine;
-        const int64_t need = s_remaining;
-        if (above < need && above + mine >= need) {
-          int64_t cum = above;
-          for (int q = 3; q >= 0; --q) {
-            if (cum + hb[q] >= need) {
-              const int bin = 4 * lane + q;
-              s_remaining = need - cum;
-              s_prefix = prefix | (static_cast<uint64_t>(bin) << shift);
-              s_mask = mask | (255ull << shift);
-              s_done = (need - cum) == hb[q];
-              break;
-            }
-            cum += hb[q];
-          }
-        }
-      }
-      __syncthreads();
-    }
+    radix_select_regs(kb, av, hist, wred, s_prefix, s_mask, s_remaining, s_done, s_start);
     const uint64_t thr = s_prefix, mask = s_mask;
     const int64_t need_eq = s_remaining;
     uint32_t gt = 0, eq = 0;
