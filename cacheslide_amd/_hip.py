@@ -90,6 +90,20 @@ class CsWcaUpdateArgs(ctypes.Structure):
     ]
 
 
+class CsWcaInitializeArgs(ctypes.Structure):
+    """cs_wca_initialize_args: one WCAState.initialize in one library call."""
+
+    _fields_ = [
+        ("cached_k", CsView), ("recomputed_k", CsView),
+        ("reused", ctypes.c_void_p), ("mandatory", ctypes.c_void_p), ("n", ctypes.c_int64),
+        ("epsilon", ctypes.c_double), ("fraction", ctypes.c_double), ("clamp", ctypes.c_int32),
+        ("clear_status", ctypes.c_int32), ("err", ctypes.c_void_p), ("norm", ctypes.c_void_p), ("alpha", ctypes.c_void_p),
+        ("candidate", ctypes.c_void_p), ("selected", ctypes.c_void_p), ("removed", ctypes.c_void_p),
+        ("scratch", ctypes.c_void_p), ("promoted", ctypes.c_void_p), ("active", ctypes.c_void_p),
+        ("flags", ctypes.c_void_p), ("counts", ctypes.c_void_p), ("report", ctypes.c_void_p),
+    ]
+
+
 # cs_wca_update_args from ``rows`` to ``report`` as bytes: two pointers, a, n,
 # budget, seventeen pointers, epsilon, threshold, six int32 fields, report
 WCA_UPDATE_TAIL = struct.Struct("<2q3q17q2d6iq")
@@ -203,6 +217,7 @@ SIGNATURES = {
     "cs_rows_gather": (_I32, [_VP, _P, _I64, _VP, _P, _P]),
     "cs_copy_async": (_I32, [_P, _P, _I64, _I32, _P]),
     "cs_wca_update": (_I32, [ctypes.POINTER(CsWcaUpdateArgs), _P]),
+    "cs_wca_initialize": (_I32, [ctypes.POINTER(CsWcaInitializeArgs), _P]),
     "cs_snapshot_convert": (_I32, [_VP, _VP, _I32, _P, _P]),
     "cs_freelist_acquire": (_I32, [_P, _I64, _I64, _P, _P, _P]),
     "cs_wca_score": (_I32, [_VP, _P, _VP, _P, _P, _P, _P]),

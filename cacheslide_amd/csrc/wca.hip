@@ -128,7 +128,7 @@ __global__ void __launch_bounds__(64 * kWaves) wca_score_kernel(dview old_src,
 __global__ void __launch_bounds__(64 * kWaves) wca_score_bf16_kernel(
     const uint16_t* old_base, int64_t old_stride, const int64_t* old_rows,
     const uint16_t* new_base, int64_t new_stride, int64_t n, int64_t words, double* err,
-    double* norm, int32_t* flags) {
+    double* norm, int32_t* flags, int32_t old_bit, int32_t new_bit) {
   const int lane = threadIdx.x & 63;
   const int64_t i = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
   if (i >= n) return;
@@ -136,8 +136,13 @@ __global__ void __launch_bounds__(64 * kWaves) wca_score_bf16_kernel(
   const uint4* o = reinterpret_cast<const uint4*>(old_base + row * old_stride);
   const uint4* f = reinterpret_cast<const uint4*>(new_base + i * new_stride);
   score_acc acc;
+  // with old_bit / new_bit set, the finite checks of both row sets ride on
+  // these loads (cs_check_finite's bits, for callers that read every row)
+  bool bad_o = false, bad_f = false;
   for (int64_t w = lane; w < words; w += 64) {
     const uint4 ov = o[w], fv = f[w];
+    if (old_bit) bad_o |= word_nonfinite<0>(ov);
+    if (new_bit) bad_f |= word_nonfinite<0>(fv);
     const uint32_t ow[4] = {ov.x, ov.y, ov.z, ov.w}, fw[4] = {fv.x, fv.y, fv.z, fv.w};
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -146,6 +151,8 @@ __global__ void __launch_bounds__(64 * kWaves) wca_score_bf16_kernel(
               bf16_to_float(static_cast<uint16_t>(fw[q] >> 16)));
     }
   }
+  const int32_t bits = (__any(bad_o) ? old_bit : 0) | (__any(bad_f) ? new_bit : 0);
+  if (lane == 0 && bits) atomicOr(flags, bits);
   acc.finish(lane, i, err, norm, flags);
 }
 
@@ -1024,7 +1031,7 @@ extern "C" int cs_wca_score(const cs_view* old_rows_src, const int64_t* old_rows
     hipLaunchKernelGGL(wca_score_bf16_kernel, dim3(ceil_div(n, kWaves)), dim3(64 * kWaves), 0,
                        as_stream(stream), static_cast<const uint16_t*>(old_rows_src->data),
                        old_rows_src->stride[0], old_rows, static_cast<const uint16_t*>(fresh->data),
-                       fresh->stride[0], n, fresh->shape[1] * fresh->shape[2] / 8, err, norm, flags);
+                       fresh->stride[0], n, fresh->shape[1] * fresh->shape[2] / 8, err, norm, flags, 0, 0);
   } else {
     hipLaunchKernelGGL(wca_score_kernel, dim3(ceil_div(n, kWaves)), dim3(64 * kWaves), 0,
                        as_stream(stream), to_dview(old_rows_src), old_rows, to_dview(fresh), err,
@@ -1355,6 +1362,35 @@ __global__ void status_clear_kernel(int32_t* flags, int64_t* counts) {
 
 __global__ void status_report_kernel(int64_t* report, int32_t* flags, int64_t* counts, int32_t clear) {
   if (threadIdx.x == 0) write_report(report, flags, counts, clear != 0);
+}
+
+// The status of a one-call initialize: the flags word and five counts.
+__global__ void init_status_clear_kernel(int32_t* flags, int64_t* counts) {
+  if (threadIdx.x == 0) *flags = 0;
+  if (threadIdx.x < 5) counts[threadIdx.x] = 0;
+}
+
+// ... written into the caller's report word, after which the block is
+// zeroed for the next call (every other write to it is ordered before).
+__global__ void init_status_report_kernel(int64_t* report, int32_t* flags, int64_t* counts) {
+  if (threadIdx.x == 0) {
+    report[0] = static_cast<int64_t>(static_cast<uint32_t>(*flags));
+    for (int i = 0; i < 5; ++i) report[1 + i] = counts[i];
+    *flags = 0;
+    for (int i = 0; i < 5; ++i) counts[i] = 0;
+  }
+}
+
+// The promotion of WCAState.initialize with its budget taken on the device
+// from the mask counts (wca.py:177-180): min(ceil(fraction * reused),
+// candidates), written to counts[2]; the promoted count goes to counts[3].
+__global__ void __launch_bounds__(kSelThreads) wca_initial_promote_kernel(
+    const double* key, const uint8_t* candidate, const uint8_t* removed, uint8_t* selected, int64_t n,
+    int64_t* counts, double fraction, int64_t* scratch, const int32_t* abort_flags, int32_t abort_mask) {
+  int64_t budget = static_cast<int64_t>(ceil(fraction * static_cast<double>(counts[0])));
+  if (budget > counts[1]) budget = counts[1];
+  if (threadIdx.x == 0) counts[2] = budget;
+  promote_block(key, candidate, removed, selected, n, budget, scratch, counts + 3, abort_flags, abort_mask);
 }
 
 struct update_final {
@@ -1824,5 +1860,61 @@ extern "C" int cs_wca_update(const cs_wca_update_args* u, void* stream) {
                        u->clear_status & 2);
     CS_LAUNCH_CHECK("wca_update report");
   }
+  return CS_OK;
+}
+
+extern "C" int cs_wca_initialize(const cs_wca_initialize_args* a, void* stream) {
+  CS_REQUIRE(a && a->flags && a->counts && a->report, "null arguments");
+  const int64_t n = a->n;
+  CS_REQUIRE(n >= 0 && n <= (1ll << 24), "at most 2^24 tokens");
+  CS_REQUIRE(n == 0 || (a->reused && a->mandatory && a->err && a->norm && a->alpha && a->candidate &&
+                        a->selected && a->removed && a->scratch && a->promoted && a->active),
+             "null arguments");
+  CS_REQUIRE(a->cached_k.ndim == 3 && a->recomputed_k.ndim == 3 && a->cached_k.shape[0] == n &&
+                 a->recomputed_k.shape[0] == n,
+             "K views must be [n, H, D]");
+  hipStream_t s = as_stream(stream);
+  int32_t* f = a->flags;
+  int st;
+  if (a->clear_status & 1) {
+    hipLaunchKernelGGL(init_status_clear_kernel, dim3(1), dim3(64), 0, s, f, a->counts);
+    CS_LAUNCH_CHECK("wca_initialize status");
+  }
+#define CS_STEP(expr) \
+  do {                \
+    st = (expr);      \
+    if (st != CS_OK) return st; \
+  } while (0)
+  const cs_view& ck = a->cached_k;
+  const cs_view& rk = a->recomputed_k;
+  if (bf16_rows16(&ck) && bf16_rows16(&rk) && ck.shape[1] == rk.shape[1] && ck.shape[2] == rk.shape[2]) {
+    // the score reads every row of both: the finite checks ride on its loads
+    if (n > 0) {
+      hipLaunchKernelGGL(wca_score_bf16_kernel, dim3(ceil_div(n, kWaves)), dim3(64 * kWaves), 0, s,
+                         static_cast<const uint16_t*>(ck.data), ck.stride[0], nullptr,
+                         static_cast<const uint16_t*>(rk.data), rk.stride[0], n, rk.shape[1] * rk.shape[2] / 8,
+                         a->err, a->norm, f, 1 << 20, 1 << 21);
+      CS_LAUNCH_CHECK("wca_initialize score");
+    }
+  } else {
+    CS_STEP(cs_check_finite(&ck, 1 << 20, f, stream));
+    CS_STEP(cs_check_finite(&rk, 1 << 21, f, stream));
+    CS_STEP(cs_wca_score(&ck, nullptr, &rk, a->err, a->norm, f, stream));
+  }
+  CS_STEP(cs_wca_init_masks(a->err, a->reused, a->mandatory, n, a->candidate, a->counts, f, stream));
+  CS_STEP(cs_wca_alpha(a->err, a->norm, n, a->epsilon, a->clamp, a->alpha, f, stream));
+  if (n > 0) {
+    const int32_t abort = (1 << 20) | (1 << 21) | 2 | 4 | 16 | 32;
+    hipLaunchKernelGGL(wca_initial_promote_kernel, dim3(1), dim3(kSelThreads), 0, s, a->err, a->candidate,
+                       a->removed, a->selected, n, a->counts, a->fraction, a->scratch, f, abort);
+    // the budget is on the device: n bounds the promoted count
+    hipLaunchKernelGGL(wca_promote_order_kernel, dim3(ceil_div(n, 64)), dim3(64 * kOrderSlices), 0, s, a->scratch,
+                       n, a->counts + 3, a->promoted, int64_t(0));
+    CS_LAUNCH_CHECK("wca_initialize promote");
+  }
+  CS_STEP(cs_mask_nonzero(a->selected, a->mandatory, n, a->active, a->counts + 4, stream));
+#undef CS_STEP
+  hipLaunchKernelGGL(init_status_report_kernel, dim3(1), dim3(64), 0, s, a->report, f, a->counts);
+  CS_LAUNCH_CHECK("wca_initialize report");
   return CS_OK;
 }

@@ -11,6 +11,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import threading
 from dataclasses import dataclass, field
 
 import torch
@@ -125,6 +126,54 @@ def _update_steps(computed: bool) -> tuple[list, int]:
             mask |= bits
         _UPDATE_STEPS[computed] = (steps, mask)
     return _UPDATE_STEPS[computed]
+
+
+# the one-call initialize's checks in the order the checked path registers them
+_INIT_STEPS = (
+    (1 << 20, WCANumericalError, "cached_k must have finite values"),
+    (1 << 21, WCANumericalError, "recomputed_k must have finite values"),
+    (2, WCANumericalError, "squared deviation overflowed float64"),
+    (32, ValueError, "every dynamic/non-reused token must be mandatory"),
+    (2 | 16, WCANumericalError, "adaptation weight overflowed float64"),
+    (4, WCANumericalError, "adaptation weight overflowed; inspect the K magnitudes"),
+)
+_INIT_CK = _hip.CsWcaInitializeArgs.cached_k.offset
+_INIT_RK = _hip.CsWcaInitializeArgs.recomputed_k.offset
+
+
+_INIT_STATUS = threading.local()
+
+
+def _init_status(device) -> list:
+    """This thread's status block for one-call initializes on ``device``:
+    [device int64[6] block, pinned host int64[6] report, dirty].  The call's
+    last kernel zeroes the block, so only a new block or one left by a call
+    that returned an error is cleared by the next call."""
+    table = getattr(_INIT_STATUS, "table", None)
+    if table is None:
+        table = _INIT_STATUS.table = {}
+    status = table.get(device)
+    if status is None:
+        status = table[device] = [torch.empty(6, dtype=torch.int64, device=device),
+                                  torch.empty(6, dtype=torch.int64, pin_memory=True), True]
+    return status
+
+
+def _initialize_inputs_pass(cached_k, recomputed_k, reused_mask, mandatory_mask) -> bool:
+    """True when none of initialize's host-side checks (_kv, _matching, _mask) would raise,
+    for a request of 1 .. 2^24 tokens."""
+    if not all(isinstance(t, Tensor) for t in (cached_k, recomputed_k, reused_mask, mandatory_mask)):
+        return False
+    if cached_k.ndim != 3 or not cached_k.is_floating_point() or min(cached_k.shape[1:]) < 1:
+        return False
+    n = cached_k.shape[0]
+    if not 0 < n <= 1 << 24:
+        return False
+    if (recomputed_k.shape, recomputed_k.dtype, recomputed_k.device) != (cached_k.shape, cached_k.dtype,
+                                                                       cached_k.device):
+        return False
+    return all(m.shape == (n,) and m.dtype == torch.bool and m.device == cached_k.device and m.is_contiguous()
+               for m in (reused_mask, mandatory_mask))
 
 
 # byte offsets of the per-call fields of cs_wca_update_args
@@ -294,6 +343,8 @@ class WCAState:
     ) -> "WCAState":
         config = config or WCAConfig()
         device = _hip.require_device(cached_k)
+        if _initialize_inputs_pass(cached_k, recomputed_k, reused_mask, mandatory_mask):
+            return cls._initialize_device(cached_k, recomputed_k, reused_mask, mandatory_mask, config, device)
         fl = _Flags(device, 2)
         _kv("cached_k", cached_k, fl)
         _matching("recomputed_k", recomputed_k, cached_k.shape, cached_k, fl)
@@ -306,8 +357,9 @@ class WCAState:
         except ValueError as error:
             fl.finish(error)
         candidate = torch.empty(n, dtype=torch.bool, device=device)
-        call("cs_wca_init_masks", ptr(err), ptr(reused_mask), ptr(mandatory_mask), n,
-             ptr(candidate), fl.counter(0), fl.ptr, fl.stream)
+        # the kernels read the masks as contiguous bytes
+        call("cs_wca_init_masks", ptr(err), ptr(reused_mask.contiguous()), ptr(mandatory_mask.contiguous()),
+             n, ptr(candidate), fl.counter(0), fl.ptr, fl.stream)
         fl.step(32, ValueError, "every dynamic/non-reused token must be mandatory")
         alpha = _alpha(err, norm, config.epsilon, config.clamp_alpha, fl)
         fl.finish(read=True)
@@ -325,6 +377,59 @@ class WCAState:
             budget=budget,
         )
         state._promote()
+        return state
+
+    @classmethod
+    def _initialize_device(cls, cached_k, recomputed_k, reused_mask, mandatory_mask, config,
+                           device) -> "WCAState":
+        """The launches of the checked initialize and _promote in one
+        cs_wca_initialize call (the budget taken on the device), one readback."""
+        n = cached_k.shape[0]
+        err = torch.empty(n, dtype=torch.float64, device=device)
+        norm = torch.empty(n, dtype=torch.float64, device=device)
+        alpha = torch.empty(n, dtype=torch.float64, device=device)
+        candidate = torch.empty(n, dtype=torch.bool, device=device)
+        zeroed = torch.zeros(2 * n, dtype=torch.bool, device=device)  # selected, removed
+        selected, removed = zeroed[:n], zeroed[n:]
+        ibuf = torch.empty(4 * n, dtype=torch.long, device=device)  # scratch 2n, promoted, active
+        status = _init_status(device)
+        block, host = status[0], status[1]
+        a = _hip.CsWcaInitializeArgs()
+        _hip.pack_view3(a, _INIT_CK, cached_k)
+        _hip.pack_view3(a, _INIT_RK, recomputed_k)
+        ib, sp = ibuf.data_ptr(), block.data_ptr()
+        a.reused, a.mandatory, a.n = reused_mask.data_ptr(), mandatory_mask.data_ptr(), n
+        a.epsilon, a.fraction = float(config.epsilon), float(config.correction_fraction)
+        a.clamp = 1 if config.clamp_alpha else 0
+        a.err, a.norm, a.alpha = err.data_ptr(), norm.data_ptr(), alpha.data_ptr()
+        a.candidate, a.selected, a.removed = candidate.data_ptr(), selected.data_ptr(), removed.data_ptr()
+        a.scratch, a.promoted, a.active = ib, ib + 16 * n, ib + 24 * n
+        a.flags, a.counts, a.report = sp, sp + 8, host.data_ptr()
+        a.clear_status = 1 if status[2] else 0
+        status[2] = True
+        call("cs_wca_initialize", ctypes.byref(a), _hip.stream_of(device))
+        status[2] = False  # the call's last kernel leaves the block zeroed
+        # the state's own mask copies, queued while the device works
+        reused_copy, mandatory_copy = reused_mask.clone(), mandatory_mask.clone()
+        torch.cuda.current_stream(device).synchronize()
+        words = host.tolist()
+        value = words[0] & 0xFFFFFFFF
+        for bits, exc, message in _INIT_STEPS:
+            if value & bits:
+                raise exc(message)
+        budget, n_active = words[3], words[5]
+        state = cls(
+            config=config,
+            reused_mask=reused_copy,
+            mandatory_mask=mandatory_copy,
+            initial_deviation=err,
+            candidate_mask=candidate,
+            selected_mask=selected,
+            removed_mask=removed,
+            alpha=alpha,
+            budget=budget,
+        )
+        state._cache_active(ibuf[3 * n:3 * n + n_active], n_active)
         return state
 
     def _mask_key(self) -> tuple:

@@ -499,6 +499,45 @@ typedef struct cs_wca_update_args {
 
 int cs_wca_update(const cs_wca_update_args* u, void* stream);
 
+/* WCAState.initialize (wca.py:151-199, with _promote at wca.py:202-215) in a
+ * single call, for callers that have already made the host-side checks
+ * (floating [n, H, D] K views of equal shape, dtype and device; bool masks
+ * [n]): cs_check_finite of cached K (1<<20) and recomputed K (1<<21) --
+ * for bf16 rows with contiguous heads on the score's own loads --,
+ * cs_wca_score (2), cs_wca_init_masks (32; counts[0] = reused tokens,
+ * counts[1] = candidates), cs_wca_alpha (2|16, 4), then the budget
+ * min(ceil(fraction * counts[0]), counts[1]) into counts[2] on the device,
+ * the promotion (counts[3], order in promoted[]) and cs_mask_nonzero of
+ * selected | mandatory (counts[4]).  The promotion does nothing when any of
+ * those bits fired.  Its last kernel copies flags and counts[5] into report
+ * (host-visible int64[6]: flags word, then counts[0..4]; read it after
+ * synchronizing the stream) and then zeroes them, so a block kept from call
+ * to call needs clearing (clear_status bit 0: zeroed by the call first) only
+ * when new or after a call that returned an error. */
+typedef struct cs_wca_initialize_args {
+  cs_view cached_k, recomputed_k;
+  const uint8_t* reused;     /* [n] */
+  const uint8_t* mandatory;  /* [n] */
+  int64_t n;
+  double epsilon, fraction;
+  int32_t clamp;
+  int32_t clear_status;      /* bit 0: zero flags and counts first */
+  double* err;               /* out [n] */
+  double* norm;              /* out [n] */
+  double* alpha;             /* out [n] */
+  uint8_t* candidate;        /* out [n] */
+  uint8_t* selected;         /* [n], zero on entry */
+  const uint8_t* removed;    /* [n], zero */
+  int64_t* scratch;          /* work [2n] */
+  int64_t* promoted;         /* out [n] */
+  int64_t* active;           /* out [n] */
+  int32_t* flags;            /* status word */
+  int64_t* counts;           /* [5] */
+  int64_t* report;           /* host-visible int64[6] */
+} cs_wca_initialize_args;
+
+int cs_wca_initialize(const cs_wca_initialize_args* a, void* stream);
+
 /* ------------------------------------------------------------------------ *
  * Row bookkeeping of the selective prefill (runtime.py:408-456).  Row views
  * are [rows, H] with contiguous H; rows move bit for bit (any dtype).  Token

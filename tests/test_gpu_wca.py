@@ -385,3 +385,74 @@ def test_fused_update_checks_raise_in_reference_order(device):
         assert state.last_layer == 1
     result = state.update(2, cached, cached, rk, rv, computed_indices=rows.clone())
     assert result.fused_k.shape == rk.shape and state.last_layer == 2
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("n,fraction", [(1, 0.15), (700, 0.15), (5000, 0.5), (16384, 0.15), (20000, 0.3)])
+def test_single_call_initialize_equals_checked_initialize(device, monkeypatch, dtype, n, fraction):
+    """initialize makes its device work one cs_wca_initialize call (budget on
+    the device, one readback) when the host checks pass; every field of the
+    state equals the step-by-step path's, bit for bit."""
+    import cacheslide_amd.wca as wca_mod
+
+    gen = torch.Generator().manual_seed(n)
+    cached = torch.randn(n, 2, 16, generator=gen).to(dtype)
+    fresh = (cached.float() + 0.05 * torch.randn(n, 2, 16, generator=gen)).to(dtype)
+    fresh[: n // 7] = cached[: n // 7]  # zero deviations: not candidates
+    cached, fresh = cached.to(device), fresh.to(device)
+    reused = torch.rand(n, generator=gen).to(device) < 0.97
+    config = WCAConfig(correction_fraction=fraction, clamp_alpha=n % 2 == 0)
+    calls = []
+    real = wca_mod.call
+
+    def spy(name, *args):
+        calls.append(name)
+        return real(name, *args)
+
+    monkeypatch.setattr(wca_mod, "call", spy)
+    fast = WCAState.initialize(cached, fresh, reused, ~reused, config)
+    assert calls == ["cs_wca_initialize"]
+    monkeypatch.setattr(wca_mod, "_initialize_inputs_pass", lambda *a: False)
+    slow = WCAState.initialize(cached, fresh, reused, ~reused, config)
+    assert "cs_wca_initialize" not in calls[1:]
+    assert fast.budget == slow.budget
+    for name in ("initial_deviation", "alpha", "candidate_mask", "selected_mask", "removed_mask",
+                 "reused_mask", "mandatory_mask"):
+        a, b = getattr(fast, name), getattr(slow, name)
+        assert a.dtype == b.dtype and a.shape == b.shape, name
+        if a.dtype == torch.float64:
+            assert torch.equal(a.view(torch.int64), b.view(torch.int64)), name
+        else:
+            assert torch.equal(a, b), name
+    assert torch.equal(fast.active_indices, slow.active_indices)
+    # and the states continue alike
+    idx = fast.active_indices
+    u1 = fast.update(2, cached, cached, fresh[idx], fresh[idx])
+    u2 = slow.update(2, cached, cached, fresh[idx], fresh[idx])
+    assert torch.equal(u1.next_indices, u2.next_indices) and torch.equal(u1.fused_k, u2.fused_k)
+
+
+def test_single_call_initialize_raises_in_reference_order(device):
+    """The one-call initialize raises the checked path's first error."""
+    cached = torch.randn(300, 2, 16, device=device)
+    fresh = cached + 0.1
+    reused = torch.ones(300, dtype=torch.bool, device=device)
+    reused[-1] = False
+    bad = cached.clone()
+    bad[5, 1, 3] = float("nan")
+    with pytest.raises(WCANumericalError, match="cached_k must have finite values"):
+        WCAState.initialize(bad, fresh, reused, ~reused)
+    with pytest.raises(WCANumericalError, match="recomputed_k must have finite values"):
+        WCAState.initialize(cached, bad, reused, ~reused)
+    # NaN in cached K and a token neither reused nor mandatory: the finite check first
+    none = torch.zeros(300, dtype=torch.bool, device=device)
+    with pytest.raises(WCANumericalError, match="cached_k must have finite values"):
+        WCAState.initialize(bad, fresh, reused, none)
+    with pytest.raises(ValueError, match="mandatory"):
+        WCAState.initialize(cached, fresh, reused, none)
+    huge = torch.full((4, 1, 1), 1e308, dtype=torch.float64, device=device)
+    with pytest.raises(WCANumericalError, match="deviation overflow"):
+        WCAState.initialize(torch.zeros_like(huge), huge, reused[:4], ~reused[:4])
+    state = WCAState.initialize(cached, fresh, reused, ~reused)
+    # ceil(0.26 * 299) = 78 of 299 candidates, plus the mandatory token
+    assert state.budget == 78 and state.active_indices.numel() == 79
