@@ -570,14 +570,15 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
     // key v of the tile (8 (v/4) + 4h + v%4) is visible to the column when
     // 8 (v/4) + v%4 <= lim
     const int lim = (qp32 < kend32 - 1 ? qp32 : kend32 - 1) - base - 4 * h;
-    // s holds the raw scores minus m_base
-    if (__all(carry >= top)) {
-      if (need_mask) {
+    // s holds the raw scores minus m_base; the causal mask first, for both
+    // paths (a masked score stays -inf through the bias, and its gate is
+    // dropped by the visibility test below)
+    if (need_mask) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v)
-          if (8 * (v >> 2) + (v & 3) > lim) s[v] = -INFINITY;
-      }
-    } else {
+      for (int v = 0; v < 16; ++v)
+        if (8 * (v >> 2) + (v & 3) > lim) s[v] = -INFINITY;
+    }
+    if (!__all(carry >= top)) {
       const float gate_off = -m_base * (kInvSqrtD * kLog2e);
       // gates; runs of 4 keys (8 j4 + 4h + 0..3) and their in-run suffix sums
       float gsuf[16], run[4];
@@ -592,7 +593,6 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
           const float e = __builtin_amdgcn_exp2f(fmaf(s[v], -kInvSqrtD * kLog2e, gate_off));
           acc += ok ? __builtin_amdgcn_rcpf(1.f + e) : 0.f;
           gsuf[v] = acc;
-          s[v] = ok ? s[v] : -INFINITY;
         }
         run[j4] = acc;
       }
