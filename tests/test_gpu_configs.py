@@ -12,7 +12,9 @@ untouched memory).
 * SLIDE: one relocation step on 32 layers x [100000 blocks, 8, 16, 256] bf16,
   512 chunks of 64..2048 tokens;
 * WCA: one request's 32-layer trajectory at T = 16384, fraction 0.15,
-  gate every 4 layers, threshold 0.12, paper_cosine_lt.
+  gate every 4 layers, threshold 0.12, paper_cosine_lt;
+* the reuse call: 16384 keys, 2676 active rows, 32q/8kv heads, strict
+  canonical profile, against the generic kernel.
 
 Inputs are drawn on the device from seeded generators; the oracle reads the
 same bits copied back to the host.
@@ -243,3 +245,64 @@ def test_slide_relocation_step_32x100k_bit_exact(device):
     np.testing.assert_array_equal(free.acquire(1000).cpu().numpy(), want)
     del cache, bits, words, part_before
     torch.cuda.empty_cache()
+
+
+def test_reuse_call_16k_mfma_path_matches_generic_kernel(device, monkeypatch):
+    """The reuse call (runtime.py:576-609) at its benchmark workload: 16384
+    keys (8 reused chunks x 2016 + 256 recomputed), 2420 selected fixed rows
+    and the 256 recomputed rows, 32q/8kv x 128, bf16, P = 64, a strict
+    canonical profile [32, 16128, 16128] fp32 (a head-broadcast view of one
+    calibration-like path, 0.5 per token), updated_and_self visibility.  The
+    MFMA policy path (attention kernel and the checker beside it) equals the
+    generic kernel -- itself checked against the oracle -- within the bf16
+    tolerance, every output is finite, and the generic kernel ran only for
+    the reference call (explicit key coordinates)."""
+    import math
+
+    import cacheslide_amd.position as position_module
+    from cacheslide_amd import (CCPEProfile, CanonicalPositionPolicy, ChunkIdentity, RequestPlan,
+                                SelectedAssociationPolicy, cope_attention)
+
+    CH, CHUNKS, DYN, HQ, HKV, D, P = 2016, 8, 256, 32, 8, 128, 64
+    F = CH * CHUNKS
+    n = F + DYN
+    spec = [{"id": f"C{i}", "role": "reuse", "start": i * CH, "end": (i + 1) * CH} for i in range(CHUNKS)]
+    spec.append({"id": "question", "role": "recompute", "start": F, "end": n})
+    plan = RequestPlan.parse({"version": 1, "namespace": "test", "task_id": "reuse", "operation": "reuse",
+                              "chunks": spec}, [(7 * i) % 32000 for i in range(n)])
+    gen = torch.Generator(device=device).manual_seed(6106)
+    q_all = torch.randn((n, HQ, D), generator=gen, device=device).to(torch.bfloat16)
+    k = torch.randn((n, HKV, D), generator=gen, device=device).to(torch.bfloat16)
+    v = torch.randn((n, HKV, D), generator=gen, device=device).to(torch.bfloat16)
+    cope = CoPE(D, P, device=device)
+    with torch.no_grad():
+        cope.position_embeddings.copy_(torch.randn((D, P), generator=torch.Generator().manual_seed(61)) * 0.1)
+    sel = torch.randperm(F, generator=torch.Generator().manual_seed(62))[:math.ceil(0.15 * F)].sort().values
+    rows = torch.cat([sel, torch.arange(F, n)]).to(device)
+    ords = torch.arange(F, device=device, dtype=torch.float32)
+    path = ((ords[:, None] - ords[None, :] + 1) * 0.5).clamp_(0, P - 1)
+    path.masked_fill_(ords[None, :] > ords[:, None], 0.0)
+    profile = CCPEProfile(trained_profile_version="v1", checkpoint_id="ckpt",
+                          chunks=tuple(ChunkIdentity(*c) for c in plan.fixed_layout),
+                          query_positions=torch.arange(F), key_positions=torch.arange(F),
+                          canonical_positions=path.expand(HQ, F, F), max_positions=P, histogram_bin_width=0.25,
+                          sample_count=1)
+    policy = CanonicalPositionPolicy(plan, profile, "ckpt", mode="strict_contextual")
+    visibility = SelectedAssociationPolicy(plan.fixed_indices, sel.to(device))
+    q = q_all[rows].contiguous()
+    called = []
+    real = position_module.call
+
+    def spy(name, *args):
+        called.append(name)
+        return real(name, *args)
+
+    monkeypatch.setattr(position_module, "call", spy)
+    fast = cope_attention(q, k, v, cope, rows, None, positions_transform=policy, visibility_transform=visibility,
+                          query_chunk_size=64)
+    assert "cs_ccpe_attention" not in called, called
+    ref = cope_attention(q, k, v, cope, rows, torch.arange(n, device=device), positions_transform=policy,
+                         visibility_transform=visibility, query_chunk_size=64)
+    assert "cs_ccpe_attention" in called
+    assert fast.shape == (rows.numel(), HQ, D) and bool(torch.isfinite(fast.float()).all())
+    assert_close_bf16(fast, ref.float().cpu().numpy())
