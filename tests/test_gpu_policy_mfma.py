@@ -104,6 +104,9 @@ def compare(expected, actual):
 
 
 BIG = dict(a=700, dyn=150, b=900, n_sel=60)
+# 724 fixed tokens: the profile [8, 724, 724] holds 4193408 cells, at the
+# reference's max_profile_elements budget of 4194304 (config.py:19)
+BUDGET = dict(a=360, dyn=100, b=364, n_sel=80)
 SMALL = dict(a=40, dyn=30, b=60, n_sel=50)   # positions never saturate: the boundary pairs decide
 
 CASES = {
@@ -120,6 +123,9 @@ CASES = {
     "boundary_gap_strict": (SMALL, 20, 8, 0.0, 0, "strict_contextual", 16, "error"),
     "boundary_order_strict": (SMALL, 20, 4, 0.0, 0, "strict_contextual", 16, "error"),
     "boundary_mixed": (SMALL, 20, 8, 0.0, 0, "mixed_bias_override", 16, "ok"),
+    "budget_strict": (BUDGET, 30, 0, 0.0, 0, "strict_contextual", 64, "ok"),
+    "budget_shifted_mixed": (BUDGET, 31, 16, 0.0, 0, "mixed_bias_override", 64, "ok"),
+    "budget_perturbed_strict": (BUDGET, 32, 0, 0.05, 0, "strict_contextual", 64, "error"),
 }
 
 
@@ -132,6 +138,8 @@ def test_mfma_policy_call_matches_oracle(device, monkeypatch, name):
     q, k, v, e, rows, plan, canonical, ordinals, sel = scenario(seed, shift=shift, perturb=perturb, drop=drop,
                                                                 **layout)
     strict = mode == "strict_contextual"
+    if layout is BUDGET:
+        assert 0.99 * 4_194_304 < canonical.size <= 4_194_304
     expected = oracle_run(q, k, v, e, rows, plan, canonical, ordinals, strict, sel, chunk)
     assert expected[0] == want, expected[:3] if expected[0] == "error" else "ok"
     actual, called = device_run(q, k, v, e, rows, plan, profile_for(plan, canonical, ordinals), mode, sel, chunk,
