@@ -11,6 +11,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import struct
 import threading
 from dataclasses import dataclass, field
 
@@ -180,6 +181,12 @@ def _initialize_inputs_pass(cached_k, recomputed_k, reused_mask, mandatory_mask)
 _CK, _CV, _RK, _RV, _FK, _FV = (getattr(_hip.CsWcaUpdateArgs, f).offset for f in (
     "cached_k", "cached_v", "recomputed_k", "recomputed_v", "fused_k", "fused_v"))
 _TAIL = _hip.CsWcaUpdateArgs.rows.offset
+# the whole cs_wca_update_args block in one pack: six 3-d views, then the tail
+_VIEW3 = "qii3q3x3q3x".replace("3x", "24x")
+_UPDATE_ALL = struct.Struct("<" + _VIEW3 * 6 + _hip.WCA_UPDATE_TAIL.format.lstrip("<"))
+assert (_CK, _CV, _RK, _RV, _FK, _FV) == tuple(i * _hip._VIEW.size for i in range(6))
+assert _TAIL == 6 * _hip._VIEW.size
+assert _UPDATE_ALL.size == ctypes.sizeof(_hip.CsWcaUpdateArgs)
 
 
 def _matching(name: str, tensor: Tensor, reference_shape, reference: Tensor, fl: _Flags,
@@ -565,11 +572,18 @@ class WCAState:
         u = self._update_args
         if u is None:
             u = self._update_args = _hip.CsWcaUpdateArgs()
-        # the six views, then every field from rows to report in one pack
-        for field, tensor in ((_CK, cached_k), (_CV, cached_v), (_RK, recomputed_k), (_RV, recomputed_v),
-                              (_FK, fused_k), (_FV, fused_v)):
-            _hip.pack_view3(u, field, tensor)
+        # the six views and every field from rows to report in one pack; the
+        # fused outputs are the two halves of the contiguous [2, a, H, D] block
         config = self.config
+        code = _hip.dtype_code(cached_k.dtype)
+        _, hh, dd = cached_k.shape
+        views = []
+        for tensor in (cached_k, cached_v, recomputed_k, recomputed_v):
+            s0, s1, s2 = tensor.shape
+            views += (tensor.data_ptr() if s0 * s1 * s2 else 0, code, 3, s0, s1, s2, *tensor.stride())
+        fk = fused.data_ptr() if a * hh * dd else 0
+        fv = fk + a * hh * dd * fused.element_size() if fk else 0
+        views += (fk, code, 3, a, hh, dd, hh * dd, dd, 1, fv, code, 3, a, hh, dd, hh * dd, dd, 1)
         base = work.data_ptr()
         flags = block.data_ptr()
         # the per-token state (NULL for a request without tokens)
@@ -577,8 +591,8 @@ class WCAState:
                  self.candidate_mask.data_ptr(), self.removed_mask.data_ptr(),
                  self.mandatory_mask.data_ptr(), scratch.data_ptr()) if n else (0,) * 7
         # clear_status bit 1: the call leaves the block zeroed; bit 0 also zeroes it first
-        _hip.WCA_UPDATE_TAIL.pack_into(
-            u, _TAIL, indices.data_ptr() if a else 0, computed.data_ptr() if computed is not None and a else 0,
+        _UPDATE_ALL.pack_into(
+            u, 0, *views, indices.data_ptr() if a else 0, computed.data_ptr() if computed is not None and a else 0,
             a, n, self.budget, *state[:6], base, base + 8 * n, base + 16 * n, base + 24 * n,
             ib, ib + 8 * (a + 2 * m) if gate else 0, ib + 8 * a, state[6], ib + 8 * (a + m),
             flags, flags + 8, float(config.epsilon), float(config.convergence_threshold),
