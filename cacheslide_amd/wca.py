@@ -542,14 +542,20 @@ class WCAState:
     def _status(self, device) -> tuple:
         """The one-call update's status: a device int64[4] block (flags word,
         three counts) that cs_wca_update zeroes again after its last kernel
-        has copied it into the pinned host mirror, and the launch stream."""
+        has copied it into the pinned host mirror, and the launch stream: the
+        caller's current stream at this call (kept while it stays current)."""
+        raw = torch._C._cuda_getCurrentRawStream(device.index)
         status = self._status_block
         if status is None or status[0].device != device:
             block = torch.zeros(4, dtype=torch.int64, device=device)
             host = torch.zeros(4, dtype=torch.int64, pin_memory=True)
             status = self._status_block = (block, host, _hip.stream_of(device),
-                                           torch.cuda.current_stream(device))
+                                           torch.cuda.current_stream(device), raw)
             self._status_dirty = True
+        elif status[4] != raw:
+            # the block was left zeroed by the last call, which was waited for
+            status = self._status_block = (status[0], status[1], _hip.stream_of(device),
+                                           torch.cuda.current_stream(device), raw)
         return status
 
     def _update_device(self, layer_index, device, cached_k, cached_v, recomputed_k, recomputed_v,
@@ -557,7 +563,7 @@ class WCAState:
         """The launches of _update_checked in one cs_wca_update call, with its checks registered."""
         indices = self.active_indices
         a, n = indices.numel(), self.selected_mask.numel()
-        block, host, stream, torch_stream = self._status(device)
+        block, host, stream, torch_stream, _ = self._status(device)
         work, scratch = self._workspace()
         gate = layer_index % self.config.gate_interval == 0 and a > 0
         # fresh outputs in two allocations: fused K and V; the index lists and the weights used

@@ -342,6 +342,32 @@ def test_single_call_update_equals_checked_update(device, weight_update, mode, d
     assert fast.last_layer == before[2]
 
 
+def test_single_call_update_follows_the_current_stream(device):
+    """Each update launches on the caller's current stream at that call: inputs
+    produced on a side stream just before the update are read complete."""
+    gen = torch.Generator().manual_seed(91)
+    T, H, D = 4096, 8, 128
+    fresh = torch.randn(T, H, D, generator=gen).to(torch.bfloat16).to(device)
+    cached = (fresh.float() + 0.05).to(torch.bfloat16)
+    reused = torch.ones(T, dtype=torch.bool, device=device)
+    config = WCAConfig(gate_interval=2)
+    fast = WCAState.initialize(cached, fresh, reused, ~reused, config)
+    slow = WCAState.initialize(cached, fresh, reused, ~reused, config)
+    side = torch.cuda.Stream(device)
+    for layer in range(2, 6):
+        rows = fast.active_indices
+        stream = side if layer % 2 else torch.cuda.current_stream(device)
+        with torch.cuda.stream(stream):
+            # produced on the stream the update then runs on
+            big = (fresh.float() * (1 + 0.01 * layer)).to(torch.bfloat16)
+            rk, rv = big[rows], (2 * big)[rows]
+            a = fast.update(layer, cached, cached, rk, rv)
+            b = slow._update_checked(layer, device, cached, cached, rk, rv, None)
+        torch.cuda.synchronize(device)
+        for name in ("fused_k", "fused_v", "alpha", "removed_indices", "promoted_indices", "next_indices"):
+            assert torch.equal(getattr(a, name), getattr(b, name)), (layer, name)
+
+
 def test_fused_update_checks_raise_in_reference_order(device):
     """The single-launch checks of cached K/V, the computed rows and recomputed
     K/V raise their own errors, the first in the reference's order when several
