@@ -161,6 +161,7 @@ class CsKvSource(ctypes.Structure):
         ("side_s_row", ctypes.c_int64),
         ("side_s_head", ctypes.c_int64),
         ("side_rows", ctypes.c_int64),
+        ("slots_cols", ctypes.c_int64),
     ]
 
 

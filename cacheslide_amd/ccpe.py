@@ -74,6 +74,7 @@ def _slot_source(cache: Tensor, slots: Tensor, side_k: Tensor | None,
         raise ValueError("slots must be int64 [batch, tokens] with contiguous rows")
     src.slots = slots.data_ptr()
     src.slots_stride = slots.stride(0)
+    src.slots_cols = slots.shape[1]
     if (side_k is None) != (side_v is None):
         raise ValueError("side_k and side_v go together")
     if side_k is not None:

@@ -66,7 +66,7 @@ struct kv_addr {
   const uint16_t* v;
   int64_t k_sb, k_st, k_sh, v_sb, v_st, v_sh;
   const int64_t* slots;  // per-token slot map (replaces the block table)
-  int64_t slots_stride;
+  int64_t slots_stride, slots_cols;
   int64_t native_slots;  // num_blocks * block_size
   const uint16_t* side_k;
   const uint16_t* side_v;
@@ -124,8 +124,17 @@ struct split_ctx {
   int64_t lo, hi;
 };
 
-__device__ inline bool make_ctx(const decode_params& p, int b, int kvh, int r, split_ctx& c) {
+// Keys the call may read for request b: its context length, clamped to
+// max_nk.  A longer context is flagged (CS_FLAG_CONTEXT_RANGE) and its output
+// row is not valid, but every read stays inside the [B, max_nk] slot map and
+// the max_nk keys the caller sized its K/V for.
+__device__ inline int keys_of(const decode_params& p, int b) {
   const int nk = p.nk[b];
+  return nk < p.max_nk ? nk : p.max_nk;
+}
+
+__device__ inline bool make_ctx(const decode_params& p, int b, int kvh, int r, split_ctx& c) {
+  const int nk = keys_of(p, b);
   int splits = (nk + p.split - 1) / p.split;
   if (splits > p.smax) splits = p.smax;  // the workspace holds smax splits
   if (r >= splits) return false;
@@ -203,7 +212,7 @@ __device__ void load_offsets(const decode_params& p, smem_t<G>& s, const split_c
     const int64_t sk = p.kv.side_k ? p.kv.side_k - p.kv.cache : 0;
     const int64_t sv = p.kv.side_v ? p.kv.side_v - p.kv.cache : 0;
     for (int i = threadIdx.x; i < n; i += kThreads) {
-      const int64_t slot = row[c.lo + i];
+      const int64_t slot = c.lo + i < p.kv.slots_cols ? row[c.lo + i] : -1;
       int64_t kr = zk, vr = zk + kD;
       if (slot >= 0 && slot < p.kv.native_slots) {
         const int64_t blk = p.kv.bs_shift >= 0 ? (slot >> p.kv.bs_shift) : slot / p.kv.block_size;
@@ -843,7 +852,7 @@ __global__ void __launch_bounds__(kThreads) decode_finish_kernel(decode_params p
   __shared__ smem_t<G> s;
   const int b = blockIdx.x / p.hkv, kvh = blockIdx.x % p.hkv;
   const int h0 = kvh * G;
-  int splits = (p.nk[b] + p.split - 1) / p.split;
+  int splits = (keys_of(p, b) + p.split - 1) / p.split;
   if (splits > p.smax) splits = p.smax;
   if (splits < 0) splits = 0;  // no key: zero rows (the call is flagged)
   bool bad = false;
@@ -932,6 +941,7 @@ int prepare_decode(const void* q, int64_t q_s_batch, int64_t q_s_head, int32_t b
       if ((1 << sh) == kv->block_size) p.kv.bs_shift = sh;
     if (kv->slots) {
       CS_REQUIRE(kv->slots_stride >= 0, "slot map stride must be non-negative");
+      CS_REQUIRE(kv->slots_cols > 0, "slot map needs at least one column");
       CS_REQUIRE(kv->side_rows >= 0, "side_rows must be non-negative");
       if (kv->side_rows > 0)
         CS_REQUIRE(kv->side_k && kv->side_v && (reinterpret_cast<uintptr_t>(kv->side_k) % 16) == 0 &&
@@ -941,6 +951,7 @@ int prepare_decode(const void* q, int64_t q_s_batch, int64_t q_s_head, int32_t b
                    "sidecar rows must be 16-byte aligned");
       p.kv.slots = kv->slots;
       p.kv.slots_stride = kv->slots_stride;
+      p.kv.slots_cols = kv->slots_cols;
       p.kv.native_slots = kv->num_blocks * kv->block_size;
       p.kv.side_k = static_cast<const uint16_t*>(kv->side_k);
       p.kv.side_v = static_cast<const uint16_t*>(kv->side_v);

@@ -117,7 +117,7 @@ struct kv_addr {
   const uint16_t* v;
   int64_t k_sb, k_st, k_sh, v_sb, v_st, v_sh;
   const int64_t* slots;  // per-token slot map (mode 2)
-  int64_t slots_stride;
+  int64_t slots_stride, slots_cols;
   int64_t native_slots;  // num_blocks * block_size (< 2^31)
   const uint16_t* side_k;
   const uint16_t* side_v;
@@ -360,7 +360,7 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
       for (int i = tid; i < n_win; i += kThreads) {
         const int key = klo + i;
         uint32_t ent = kNoSlot;
-        if (key < kend) {
+        if (key < kend && key < p.kv.slots_cols) {
           const int64_t slot = srow[key];
           if (slot >= 0 && slot < p.kv.native_slots)
             ent = static_cast<uint32_t>(slot);
@@ -863,7 +863,7 @@ int fill_kv(const cs_kv_source* kv, cs::kv_addr* a) {
       if ((1 << s) == kv->block_size) r.bs_shift = s;
     r.num_blocks = kv->num_blocks;
     if (kv->slots) {
-      CS_REQUIRE(kv->slots_stride >= 0 && kv->side_rows >= 0, "bad slot map");
+      CS_REQUIRE(kv->slots_stride >= 0 && kv->side_rows >= 0 && kv->slots_cols > 0, "bad slot map");
       CS_REQUIRE(kv->num_blocks * kv->block_size < (int64_t(1) << 31) && kv->side_rows < (int64_t(1) << 31),
                  "the slot-map prefill needs fewer than 2^31 native slots and sidecar rows");
       if (kv->side_rows > 0)
@@ -874,6 +874,7 @@ int fill_kv(const cs_kv_source* kv, cs::kv_addr* a) {
                    "sidecar rows must be 16-byte aligned");
       r.slots = kv->slots;
       r.slots_stride = kv->slots_stride;
+      r.slots_cols = kv->slots_cols;
       r.native_slots = kv->num_blocks * kv->block_size;
       r.side_k = static_cast<const uint16_t*>(kv->side_k);
       r.side_v = static_cast<const uint16_t*>(kv->side_v);

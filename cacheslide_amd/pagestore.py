@@ -223,11 +223,24 @@ class PageStore:
             pending.unlink(missing_ok=True)
             raise
         with self._lock:
-            self._pages[key] = _Page(generation, checksum, len(payload), selected_count, path, file_bytes)
-            self._cache(key, payload)
+            winner = self._pages.get(key)
+            if winner is None and not self._closed:
+                self._pages[key] = _Page(generation, checksum, len(payload), selected_count, path, file_bytes)
+                self._cache(key, payload)
+                return
+            # a concurrent put of the same key published first (or the store
+            # closed meanwhile): this generation is withdrawn
+            self._disk_bytes -= file_bytes
+        path.unlink(missing_ok=True)
+        if winner is None:
+            raise RuntimeError("page store is closed")
+        if winner.checksum != checksum or winner.size != len(payload):
+            raise ValueError("pages are immutable: the key holds different bytes")
 
     def read(self, key: str) -> bytes:
-        """The page's bytes, from RAM or from its file (checksum verified)."""
+        """The page's bytes, from RAM or from its file; either way the payload's
+        sha256 is checked against the page record first (a resident payload
+        too, as storage.py:453-460 re-verifies it on every load)."""
         with self._lock:
             self._check_open()
             page = self._pages.get(key)
@@ -236,7 +249,10 @@ class PageStore:
             hit = self._ram.get(key)
             if hit is not None:
                 self._ram.move_to_end(key)
-                return hit
+        if hit is not None:
+            if len(hit) != page.size or hashlib.sha256(hit).hexdigest() != page.checksum:
+                raise CacheIntegrityError("resident page checksum mismatch")
+            return hit
         with open(page.path, "rb") as stream:
             blob = stream.read()
         head, payload = parse_page(blob, expect_key=key)

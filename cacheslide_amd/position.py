@@ -20,6 +20,7 @@ from collections import Counter
 from collections.abc import Callable, Sequence
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 from torch import Tensor, nn
 
@@ -987,11 +988,11 @@ def _verified_positions(trace, first: CoPEPositionTrace, device: torch.device) -
 
 def _modal_sample(samples: list[Tensor], bin_width: float) -> Tensor:
     """First sample of the most frequent quantised joint pattern; among equally
-    frequent patterns the lexicographically smallest wins."""
+    frequent patterns the lexicographically smallest wins (position.py:676-688)."""
     counts: Counter[tuple[int, ...]] = Counter()
     first_seen: dict[tuple[int, ...], int] = {}
     for index, sample in enumerate(samples):
-        pattern = tuple(_quantise(v, bin_width) for v in sample.flatten().tolist())
+        pattern = _quantise(sample, bin_width)
         counts[pattern] += 1
         first_seen.setdefault(pattern, index)
     top = max(counts.values())
@@ -999,9 +1000,20 @@ def _modal_sample(samples: list[Tensor], bin_width: float) -> Tensor:
     return samples[first_seen[winner]]
 
 
-def _quantise(value: float, width: float) -> int:
-    """round-half-to-even of value / width, as torch.round."""
-    return int(round(value / width))
+def _quantise(sample: Tensor, width: float) -> tuple[int, ...]:
+    """The joint histogram key of a sample: each position divided by the bin
+    width in the sample's own dtype (position.py:680-681 divides the fp32 or
+    fp64 positions tensor by the Python width, so the quotient is rounded to
+    that dtype), then rounded half to even."""
+    flat = sample.detach().cpu().flatten()
+    if flat.dtype in (torch.float32, torch.float64):
+        values = flat.numpy()
+        quotient = values / values.dtype.type(width)
+    else:
+        # reduced-precision positions: the quotient is formed in fp32 and
+        # rounded back to the positions' dtype before the bin is taken
+        quotient = (flat.float() / torch.tensor(width, dtype=torch.float32)).to(flat.dtype).float().numpy()
+    return tuple(np.rint(quotient).astype(np.int64).tolist())
 
 
 def _trace_positions(trace: CoPEPositionTrace, device: torch.device) -> Tensor | None:

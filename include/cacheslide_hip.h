@@ -255,13 +255,15 @@ typedef struct cs_kv_source {
   int64_t k_s_batch, k_s_tok, k_s_head;
   int64_t v_s_batch, v_s_tok, v_s_head;
   /* slot form (slots != NULL; cache, strides, block_size and num_blocks as above, the
-   * block table is not read): int64 slots [B, >= nk] */
+   * block table is not read): int64 slots [B, slots_cols] */
   const int64_t* slots;
   int64_t slots_stride;       /* elements between requests of slots */
   const void* side_k;         /* bf16 [side_rows, Hkv, 128] or NULL */
   const void* side_v;
   int64_t side_s_row, side_s_head; /* element strides shared by side_k and side_v */
   int64_t side_rows;
+  int64_t slots_cols;         /* entries per slots row (> 0 with slots): keys at or past it
+                               * read zeros and set CS_FLAG_BLOCK_INVALID */
 } cs_kv_source;
 
 /* Prefill (position.py:404-560 for q >> 1) on MFMA.

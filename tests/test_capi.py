@@ -139,5 +139,9 @@ def test_decode_refuses_a_small_workspace_without_a_device():
     slot_src.num_blocks, slot_src.side_rows = 1, 4
     slot_src.side_k, slot_src.side_v, slot_src.side_s_row, slot_src.side_s_head = base + 2, base, 128, 128
     args[8] = ctypes.byref(slot_src)
+    # a slot map must state its width
+    assert lib.cs_ccpe_decode_bf16(*args, need, *tail) == _hip.CS_EINVAL
+    assert b"slot map needs at least one column" in lib.cs_last_error()
+    slot_src.slots_cols = 1000
     assert lib.cs_ccpe_decode_bf16(*args, need, *tail) == _hip.CS_EINVAL
     assert b"sidecar rows must be 16-byte aligned" in lib.cs_last_error()

@@ -191,3 +191,37 @@ def test_decode_context_and_workspace_checks(device):
     out = ccpe_decode_paged(q, cache, table, torch.tensor([5, 100], dtype=torch.int32, device=device), cope,
                             split=64, max_context=100, workspace=ws)
     assert out.shape == (2, 4, 128) and bool(torch.isfinite(out.float()).all())
+
+
+def test_decode_context_past_slot_map_raises(device):
+    """A context longer than max_context with a slot map exactly max_context
+    wide: the decode clamps its reads to the map and flags the call."""
+    cache = seeded((8, 2, 16, 256), 950, dtype=torch.bfloat16).to(device)
+    cope = CoPE(128, 8, device=device)
+    max_context = 64
+    slots = torch.arange(max_context, dtype=torch.long, device=device)[None].repeat(2, 1).contiguous()
+    lens = torch.tensor([40, 100], dtype=torch.int32, device=device)
+    q = seeded((2, 8, 128), 951, dtype=torch.bfloat16).to(device)
+    with pytest.raises(ValueError, match="exceeds max_context"):
+        ccpe_decode_paged(q, cache, None, lens, cope, slots=slots, max_context=max_context, split=64)
+    # the in-range request of the same call is unaffected by the clamp
+    ok = ccpe_decode_paged(q[:1], cache, None, lens[:1], cope, slots=slots[:1], max_context=max_context,
+                           split=64)
+    assert bool(torch.isfinite(ok.float()).all())
+
+
+def test_prefill_slot_map_narrower_than_context_raises(device):
+    """Keys past the slot map's width read zeros and flag the call rather
+    than reading past the map."""
+    cache = seeded((8, 1, 16, 256), 952, dtype=torch.bfloat16).to(device)
+    cope = CoPE(128, 8, device=device)
+    slots = torch.arange(20, dtype=torch.long, device=device)[None].contiguous()
+    lens = torch.tensor([48], dtype=torch.int32, device=device)
+    q = seeded((1, 48, 4, 128), 953, dtype=torch.bfloat16).to(device)
+    qpos = torch.arange(48, dtype=torch.long, device=device)[None].contiguous()
+    with pytest.raises(ValueError, match="outside the cache"):
+        ccpe_prefill_paged(q, cache, None, lens, cope, qpos, slots=slots)
+    # the same map covering every key is accepted
+    full = torch.arange(48, dtype=torch.long, device=device)[None].contiguous()
+    out = ccpe_prefill_paged(q, cache, None, lens, cope, qpos, slots=full)
+    assert bool(torch.isfinite(out.float()).all())

@@ -141,3 +141,59 @@ def test_single_writer_and_foreign_directories(tmp_path):
     closed.close()
     with pytest.raises(RuntimeError, match="closed"):
         closed.put("k", b"x")
+
+
+def test_resident_page_is_verified_on_read(tmp_path):
+    """A RAM-resident payload is checked against the page's sha256 on every
+    read, as storage.py:453-460 re-verifies resident pages on load."""
+    with store_at(tmp_path / "s") as store:
+        store.put("k", b"data")
+        assert store.metadata("k")["resident"]
+        assert store.read("k") == b"data"
+        store._ram["k"] = b"dat4"          # the resident copy goes bad in memory
+        with pytest.raises(CacheIntegrityError, match="resident page checksum"):
+            store.read("k")
+
+
+def test_concurrent_puts_of_one_key_publish_one_generation(tmp_path, monkeypatch):
+    """A second put of the same key that publishes while the first is still
+    writing its file wins; the first withdraws its file and, holding
+    different bytes, is refused.  The directory then reopens with one page."""
+    import os
+
+    from cacheslide_amd import pagestore
+
+    real_fsync = os.fsync
+    nested = {"done": False}
+    store = store_at(tmp_path / "s")
+
+    def racing_fsync(fd):
+        real_fsync(fd)
+        if not nested["done"]:
+            nested["done"] = True
+            store.put("k", b"second")       # publishes while the first put is mid-write
+
+    monkeypatch.setattr(pagestore.os, "fsync", racing_fsync)
+    with pytest.raises(ValueError, match="immutable"):
+        store.put("k", b"first!")
+    monkeypatch.setattr(pagestore.os, "fsync", real_fsync)
+    assert store.read("k") == b"second"
+    disk = store.stats()["disk_bytes"]
+    files = [p for p in (tmp_path / "s").iterdir() if p.name.endswith(".page")]
+    assert len(files) == 1 and disk == files[0].stat().st_size
+    # same bytes racing: the loser returns quietly
+    nested["done"] = False
+
+    def same_fsync(fd):
+        real_fsync(fd)
+        if not nested["done"]:
+            nested["done"] = True
+            store.put("j", b"same")
+
+    monkeypatch.setattr(pagestore.os, "fsync", same_fsync)
+    store.put("j", b"same")
+    monkeypatch.setattr(pagestore.os, "fsync", real_fsync)
+    store.close()
+    with store_at(tmp_path / "s") as again:
+        assert again.read("k") == b"second" and again.read("j") == b"same"
+        assert again.stats()["pages"] == 2
