@@ -58,147 +58,13 @@
 
 #include "common.h"
 #include "ccpe_path.h"
+#include "prefill_shared.h"
 
 namespace cs {
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef float floatx16 __attribute__((ext_vector_type(16)));
-typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4_tr;
-#define CS_LDS __attribute__((address_space(3)))
-
-constexpr int kD = 128;
-constexpr int kCols = 32;  // (row, head) columns per wave
-constexpr int kTileN = 32;               // keys per tile
-constexpr int kChunks = 16;              // 16-byte chunks of a 256-byte K or V row
-constexpr int kStageSlots = kTileN * kChunks;  // uint4 slots of one K (or V) stage
-constexpr int kMaxPos = 128;
-constexpr int kPosChunk = 64;  // E^T positions staged per pass (bf16 hi and lo, 16 KB each)
-constexpr int kBtWindow = 1024;  // block-table (or slot-map) entries held in LDS at a time
 constexpr int kStages = 3;
 constexpr size_t kStaticLds = kStages * 2 * kStageSlots * 16 + 4 * kBtWindow + 16;
-constexpr size_t kLdsLimit = 160 * 1024;
-constexpr float kInvSqrtD = 0.08838834764831845f;  // 1/sqrt(128)
-constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kSqrtD = 11.313708498984761f;  // sqrt(128)
-constexpr float kLn2 = 0.6931471805599453f;
-
-// Exchange with lane l ^ 32: v_permlane32_swap of x with itself leaves
-// {x[l], x[l ^ 32]} in the two results, in an order that depends on the half.
-__device__ inline void swap_halves(float x, float& lo, float& hi) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  lo = __uint_as_float(r[0]);
-  hi = __uint_as_float(r[1]);
-}
-
-__device__ inline uint32_t pack_bf16x2(float a, float b) {
-  const bf16x2 v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
-  return __builtin_bit_cast(uint32_t, v);
-}
-
-// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
-// vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt[5:4] in [15:14]).
-constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
-
-// Keys past the causal range and keys of invalid blocks are loaded from this
-// zero record (256 bf16), so every tile load is issued unconditionally.
-__device__ __attribute__((aligned(16))) uint32_t g_zero_record[kD] = {};
-
-struct kv_addr {
-  const uint16_t* cache;
-  int64_t s_block, s_head, s_offset;
-  int32_t block_size, bs_shift;  // bs_shift >= 0 when block_size is a power of two
-  int64_t num_blocks;
-  const int32_t* block_table;
-  int64_t bt_stride, bt_cols;
-  const uint16_t* k;
-  const uint16_t* v;
-  int64_t k_sb, k_st, k_sh, v_sb, v_st, v_sh;
-  const int64_t* slots;  // per-token slot map (mode 2)
-  int64_t slots_stride, slots_cols;
-  int64_t native_slots;  // num_blocks * block_size (< 2^31)
-  const uint16_t* side_k;
-  const uint16_t* side_v;
-  int64_t side_sr, side_sh, side_rows;
-};
-
-// Slot-map window entries (mode 2): a native slot (< 2^31), kSideTag | sidecar
-// row, or kNoSlot for an invalid slot.
-constexpr uint32_t kSideTag = 0x80000000u;
-constexpr uint32_t kNoSlot = 0xFFFFFFFFu;
-
-struct prefill_params {
-  const uint16_t* q;
-  int64_t q_sb, q_st, q_sh;
-  const int64_t* qpos;
-  int64_t qpos_sb;
-  int32_t batch, nq, hq, hkv, group, rows_per_wg, row_blocks, total_wg;
-  const int32_t* nk;
-  kv_addr kv;
-  const float* e;
-  int32_t npos, tab_stride;
-  uint16_t* out;
-  int32_t* flags;
-  // Policy lowering (dense calls of the POLICY variant): selected rows, fixed
-  // keys as a bitmap (bit j % 32 of word j / 32), the canonical position of
-  // each (head, row)'s own key (NaN: no substitution) and the fixed-row map.
-  const uint8_t* sel_rows;
-  const uint32_t* fixed_bits;
-  const float* canon_self;  // [hq, nq]
-  const int64_t* q_ord;     // -1: not a fixed row
-};
-
-__device__ inline bf16x8 as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
-
-// Direct global -> LDS load of 16 bytes per lane: lane i's bytes land at LDS
-// byte address lds + 16 i (lds wave-uniform, in an SGPR).  Issued through
-// inline assembly so the compiler does not tie later LDS reads to it;
-// completion is made visible only by the explicit vmcnt wait and barrier of
-// the tile loop.
-__device__ inline void lds_dma16(const void* gptr, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
-               : : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(gptr) : "memory", "m0");
-}
-
-// The same with a wave-uniform 64-bit base in SGPRs and a 32-bit per-lane
-// byte offset (the instruction's saddr form): no per-lane address arithmetic.
-__device__ inline void lds_dma16_s(uint32_t voff, uint64_t sbase, uint32_t lds) {
-  // readfirstlane returns int: each half goes through uint32_t so that widening
-  // never sign-extends the low word
-  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(sbase >> 32)));
-  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(sbase)));
-  const uint64_t base = (static_cast<uint64_t>(hi) << 32) | lo;
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
-               : : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(base) : "memory", "m0");
-}
-
-// LDS byte address of a __shared__ object (the generic -> LDS conversion,
-// done once outside the tile loop)
-__device__ inline uint32_t lds_address(const void* p) {
-  return __builtin_amdgcn_readfirstlane(
-      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((CS_LDS const void*)p)));
-}
-
-// Flat workgroup id -> (batch, kv head, row block).  Dispatch is round-robin
-// over the 8 XCDs by id, so contiguous logical ranges are spread as one per
-// XCD: a (batch, kv head)'s K/V stays in one XCD's L2.  The heaviest
-// (right-most) row blocks go first.
-__device__ inline void decode_wg(const prefill_params& p, int& b, int& kvh, int& rb) {
-  const int id = blockIdx.x;
-  int logical = id;
-  if (p.total_wg % 8 == 0) logical = (id % 8) * (p.total_wg / 8) + id / 8;
-  rb = p.row_blocks - 1 - (logical % p.row_blocks);
-  const int rest = logical / p.row_blocks;
-  kvh = rest % p.hkv;
-  b = rest / p.hkv;
-}
-
-struct stage_t {
-  uint4 k[kStageSlots];
-  uint4 v[kStageSlots];
-};
 
 // WAVES wavefronts of 32 columns each (2, 4 or 8); registers for two
 // wavefronts per SIMD.  POLICY (dense
@@ -218,9 +84,8 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
   // of keys [bt_lo, bt_lo + kBtWindow)
   __shared__ int32_t bt_lds[kBtWindow];
   __shared__ int64_t wg_max_pos;
-  // [32 WAVES columns][tab_stride] QE log2(e), fp16 (the table only enters
-  // bias differences of unsaturated keys; 2^-11 relative precision)
-  extern __shared__ __align__(16) _Float16 tab[];
+  // [32 WAVES columns][tab_stride] QE log2(e), fp32
+  extern __shared__ __align__(16) float tab[];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -276,7 +141,7 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
   // stages, swizzled like K: chunk c of position pos at c ^ (pos % 16).
   uint16_t* ehi = reinterpret_cast<uint16_t*>(&st0);  // [64 pos][128 dims], 16 KB
   uint16_t* elo = reinterpret_cast<uint16_t*>(&st1);
-  _Float16* tcol = tab + c * p.tab_stride;
+  float* tcol = tab + c * p.tab_stride;
   for (int pc = 0; pc < p.npos; pc += kPosChunk) {
     // item (position pc + i % 64, dims 8 (i / 64) .. + 7) for i = tid + kThreads r:
     // its 8 values become one 16-byte chunk of E^T hi and one of lo.  All of a
@@ -320,23 +185,17 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
         acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, qb[ks], acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, qb[ks], acc, 0, 0, 0);
       }
-      // finite in fp16 (clamped; NaN becomes -65000), so bias + (-inf) stays -inf;
-      // positions 2i, 2i + 1 in one 32-bit store (rows are 4-byte aligned, P is even)
+      // finite (clamped to +-1e30; NaN becomes -1e30), so bias + (-inf) stays -inf
 #pragma unroll
-      for (int v = 0; v < 16; v += 2) {
+      for (int v = 0; v < 16; ++v) {
         const int pv = pc + 32 * pb + 8 * (v >> 2) + 4 * h + (v & 3);
-        if (pv < p.npos) {
-          typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-          const half2_t w = {static_cast<_Float16>(fminf(fmaxf(acc[v] * kLog2e, -65000.f), 65000.f)),
-                             static_cast<_Float16>(fminf(fmaxf(acc[v + 1] * kLog2e, -65000.f), 65000.f))};
-          *reinterpret_cast<half2_t*>(tcol + pv) = w;
-        }
+        if (pv < p.npos) tcol[pv] = fminf(fmaxf(acc[v] * kLog2e, -1e30f), 1e30f);
       }
     }
   }
   __syncthreads();
   // QE[P-1] of the column: the bias of saturated keys, subtracted from every bias
-  const float top_qe = static_cast<float>(tcol[p.npos - 1]);
+  const float top_qe = tcol[p.npos - 1];
 
   const int64_t wgmax = wg_max_pos;
   const int64_t kend = wgmax + 1 < nk ? wgmax + 1 : (nk > 0 ? nk : 0);  // keys [0, kend)
@@ -632,10 +491,9 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
         pos = pos > 0.f ? pos : 0.f;
         const int lo = static_cast<int>(pos);  // pos >= 0: truncation is floor
         const float frac = __builtin_amdgcn_fractf(pos);
-        // hi clamped (not lo + 1): two 16-bit reads, never one misaligned 32-bit read
         const int hi = lo + 1 < p.npos - 1 ? lo + 1 : p.npos - 1;
-        const float tlo = static_cast<float>(tcol[lo]);
-        const float bias = fmaf(frac, static_cast<float>(tcol[hi]) - tlo, tlo - top_qe);
+        const float tlo = tcol[lo];
+        const float bias = fmaf(frac, tcol[hi] - tlo, tlo - top_qe);
         // raw score plus the bias in raw units (the table holds QE log2(e));
         // a masked key stays -inf (table entries are finite)
         s[v] = fmaf(bias, kSqrtD * kLn2, s[v]);
@@ -956,20 +814,19 @@ int prepare_prefill(const void* q, int64_t q_s_batch, int64_t q_s_tok, int64_t q
   p.hq = hq;
   p.hkv = hkv;
   p.group = group;
-  // 4 wavefronts (128 columns): two workgroups per CU while the QE table is
-  // small enough, so one workgroup's prologue and barriers overlap the other's
-  // tile loop; larger tables use 8 wavefronts, one workgroup per CU
-  // QE table row length in halfs: even (rows 4-byte aligned for the paired
-  // table stores) and an odd number of 32-bit words (no bank conflicts
-  // between columns)
-  int tab_stride = (max_positions + 1) / 2 * 2 + 2;
-  if ((tab_stride / 2) % 2 == 0) tab_stride += 2;
-  const size_t tab4 = 2 * 4 * kCols * static_cast<size_t>(tab_stride);
-  int waves = 2 * (tab4 + kStaticLds) <= kLdsLimit ? 4 : 8;
+  // fp32 QE table rows of an odd number of words (no bank conflicts between
+  // columns).  4 wavefronts (128 columns) while two such workgroups fit in a
+  // CU, so one workgroup's prologue and barriers overlap the other's tile
+  // loop; else 8 wavefronts (one workgroup, still two waves per SIMD) while
+  // its table fits, else 4.
+  const int tab_stride = max_positions | 1;
+  auto tab_bytes = [&](int w) { return sizeof(float) * kCols * w * static_cast<size_t>(tab_stride); };
+  int waves = 2 * (tab_bytes(4) + kStaticLds) <= kLdsLimit ? 4 : (tab_bytes(8) + kStaticLds <= kLdsLimit ? 8 : 4);
   // A launch of fewer 4-wave workgroups than two per CU (a selective call's
   // few hundred rows) runs 2-wave workgroups: twice as many workgroups share
   // the longest key walks.
-  if (waves == 4 && static_cast<int64_t>(batch) * hkv * ceil_div(nq, kCols * 4 / group) < 2 * device_cus())
+  if (static_cast<int64_t>(batch) * hkv * ceil_div(nq, kCols * 4 / group) < 2 * device_cus() &&
+      2 * (tab_bytes(2) + kStaticLds) <= kLdsLimit)
     waves = 2;
   p.rows_per_wg = kCols * waves / group;
   p.row_blocks = static_cast<int32_t>(ceil_div(nq, p.rows_per_wg));
@@ -982,7 +839,7 @@ int prepare_prefill(const void* q, int64_t q_s_batch, int64_t q_s_tok, int64_t q
   const int64_t total = static_cast<int64_t>(batch) * hkv * p.row_blocks;
   CS_REQUIRE(total < (1ll << 31), "grid too large");
   p.total_wg = static_cast<int32_t>(total);
-  const size_t smem = 2 * kCols * waves * static_cast<size_t>(p.tab_stride);
+  const size_t smem = tab_bytes(waves);
   if (smem + kStaticLds > kLdsLimit) {
     set_error("prefill LDS %zu bytes exceeds the workgroup limit", smem + kStaticLds);
     return CS_EUNSUPPORTED;
