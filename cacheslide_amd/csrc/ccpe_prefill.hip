@@ -185,17 +185,26 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
         acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, qb[ks], acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, qb[ks], acc, 0, 0, 0);
       }
-      // finite (clamped to +-1e30; NaN becomes -1e30), so bias + (-inf) stays -inf
+      // raw-score units; finite (clamped to +-1e30, NaN to -1e30), so
+      // bias + (-inf) stays -inf
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int pv = pc + 32 * pb + 8 * (v >> 2) + 4 * h + (v & 3);
-        if (pv < p.npos) tcol[pv] = fminf(fmaxf(acc[v] * kLog2e, -1e30f), 1e30f);
+        if (pv < p.npos) tcol[pv] = fminf(fmaxf(acc[v] * kSqrtD, -1e30f), 1e30f);
       }
     }
   }
+  // Shift every entry by the column's QE[P-1] (the bias of saturated keys;
+  // softmax is invariant to it) and repeat entry P-1 as entry P: a position p
+  // then reads entries lo = floor(min(p, P-1)) and lo + 1 with no clamp, and
+  // a saturated key adds 0.
   __syncthreads();
-  // QE[P-1] of the column: the bias of saturated keys, subtracted from every bias
-  const float top_qe = tcol[p.npos - 1];
+  {
+    const float top_qe = tcol[p.npos - 1];
+    __syncthreads();  // both lanes of every column hold it before any entry moves
+    for (int j = h; j <= p.npos; j += 2) tcol[j] = j < p.npos - 1 ? tcol[j] - top_qe : 0.f;
+  }
+  __syncthreads();
 
   const int64_t wgmax = wg_max_pos;
   const int64_t kend = wgmax + 1 < nk ? wgmax + 1 : (nk > 0 ? nk : 0);  // keys [0, kend)
@@ -439,7 +448,9 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
     }
     if (!__all(carry >= top)) {
       const float gate_off = -m_base * (kInvSqrtD * kLog2e);
-      // gates; runs of 4 keys (8 j4 + 4h + 0..3) and their in-run suffix sums
+      // gates; runs of 4 keys (8 j4 + 4h + 0..3) and their in-run suffix sums.
+      // A key past the causal end holds a -inf score (masked above whenever
+      // the tile reaches past any column's row): its gate is 0.
       float gsuf[16], run[4];
 #pragma unroll
       for (int j4 = 0; j4 < 4; ++j4) {
@@ -447,10 +458,9 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
 #pragma unroll
         for (int i = 3; i >= 0; --i) {
           const int v = 4 * j4 + i;
-          const bool ok = 8 * j4 + i <= lim;
           // sigmoid(q.k / sqrt(D)) = 1 / (1 + 2^(-(s + m_base) log2(e) / sqrt(D)))
           const float e = __builtin_amdgcn_exp2f(fmaf(s[v], -kInvSqrtD * kLog2e, gate_off));
-          acc += ok ? __builtin_amdgcn_rcpf(1.f + e) : 0.f;
+          acc += __builtin_amdgcn_rcpf(1.f + e);
           gsuf[v] = acc;
         }
         run[j4] = acc;
@@ -487,16 +497,14 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
       for (int v = 0; v < 16; ++v) {
         float pos = start[v >> 2] + gsuf[v];
         if constexpr (POLICY) pos = v == self_v ? canon_self : pos;
-        pos = pos < top ? pos : top;  // NaN becomes top: table reads stay in range
-        pos = pos > 0.f ? pos : 0.f;
-        const int lo = static_cast<int>(pos);  // pos >= 0: truncation is floor
+        // positions are >= 0; NaN becomes P-1: table reads stay in range
+        pos = fminf(pos, top);
+        const uint32_t lo = static_cast<uint32_t>(pos);
         const float frac = __builtin_amdgcn_fractf(pos);
-        const int hi = lo + 1 < p.npos - 1 ? lo + 1 : p.npos - 1;
-        const float tlo = tcol[lo];
-        const float bias = fmaf(frac, tcol[hi] - tlo, tlo - top_qe);
-        // raw score plus the bias in raw units (the table holds QE log2(e));
-        // a masked key stays -inf (table entries are finite)
-        s[v] = fmaf(bias, kSqrtD * kLn2, s[v]);
+        const float t0 = tcol[lo], t1 = tcol[lo + 1];
+        // raw score plus the bias in raw units; a masked key stays -inf
+        // (table entries are finite)
+        s[v] += fmaf(frac, t1 - t0, t0);
       }
       carry += total;
     }
@@ -819,7 +827,8 @@ int prepare_prefill(const void* q, int64_t q_s_batch, int64_t q_s_tok, int64_t q
   // CU, so one workgroup's prologue and barriers overlap the other's tile
   // loop; else 8 wavefronts (one workgroup, still two waves per SIMD) while
   // its table fits, else 4.
-  const int tab_stride = max_positions | 1;
+  // P + 1 entries per column (entry P repeats P-1), an odd number of words
+  const int tab_stride = (max_positions + 1) | 1;
   auto tab_bytes = [&](int w) { return sizeof(float) * kCols * w * static_cast<size_t>(tab_stride); };
   int waves = 2 * (tab_bytes(4) + kStaticLds) <= kLdsLimit ? 4 : (tab_bytes(8) + kStaticLds <= kLdsLimit ? 8 : 4);
   // A launch of fewer 4-wave workgroups than two per CU (a selective call's

@@ -176,6 +176,15 @@ def test_large_sparse_unsorted_rows(device):
                    qpos_fn=scattered, seed=700, sample=64)
 
 
+def test_large_paged_windows_small_blocks(device):
+    """Block size 2: one block-table window in LDS covers 63 tiles (2016
+    keys), so these contexts take two windows, with every key loaded on its
+    own."""
+    say("bs 2 windows")
+    run_paged_case(device, lens=[2500, 2100, 3000, 2048], nq=512, hq=32, hkv=8, npos=64, bs=2, seed=650,
+                   sample=64)
+
+
 def test_large_dense_cope_attention(device):
     """cope_attention's dense fast path (one request, K/V rows)."""
     n, hq, hkv, npos = 2048, 32, 8, 64
