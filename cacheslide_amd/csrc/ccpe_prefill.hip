@@ -67,10 +67,11 @@ constexpr int kStages = 3;
 constexpr size_t kStaticLds = kStages * 2 * kStageSlots * 16 + 4 * kBtWindow + 16;
 
 // WAVES wavefronts of 32 columns each (2, 4 or 8); registers for two
-// wavefronts per SIMD.  POLICY (dense
-// K/V only): SelectedAssociationPolicy visibility and the canonical position
-// of each selected fixed row's own key, for calls in which every fixed query
-// row is selected (its only visible fixed key is then itself).
+// wavefronts per SIMD.  POLICY (dense K/V only): CanonicalPositionPolicy and
+// SelectedAssociationPolicy.  A selected fixed row sees one fixed key, its
+// own, at its canonical position; a fixed row that is not selected sees every
+// fixed key at its canonical position (the calibration-layer call, and
+// selected_attention "all"); other rows keep their contextual positions.
 template <int MODE, int WAVES, bool POLICY = false>
 __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2))) ccpe_prefill_kernel(prefill_params p) {
   constexpr bool PAGED = MODE != 0;
@@ -103,14 +104,19 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
   const int64_t qp = row_ok ? p.qpos[b * p.qpos_sb + row] : -1;
   bool sel_col = false;   // the column's row is selected: fixed keys other than its own are invisible
   float canon_self = 0.f;  // canonical position of the column's own key (NaN: contextual)
+  // a fixed row that is not selected: its profile row, canonical positions
+  // of every fixed key
+  const float* canon_row = nullptr;
+  bool canon_wave = false;
   if constexpr (POLICY) {
     canon_self = __builtin_nanf("");
     if (row_ok) {
-      sel_col = p.sel_rows[row] != 0;
+      sel_col = p.sel_rows ? p.sel_rows[row] != 0 : false;
       if (p.canon_self) canon_self = p.canon_self[static_cast<int64_t>(head) * p.nq + row];
-      // a fixed row that is not selected sees every fixed key: not this variant
-      if (p.q_ord && p.q_ord[row] != -1 && !sel_col) atomicOr(p.flags, CS_FLAG_POLICY_GENERIC);
+      const int64_t qo = p.canon && p.q_ord ? p.q_ord[row] : -1;
+      if (!sel_col && qo >= 0) canon_row = p.canon + head * p.c_s0 + qo * p.c_s1;
     }
+    canon_wave = __builtin_amdgcn_readfirstlane(__any(canon_row != nullptr) ? 1 : 0) != 0;
   }
 
   if (tid == 0) wg_max_pos = 0;
@@ -409,7 +415,29 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
   const int j16 = lane & 15;
   // element offset of this lane's transposed V read within a stage
   const int vrd_off = 512 * h + 32 * (2 * ((lane >> 4) & 1) + ((j16 & 3) >> 1)) + 8 * (j16 >> 2) + 4 * (j16 & 1);
-  auto compute = [&](int t, const uint4* kst, const uint4* vst) {
+  // Canonical cells of a tile for the columns of fixed rows that are not
+  // selected, issued before the tile's K/V loads so that the wait for them
+  // leaves those loads in flight.  Per run of 4 keys (8 j4 + 4h + 0..3):
+  // one 16-byte load when the run is a whole aligned group (cgo >= 0, its
+  // first ordinal), else the zero record (the cells are then read key by key).
+  const float* zero_f = reinterpret_cast<const float*>(g_zero_record);
+  auto fetch = [&](int t, floatx4 (&cv)[4], int (&cgo)[4]) {
+    if constexpr (POLICY) {
+      if (!canon_wave || t * kTileN > wmax32) return;
+      if (uniform_load(p.fixed_bits, t) == 0u) return;
+#pragma unroll
+      for (int j4 = 0; j4 < 4; ++j4) {
+        const int32_t g0 = uniform_load(p.grp, 8 * static_cast<int64_t>(t) + 2 * j4);
+        const int32_t g1 = uniform_load(p.grp, 8 * static_cast<int64_t>(t) + 2 * j4 + 1);
+        const int32_t go = canon_row ? (h ? g1 : g0) : -1;
+        cgo[j4] = go;
+        cv[j4] = load_f4_untracked(go >= 0 ? canon_row + go : zero_f);
+      }
+    }
+  };
+  // (dma_after: this tile's K/V loads were issued after the canonical cells)
+  auto compute = [&](int t, const uint4* kst, const uint4* vst, floatx4 (&cv)[4], const int (&cgo)[4],
+                     bool dma_after) {
     const int base = t * kTileN;
     if (base > wmax32) return;  // every column of the wave precedes the tile
     uint32_t fixed_word = 0;
@@ -417,7 +445,7 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
       // A tile of fixed keys is invisible to selected columns except at their
       // own key, and a saturated column's positions no longer depend on its
       // gates: when that holds for the whole wave, the tile adds nothing.
-      fixed_word = p.fixed_bits[t];
+      fixed_word = uniform_load(p.fixed_bits, t);
       if (fixed_word == 0xFFFFFFFFu && __all(!row_ok || (sel_col && carry >= top))) return;
     }
     // all K operands first, then the 8 MFMAs of S^T
@@ -446,67 +474,98 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
       for (int v = 0; v < 16; ++v)
         if (8 * (v >> 2) + (v & 3) > lim) s[v] = -INFINITY;
     }
-    if (!__all(carry >= top)) {
-      const float gate_off = -m_base * (kInvSqrtD * kLog2e);
-      // gates; runs of 4 keys (8 j4 + 4h + 0..3) and their in-run suffix sums.
-      // A key past the causal end holds a -inf score (masked above whenever
-      // the tile reaches past any column's row): its gate is 0.
-      float gsuf[16], run[4];
+    const bool unsat = !__all(carry >= top);
+    bool canon_tile = false;
+    if constexpr (POLICY) canon_tile = canon_wave && fixed_word != 0u;
+    if (unsat || canon_tile) {
+      float pos[16];
+      if (unsat) {
+        const float gate_off = -m_base * (kInvSqrtD * kLog2e);
+        // gates; runs of 4 keys (8 j4 + 4h + 0..3) and their in-run suffix sums.
+        // A key past the causal end holds a -inf score (masked above whenever
+        // the tile reaches past any column's row): its gate is 0.
+        float gsuf[16], run[4];
 #pragma unroll
-      for (int j4 = 0; j4 < 4; ++j4) {
+        for (int j4 = 0; j4 < 4; ++j4) {
+          float acc = 0.f;
+#pragma unroll
+          for (int i = 3; i >= 0; --i) {
+            const int v = 4 * j4 + i;
+            // sigmoid(q.k / sqrt(D)) = 1 / (1 + 2^(-(s + m_base) log2(e) / sqrt(D)))
+            const float e = __builtin_amdgcn_exp2f(fmaf(s[v], -kInvSqrtD * kLog2e, gate_off));
+            acc += __builtin_amdgcn_rcpf(1.f + e);
+            gsuf[v] = acc;
+          }
+          run[j4] = acc;
+        }
+        float other[4];
+#pragma unroll
+        for (int j4 = 0; j4 < 4; ++j4) {
+          float a, c2;
+          swap_halves(run[j4], a, c2);
+          other[j4] = h ? a : c2;
+        }
+        // gate mass of the runs with larger keys: (j4, h=1) follows (j4, h=0)
+        float after[4];
         float acc = 0.f;
 #pragma unroll
-        for (int i = 3; i >= 0; --i) {
-          const int v = 4 * j4 + i;
-          // sigmoid(q.k / sqrt(D)) = 1 / (1 + 2^(-(s + m_base) log2(e) / sqrt(D)))
-          const float e = __builtin_amdgcn_exp2f(fmaf(s[v], -kInvSqrtD * kLog2e, gate_off));
-          acc += __builtin_amdgcn_rcpf(1.f + e);
-          gsuf[v] = acc;
+        for (int j4 = 3; j4 >= 0; --j4) {
+          after[j4] = acc + (h == 0 ? other[j4] : 0.f);
+          acc += run[j4] + other[j4];
         }
-        run[j4] = acc;
-      }
-      float other[4];
+        // the canonical position replaces the contextual one at a selected
+        // row's own key (its other fixed x fixed cells are invisible)
+        int self_v = -1;
+        if constexpr (POLICY) {
+          const int self_key = static_cast<int>(qp) - base - 4 * h;  // 8 j4 + i for this lane's half
+          if (!__builtin_isnan(canon_self) && self_key >= 0 && self_key < kTileN - 4 * h &&
+              (self_key & 4) == 0)
+            self_v = 4 * (self_key >> 3) + (self_key & 3);
+        }
 #pragma unroll
-      for (int j4 = 0; j4 < 4; ++j4) {
-        float a, c2;
-        swap_halves(run[j4], a, c2);
-        other[j4] = h ? a : c2;
-      }
-      // gate mass of the runs with larger keys: (j4, h=1) follows (j4, h=0)
-      float after[4];
-      float acc = 0.f;
+        for (int v = 0; v < 16; ++v) {
+          // position of the key: the carry, the runs with larger keys, the suffix in its run
+          pos[v] = (carry + after[v >> 2]) + gsuf[v];
+          if constexpr (POLICY) pos[v] = v == self_v ? canon_self : pos[v];
+        }
+        carry += acc;
+      } else {
 #pragma unroll
-      for (int j4 = 3; j4 >= 0; --j4) {
-        after[j4] = acc + (h == 0 ? other[j4] : 0.f);
-        acc += run[j4] + other[j4];
+        for (int v = 0; v < 16; ++v) pos[v] = top;  // saturated: every contextual position is P-1
       }
-      const float total = acc;
-      float start[4];  // position of the first (right-most) key of each run
-#pragma unroll
-      for (int j4 = 0; j4 < 4; ++j4) start[j4] = carry + after[j4];
-      // the canonical position replaces the contextual one at the row's own key
-      // (CanonicalPositionPolicy; its other fixed x fixed cells are invisible)
-      int self_v = -1;
       if constexpr (POLICY) {
-        const int self_key = static_cast<int>(qp) - base - 4 * h;  // 8 j4 + i for this lane's half
-        if (!__builtin_isnan(canon_self) && self_key >= 0 && self_key < kTileN - 4 * h &&
-            (self_key & 4) == 0)
-          self_v = 4 * (self_key >> 3) + (self_key & 3);
+        if (canon_tile) {
+          // the cells fetched before this tile's K/V loads have landed
+          if (dma_after)
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kInstr));
+          else
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+#pragma unroll
+          for (int j4 = 0; j4 < 4; ++j4) asm volatile("" : "+v"(cv[j4]));
+          if (canon_row) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+              const int j4 = v >> 2, i = v & 3;
+              const int kt = 8 * j4 + 4 * h + i;  // key within the tile
+              if ((fixed_word >> kt) & 1u) {
+                const float c = cgo[j4] >= 0 ? cv[j4][i] : canon_row[p.code[base + kt] * p.c_s2];
+                pos[v] = fmaxf(c, 0.f);  // negative or NaN cells (the checker rejects them) read entry 0
+              }
+            }
+          }
+        }
       }
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        float pos = start[v >> 2] + gsuf[v];
-        if constexpr (POLICY) pos = v == self_v ? canon_self : pos;
         // positions are >= 0; NaN becomes P-1: table reads stay in range
-        pos = fminf(pos, top);
-        const uint32_t lo = static_cast<uint32_t>(pos);
-        const float frac = __builtin_amdgcn_fractf(pos);
+        const float pv = fminf(pos[v], top);
+        const uint32_t lo = static_cast<uint32_t>(pv);
+        const float frac = __builtin_amdgcn_fractf(pv);
         const float t0 = tcol[lo], t1 = tcol[lo + 1];
         // raw score plus the bias in raw units; a masked key stays -inf
         // (table entries are finite)
         s[v] += fmaf(frac, t1 - t0, t0);
       }
-      carry += total;
     }
     if constexpr (POLICY) {
       // SelectedAssociationPolicy: fixed keys other than the row's own are
@@ -625,18 +684,23 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
     for (int t = thi - 1; t >= tlo; t -= 3) {
       wait_tile(t - 1 >= tlo);
       __syncthreads();
+      floatx4 cv[4];
+      int cgo[4];
+      fetch(t, cv, cgo);
       if (t - 2 >= tlo) issue(t - 2, 2);
-      compute(t, st0.k, st0.v);
+      compute(t, st0.k, st0.v, cv, cgo, t - 2 >= tlo);
       if (t - 1 < tlo) break;
       wait_tile(t - 2 >= tlo);
       __syncthreads();
+      fetch(t - 1, cv, cgo);
       if (t - 3 >= tlo) issue(t - 3, 0);
-      compute(t - 1, st1.k, st1.v);
+      compute(t - 1, st1.k, st1.v, cv, cgo, t - 3 >= tlo);
       if (t - 2 < tlo) break;
       wait_tile(t - 3 >= tlo);
       __syncthreads();
+      fetch(t - 2, cv, cgo);
       if (t - 4 >= tlo) issue(t - 4, 1);
-      compute(t - 2, st2.k, st2.v);
+      compute(t - 2, st2.k, st2.v, cv, cgo, t - 4 >= tlo);
     }
     thi = tlo;
   }
@@ -861,8 +925,9 @@ int prepare_prefill(const void* q, int64_t q_s_batch, int64_t q_s_tok, int64_t q
 
 // Fixed-key bitmap, the dynamic keys beside a fixed key (ascending), the key
 // count, and for the checker one code per key: the fixed ordinal (>= 0), -2 - s
-// for the dynamic key in boundary slot s, -1 for other dynamic keys.  One
-// workgroup.
+// for the dynamic key in boundary slot s, -1 for other dynamic keys.  The fixed
+// keys are the selected-association lowering's, or without it the keys with a
+// profile ordinal.  One workgroup.
 constexpr int kPackThreads = 1024;
 constexpr int kMaxBoundary = cs::kPolicyMaxBoundary;
 
@@ -874,6 +939,7 @@ __global__ void __launch_bounds__(kPackThreads) policy_pack_kernel(const uint8_t
   __shared__ int wave_count[kPackThreads / 64];
   __shared__ int running;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  auto is_fixed = [&](int64_t j) { return fixed_keys ? fixed_keys[j] != 0 : k_ord[j] >= 0; };
   if (tid == 0) {
     running = 0;
     nk_dev[0] = static_cast<int32_t>(nk);
@@ -883,7 +949,7 @@ __global__ void __launch_bounds__(kPackThreads) policy_pack_kernel(const uint8_t
     uint32_t word = 0;
     for (int i = 0; i < 32; ++i) {
       const int64_t j = 32 * w + i;
-      if (j < nk && fixed_keys[j]) word |= 1u << i;
+      if (j < nk && is_fixed(j)) word |= 1u << i;
     }
     bits[w] = word;
   }
@@ -891,8 +957,8 @@ __global__ void __launch_bounds__(kPackThreads) policy_pack_kernel(const uint8_t
   for (int64_t base = 0; base < nk; base += kPackThreads) {
     const int64_t j = base + tid;
     bool bnd = false;
-    if (j < nk && !fixed_keys[j])
-      bnd = (j > 0 && fixed_keys[j - 1]) || (j + 1 < nk && fixed_keys[j + 1]);
+    if (j < nk && !is_fixed(j))
+      bnd = (j > 0 && is_fixed(j - 1)) || (j + 1 < nk && is_fixed(j + 1));
     const unsigned long long m = __ballot(bnd);
     if (lane == 0) wave_count[wave] = __popcll(m);
     __syncthreads();
@@ -944,6 +1010,23 @@ __global__ void __launch_bounds__(256) policy_blocks_kernel(const int32_t* code,
   if (lane == 0) blk[t] = affine ? static_cast<int32_t>(off) : (plain ? -1 : -2);
 }
 
+// Per group of 4 keys (8 groups per 32-key tile, the last tile's padded): the
+// ordinal of its first key when all four are fixed with consecutive ordinals
+// and their canonical cells can be read as one aligned 16-byte load (aligned:
+// the profile's unit key stride and 16-byte rows), else -1.
+__global__ void policy_groups_kernel(const int32_t* code, int64_t nk, int32_t aligned, int64_t ngroups,
+                                     int32_t* grp) {
+  const int64_t g = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (g >= ngroups) return;
+  const int64_t j = 4 * g;
+  int32_t v = -1;
+  if (aligned && j + 3 < nk) {
+    const int32_t o = code[j];
+    if (o >= 0 && (o & 3) == 0 && code[j + 1] == o + 1 && code[j + 2] == o + 2 && code[j + 3] == o + 3) v = o;
+  }
+  grp[g] = v;
+}
+
 // Canonical position of each (head, row)'s own key, NaN when the row is not a
 // fixed row the profile covers: canonical[h][q_ord[row]][k_ord[qpos[row]]].
 __global__ void policy_self_kernel(const float* canon, int64_t c_s0, int64_t c_s1, int64_t c_s2,
@@ -972,6 +1055,8 @@ struct policy_ws {
   int32_t* code;
   int32_t* blk;
   float* canon_self;
+  int32_t* grp;
+  int64_t ngroups;
   int64_t bytes;
 };
 
@@ -990,6 +1075,8 @@ policy_ws carve_policy(char* base, int32_t nq, int32_t hq, int64_t nk) {
   w.code = reinterpret_cast<int32_t*>(take(4 * nk));
   w.blk = reinterpret_cast<int32_t*>(take(4 * ((nk + 255) / 256)));
   w.canon_self = reinterpret_cast<float*>(take(4 * static_cast<int64_t>(nq) * hq));
+  w.ngroups = 8 * ((nk + 31) / 32);
+  w.grp = reinterpret_cast<int32_t*>(take(4 * w.ngroups));
   w.bytes = off;
   return w;
 }
@@ -1065,8 +1152,9 @@ extern "C" int cs_ccpe_prefill_policy_bf16(const cs_ccpe_args* a, void* workspac
   CS_REQUIRE(a->kpos == nullptr, "the MFMA policy prefill takes the default key coordinates 0..nk-1");
   CS_REQUIRE(!a->attn_mask.data && !a->vis_mask.data && !a->fixed_pos.data && !a->pos_out.data,
              "the MFMA policy prefill takes no masks, fixed positions or position output");
-  CS_REQUIRE(a->sel_rows && a->fixed_keys, "the MFMA policy prefill needs the selected-row lowering");
   const bool canon = a->canonical.data != nullptr;
+  CS_REQUIRE((a->sel_rows && a->fixed_keys) || (!a->sel_rows && !a->fixed_keys && canon),
+             "the MFMA policy prefill needs the selected-row lowering, a canonical profile or both");
   if (canon) {
     const cs_view& c = a->canonical;
     CS_REQUIRE(c.ndim == 3 && c.shape[0] == qv.shape[1] && c.dtype == CS_F32 && a->q_ord && a->k_ord &&
@@ -1112,6 +1200,17 @@ extern "C" int cs_ccpe_prefill_policy_bf16(const cs_ccpe_args* a, void* workspac
                        a->k_ord, a->qpos, nq, hq, nk, w.canon_self);
     p.canon_self = w.canon_self;
     p.q_ord = a->q_ord;
+    // fixed rows that are not selected read their canonical cells directly
+    const bool aligned = c.stride[2] == 1 && c.stride[0] % 4 == 0 && c.stride[1] % 4 == 0 &&
+                         (reinterpret_cast<uintptr_t>(c.data) % 16) == 0;
+    hipLaunchKernelGGL(policy_groups_kernel, dim3(static_cast<uint32_t>((w.ngroups + 255) / 256)), dim3(256), 0,
+                       s, w.code, static_cast<int64_t>(nk), aligned ? 1 : 0, w.ngroups, w.grp);
+    p.canon = static_cast<const float*>(c.data);
+    p.c_s0 = c.stride[0];
+    p.c_s1 = c.stride[1];
+    p.c_s2 = c.stride[2];
+    p.grp = w.grp;
+    p.code = w.code;
   }
   std::unique_lock<std::mutex> side_lock(g_side_mutex, std::defer_lock);
   side_lane* side = nullptr;

@@ -49,6 +49,14 @@ struct prefill_params {
   const uint32_t* fixed_bits;
   const float* canon_self;  // [hq, nq]
   const int64_t* q_ord;     // -1: not a fixed row
+  // CanonicalPositionPolicy for fixed rows that are not selected: every fixed
+  // key takes canonical[head][q_ord[row]][ordinal of the key] (strides in
+  // floats); grp[g] is the ordinal of key 4g when keys 4g .. 4g+3 are fixed
+  // with consecutive ordinals (else -1), code[j] the ordinal of fixed key j.
+  const float* canon;
+  int64_t c_s0, c_s1, c_s2;
+  const int32_t* grp;
+  const int32_t* code;
 };
 
 namespace {
@@ -57,6 +65,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4_tr;
 #define CS_LDS __attribute__((address_space(3)))
 
@@ -117,6 +126,23 @@ __device__ inline void lds_dma16_s(uint32_t voff, uint64_t sbase, uint32_t lds) 
   const uint64_t base = (static_cast<uint64_t>(hi) << 32) | lo;
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
                : : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(base) : "memory", "m0");
+}
+
+// Element i of a read-only array at a wave-uniform index, through the
+// constant address space: a scalar load, which the vector-memory waits of
+// the tile loop do not count.
+template <typename T>
+__device__ inline T uniform_load(const T* ptr, int64_t i) {
+  return ((const __attribute__((address_space(4))) T*)ptr)[i];
+}
+
+// 16 bytes of global memory into registers without the compiler tracking the
+// load: the caller waits for it with an explicit vmcnt wait and then passes
+// the value through an empty asm before its first use.
+__device__ inline floatx4 load_f4_untracked(const float* ptr) {
+  floatx4 r;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(ptr) : "memory");
+  return r;
 }
 
 // LDS byte address of a __shared__ object (the generic -> LDS conversion,

@@ -626,16 +626,18 @@ def cope_attention(
         keep += [sel_rows, fixed_keys]
         args.sel_rows = ptr(sel_rows)
         args.fixed_keys = ptr(fixed_keys)
-    # The MFMA reuse-call path; the flags word it leaves is read once here and
-    # serves every check below (one wait for the device per call).
+    # The MFMA reuse-call path (a SelectedAssociationPolicy, a canonical
+    # profile or both); the flags word it leaves is read once here and serves
+    # every check below (one wait for the device per call).
     flags_value = None
-    if (selected is not None and default_keys
+    if ((selected is not None or canonical is not None) and default_keys
             and _policy_fast_ok(query, key, value, e, cope, amask, visibility_mask, fixed_positions,
                                 return_positions, lowered if canonical is not None else None)
             and _policy_prefill(args, query, key, ck)):
         flags_value = _hip.read_flags(ck.flags)[0]
         if flags_value & _hip.FLAG_POLICY_GENERIC:
-            # a fixed query row that is not selected: the generic kernel runs the call
+            # more fixed/dynamic boundary keys than the path checker holds: the
+            # generic kernel runs the call
             ck.flags.bitwise_and_(~_hip.FLAG_POLICY_GENERIC)
             if chunk_flags is not None:
                 chunk_flags.zero_()
@@ -680,7 +682,7 @@ def _raise_policy_errors(ck: _Checks, chunk_flags: Tensor, lowered, flags_value:
 def _policy_fast_ok(query, key, value, e, cope, amask, visibility_mask, fixed_positions, return_positions,
                     lowered) -> bool:
     """The reuse call of runtime.py:576-609 on MFMA: the dense fast path's
-    conditions with a SelectedAssociationPolicy and, if any, an fp32 profile."""
+    conditions with a SelectedAssociationPolicy, an fp32 profile or both."""
     if not _fast_path_ok(query, key, value, e, cope, amask, visibility_mask, fixed_positions, None, None,
                          return_positions):
         return False
@@ -689,8 +691,9 @@ def _policy_fast_ok(query, key, value, e, cope, amask, visibility_mask, fixed_po
 
 def _policy_prefill(args, query: Tensor, key: Tensor, ck: _Checks) -> bool:
     """Launch cs_ccpe_prefill_policy_bf16 into args.out; False (nothing
-    launched) for a layout it does not take.  A fixed query row that is not
-    selected sets FLAG_POLICY_GENERIC: the caller then runs the generic kernel."""
+    launched) for a layout it does not take.  A plan with more fixed/dynamic
+    boundary keys than the path checker holds sets FLAG_POLICY_GENERIC: the
+    caller then runs the generic kernel."""
     device = ck.device
     lib = _hip.load()
     nq, hq, nk = query.shape[0], query.shape[1], key.shape[0]

@@ -85,9 +85,9 @@ enum cs_flag {
   CS_FLAG_ROW_LOST = 1 << 20,         /* an active token in neither the previous rows nor the snapshot */
   CS_FLAG_ROWS_UNSORTED = 1 << 21,    /* a token list is not ascending and distinct */
   CS_FLAG_ROW_INDEX = 1 << 22,        /* a gather index outside the source rows */
-  /* cs_ccpe_prefill_policy_bf16: the call needs cs_ccpe_attention instead (a
-     fixed query row that is not selected, or more dynamic keys beside fixed
-     keys than the path checker holds); its results are to be discarded */
+  /* cs_ccpe_prefill_policy_bf16: the call needs cs_ccpe_attention instead
+     (more dynamic keys beside fixed keys than the path checker holds); its
+     results are to be discarded */
   CS_FLAG_POLICY_GENERIC = 1 << 23
 };
 
@@ -158,23 +158,29 @@ typedef struct cs_ccpe_args {
 int cs_ccpe_attention(const cs_ccpe_args* args, void* stream);
 
 /* cope_attention with the two runtime policies on bf16 MFMA: the reuse call of
- * runtime.py:576-609 (CanonicalPositionPolicy, attention.py:18-57, with
+ * runtime.py:576-609 (CanonicalPositionPolicy, attention.py:18-57, and/or
  * SelectedAssociationPolicy, attention.py:60-72, in updated_and_self mode)
- * over dense K/V.  Same lowered data as cs_ccpe_attention; supported when
- * q/k/v/out are bf16 with head dim 128, e is fp32 [128, P <= 128], kpos is
- * NULL (key coordinates 0..nk-1), the GQA group divides 32, there are no
- * masks, fixed positions or position output, sel_rows/fixed_keys are given
- * and canonical (optional) is fp32; otherwise CS_EUNSUPPORTED.
+ * over dense K/V: the selective calls, the calibration-layer call (a profile
+ * and no selection yet, runtime.py:448-454) and selected_attention "all".
+ * Same lowered data as cs_ccpe_attention; supported when q/k/v/out are bf16
+ * with head dim 128, e is fp32 [128, P <= 128], kpos is NULL (key coordinates
+ * 0..nk-1), the GQA group divides 32, there are no masks, fixed positions or
+ * position output, and either sel_rows/fixed_keys are given (canonical
+ * optional) or both are NULL and canonical is given (the fixed keys are then
+ * those with a profile ordinal); canonical is fp32; otherwise CS_EUNSUPPORTED.
  *
  * A selected fixed row sees no fixed key but its own, so the kernel reads one
  * canonical cell per (head, row) and skips tiles of fixed keys once a row's
- * positions have saturated.  The transform's bounds check (every fixed
- * key) and, with strict != 0, the path checks of the substituted row (over
- * fixed keys and the dynamic keys beside them; contextual cells always pass)
- * run in a checker launch over the canonical rows and set the same chunk
- * bits as cs_ccpe_attention.  When some fixed query row is not selected, the
- * call sets CS_FLAG_POLICY_GENERIC in *flags and the caller runs
- * cs_ccpe_attention instead.  workspace: at least
+ * positions have saturated.  A fixed row that is not selected sees every
+ * fixed key at canonical[h][q_ord][k_ord]: the kernel reads those cells tile
+ * by tile, 16 bytes per run of 4 keys where the profile allows.  The
+ * transform's bounds check (every fixed key) and, with strict != 0, the path
+ * checks of the substituted row (over fixed keys and the dynamic keys beside
+ * them; contextual cells always pass) run in a checker launch over the
+ * canonical rows and set the same chunk bits as cs_ccpe_attention.  When the
+ * plan has more boundary keys than the checker holds, the call sets
+ * CS_FLAG_POLICY_GENERIC in *flags and the caller runs cs_ccpe_attention
+ * instead.  workspace: at least
  * cs_ccpe_prefill_policy_workspace_bytes(nq, Hq, nk) bytes, 256-byte aligned,
  * any contents. */
 int64_t cs_ccpe_prefill_policy_workspace_bytes(int32_t nq, int32_t hq, int64_t nk);

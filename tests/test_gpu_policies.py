@@ -72,8 +72,9 @@ def contextual(q: np.ndarray, k: np.ndarray, rows: np.ndarray) -> np.ndarray:
 
 
 def oracle_run(q, k, v, e, rows, plan, canonical, ordinals, strict, selected, chunk):
-    """The reference's per-chunk evaluation with the policies, on the oracle.
-    Returns ("ok", out, trace) or ("error", type, message)."""
+    """The reference's per-chunk evaluation with the policies, on the oracle
+    (no visibility transform when ``selected`` is None).  Returns ("ok", out,
+    trace) or ("error", type, message)."""
     fixed = list(plan.fixed_indices)
     ordinal = {p: i for i, p in enumerate(fixed)}
     known = set(ordinals)
@@ -89,8 +90,8 @@ def oracle_run(q, k, v, e, rows, plan, canonical, ordinals, strict, selected, ch
 
     try:
         out, trace = orc.cope_attention(q[rows], k, v, e, rows, positions_transform=positions_transform,
-                                        visibility_transform=visibility_transform, query_chunk_size=chunk,
-                                        return_positions=True)
+                                        visibility_transform=visibility_transform if selected is not None else None,
+                                        query_chunk_size=chunk, return_positions=True)
     except orc.PathError as err:
         return ("error", CCPEPositionError, orc.PATH_MESSAGES[err.kind])
     except ValueError as err:

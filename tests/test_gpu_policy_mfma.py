@@ -68,7 +68,8 @@ def scenario(seed, *, a, dyn, b, shift=0, perturb=0.0, drop=0, n_sel=60):
 
 
 def device_run(q, k, v, e, rows, plan, profile, mode, selected, chunk, device, monkeypatch):
-    """cope_attention on the device -> (decision, kernels called)."""
+    """cope_attention on the device -> (decision, kernels called); no
+    visibility transform when ``selected`` is None."""
     called = []
     real = position_module.call
 
@@ -81,7 +82,8 @@ def device_run(q, k, v, e, rows, plan, profile, mode, selected, chunk, device, m
     with torch.no_grad():
         cope.position_embeddings.copy_(torch.from_numpy(e))
     policy = CanonicalPositionPolicy(plan, profile, "ckpt", mode=mode) if profile is not None else None
-    visibility = SelectedAssociationPolicy(plan.fixed_indices, torch.tensor(selected, device=device))
+    visibility = (SelectedAssociationPolicy(plan.fixed_indices, torch.tensor(selected, device=device))
+                  if selected is not None else None)
     as_bf16 = lambda x: torch.from_numpy(x).to(device=device, dtype=torch.bfloat16)  # noqa: E731
     try:
         out = cope_attention(as_bf16(q[rows]), as_bf16(k), as_bf16(v), cope, torch.from_numpy(rows).to(device),
@@ -163,17 +165,77 @@ def test_selected_rows_without_profile(device, monkeypatch):
     assert "cs_ccpe_attention" not in called
 
 
-def test_unselected_fixed_row_runs_the_generic_kernel(device, monkeypatch):
+def test_unselected_fixed_row_on_the_mfma_path(device, monkeypatch):
     """A fixed query row outside the selected set sees every fixed key with
-    its canonical position: the MFMA path flags the call and the generic
-    kernel runs it instead, with the oracle's result."""
+    its canonical position, beside selected rows that see only their own
+    fixed key: one MFMA call, the oracle's result."""
     q, k, v, e, rows, plan, canonical, ordinals, sel = scenario(10, a=300, dyn=100, b=400)
     partial = sel[1:]                       # sel[0] stays an active fixed row, now not selected
     expected = oracle_run(q, k, v, e, rows, plan, canonical, ordinals, False, partial, 64)
     actual, called = device_run(q, k, v, e, rows, plan, profile_for(plan, canonical, ordinals),
                                 "mixed_bias_override", partial, 64, device, monkeypatch)
     compare(expected, actual)
-    assert "cs_ccpe_attention" in called
+    assert "cs_ccpe_attention" not in called, called
+
+
+MID = dict(a=300, dyn=100, b=400, n_sel=60)
+# fixed/dynamic boundaries off the 4-key grid: key groups that are partly
+# fixed, and chunk B's ordinals not a multiple of 4 (the key-by-key reads)
+ODD = dict(a=301, dyn=99, b=403, n_sel=60)
+
+CANON_CASES = {
+    # name: (layout, seed, shift, perturb, drop, mode, chunk, rows, expected decision)
+    # rows "all": the calibration-layer call, every row in order with no
+    # selection yet (runtime.py:448-454); "active": selected_attention "all",
+    # the active rows with no visibility transform
+    "calibration_strict": (MID, 41, 0, 0.0, 0, "strict_contextual", 64, "all", "ok"),
+    "calibration_shifted_mixed": (MID, 42, 24, 0.0, 0, "mixed_bias_override", 64, "all", "ok"),
+    "calibration_perturbed_mixed": (MID, 43, 0, 0.5, 0, "mixed_bias_override", 128, "all", "ok"),
+    "calibration_perturbed_strict": (MID, 44, 0, 0.05, 0, "strict_contextual", 64, "all", "error"),
+    "all_attention_strict": (BIG, 45, 0, 0.0, 0, "strict_contextual", 48, "active", "ok"),
+    "all_attention_shifted_mixed": (BIG, 46, 16, 0.0, 0, "mixed_bias_override", 64, "active", "ok"),
+    "all_attention_untraced_strict": (BIG, 47, 0, 0.0, 4, "strict_contextual", 32, "active", "error"),
+    "odd_boundaries_calibration_mixed": (ODD, 48, 0, 0.3, 0, "mixed_bias_override", 64, "all", "ok"),
+    "odd_boundaries_strict": (ODD, 49, 0, 0.0, 0, "strict_contextual", 64, "all", "ok"),
+    "odd_boundaries_shifted_strict": (ODD, 49, 8, 0.0, 0, "strict_contextual", 64, "all", "error"),
+    "small_boundary_gap_strict": (SMALL, 20, 8, 0.0, 0, "strict_contextual", 16, "all", "error"),
+    "small_boundary_mixed": (SMALL, 20, 8, 0.0, 0, "mixed_bias_override", 16, "all", "ok"),
+    "budget_strict": (BUDGET, 50, 0, 0.0, 0, "strict_contextual", 64, "all", "ok"),
+}
+
+
+@pytest.mark.parametrize("name", list(CANON_CASES))
+def test_canonical_only_call_matches_oracle(device, monkeypatch, name):
+    """A CanonicalPositionPolicy with no SelectedAssociationPolicy on the MFMA
+    path: every fixed row reads all its fixed x fixed cells from the profile,
+    dynamic rows keep contextual positions."""
+    layout, seed, shift, perturb, drop, mode, chunk, which, want = CANON_CASES[name]
+    q, k, v, e, rows, plan, canonical, ordinals, _ = scenario(seed, shift=shift, perturb=perturb, drop=drop,
+                                                              **layout)
+    if which == "all":
+        rows = np.arange(q.shape[0])
+    strict = mode == "strict_contextual"
+    expected = oracle_run(q, k, v, e, rows, plan, canonical, ordinals, strict, None, chunk)
+    assert expected[0] == want, expected[:3] if expected[0] == "error" else "ok"
+    actual, called = device_run(q, k, v, e, rows, plan, profile_for(plan, canonical, ordinals), mode, None, chunk,
+                                device, monkeypatch)
+    compare(expected, actual)
+    assert "cs_ccpe_attention" not in called, called
+
+
+def test_canonical_only_strided_profile(device, monkeypatch):
+    """A profile whose key stride is not 1 (a transposed view): every cell is
+    read key by key."""
+    q, k, v, e, _, plan, canonical, ordinals, _ = scenario(51, **MID)
+    rows = np.arange(q.shape[0])
+    expected = oracle_run(q, k, v, e, rows, plan, canonical, ordinals, True, None, 64)
+    profile = profile_for(plan, canonical, ordinals)
+    swapped = profile.canonical_positions.transpose(1, 2).contiguous().transpose(1, 2)
+    assert swapped.stride(2) != 1 and torch.equal(swapped, profile.canonical_positions)
+    object.__setattr__(profile, "canonical_positions", swapped)
+    actual, called = device_run(q, k, v, e, rows, plan, profile, "strict_contextual", None, 64, device, monkeypatch)
+    compare(expected, actual)
+    assert "cs_ccpe_attention" not in called, called
 
 
 def test_policy_errors_in_chunk_order(device, monkeypatch):
