@@ -613,6 +613,85 @@ def reuse_measure(device, steps: int = 5) -> dict:
     }
 
 
+def calibration_measure(device, steps: int = 5) -> dict:
+    """The calibration-layer reuse call (runtime.py:448-454, 594-600): before
+    WCA has selected rows, every row of the request attends with a
+    CanonicalPositionPolicy and no SelectedAssociationPolicy (the same call
+    is every layer's under selected_attention "all").  2 reused chunks of 2048
+    tokens (4096 fixed) and a 256-token recomputed question, all 4352 rows in
+    order, 32q/8kv heads x 128, bf16 Q/K/V ~ N(0, 1), CoPE P = 64 (table
+    N(0, 0.1)), strict_contextual positions from a per-head [32, 4096, 4096]
+    fp32 profile (head h: a path of 0.4 + 0.01 h per token; 2 GiB, no
+    broadcast).  Timed: cope_attention on the MFMA policy path (``steps``
+    calls) and, once, the same call on the generic kernel (explicit key
+    coordinates); the two outputs are compared."""
+    import torch
+
+    from cacheslide_amd import CCPEProfile, CanonicalPositionPolicy, ChunkIdentity, CoPE, RequestPlan, cope_attention
+
+    CH, CHUNKS, DYN, HQ, HKV, D, P = 2048, 2, 256, 32, 8, 128, 64
+    F = CH * CHUNKS
+    n = F + DYN
+    spec = [{"id": f"C{i}", "role": "reuse", "start": i * CH, "end": (i + 1) * CH} for i in range(CHUNKS)]
+    spec.append({"id": "question", "role": "recompute", "start": F, "end": n})
+    plan = RequestPlan.parse({"version": 1, "namespace": "bench", "task_id": "calibration", "operation": "reuse",
+                              "chunks": spec}, [(11 * i) % 32000 for i in range(n)])
+    gen = torch.Generator(device=device).manual_seed(6306)
+    q = torch.randn((n, HQ, D), generator=gen, device=device).to(torch.bfloat16)
+    k = torch.randn((n, HKV, D), generator=gen, device=device).to(torch.bfloat16)
+    v = torch.randn((n, HKV, D), generator=gen, device=device).to(torch.bfloat16)
+    cope = CoPE(D, P, device=device)
+    with torch.no_grad():
+        cope.position_embeddings.copy_(torch.randn((D, P), generator=seed_gen(7, 1)) * 0.1)
+    ords = torch.arange(F, device=device, dtype=torch.float32)
+    canon = torch.empty((HQ, F, F), dtype=torch.float32, device=device)
+    for h in range(HQ):
+        canon[h] = ((ords[:, None] - ords[None, :] + 1) * (0.4 + 0.01 * h)).clamp_(0, P - 1)
+        canon[h].masked_fill_(ords[None, :] > ords[:, None], 0.0)
+    profile = CCPEProfile(trained_profile_version="v1", checkpoint_id="ckpt",
+                          chunks=tuple(ChunkIdentity(*c) for c in plan.fixed_layout),
+                          query_positions=torch.arange(F), key_positions=torch.arange(F),
+                          canonical_positions=canon, max_positions=P, histogram_bin_width=0.25, sample_count=1)
+    policy = CanonicalPositionPolicy(plan, profile, "ckpt", mode="strict_contextual")
+    rows = torch.arange(n, device=device)
+    keys = torch.arange(n, device=device)
+
+    def run(explicit_keys=False):
+        return cope_attention(q, k, v, cope, rows, keys if explicit_keys else None, positions_transform=policy,
+                              query_chunk_size=64)
+
+    out = run()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        out = run()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    t0 = time.perf_counter()
+    ref = run(explicit_keys=True)
+    torch.cuda.synchronize()
+    ms_generic = (time.perf_counter() - t0) * 1e3
+    err = float((out.float() - ref.float()).abs().max())
+    causal = float((rows.double() + 1).sum())
+    flops = 4.0 * HQ * D * causal + 2.0 * HQ * D * P * n
+    canon_bytes = HQ * F * (F + 1) // 2 * 4           # the causal fixed x fixed cells, once each
+    del canon, profile, policy
+    torch.cuda.empty_cache()
+    return {
+        "workload": "cope_attention calibration-layer call: 4352 keys (2 reused chunks x 2048 + 256 recomputed), "
+                    "all 4352 rows, 32q/8kv heads x 128, bf16, P=64, strict per-head canonical profile "
+                    "[32, 4096, 4096] fp32, no selected set",
+        "ms_per_call": round(ms, 3),
+        "generic_ms_per_call": round(ms_generic, 2),
+        "speedup_vs_generic": round(ms_generic / ms, 1),
+        "max_abs_diff_vs_generic": round(err, 5),
+        "reference_flop_per_call": flops,
+        "reference_equivalent_TFLOPs": round(flops / (ms * 1e-3) / 1e12, 1),
+        "canonical_bytes_read": canon_bytes,
+        "canonical_GBs_whole_call": round(canon_bytes / (ms * 1e-3) / 1e9, 1),
+    }
+
+
 def note(message: str) -> None:
     """Progress line on stderr (stdout carries only the JSON record)."""
     print(f"bench: {message}", file=sys.stderr, flush=True)
@@ -1089,6 +1168,9 @@ def main() -> int:
     if not args.no_reuse:
         record["reuse"] = reuse_measure(device)
         note(f"reuse: {record['reuse']['ms_per_call']} ms/call (generic {record['reuse']['generic_ms_per_call']})")
+        record["calibration_call"] = calibration_measure(device)
+        note(f"calibration call: {record['calibration_call']['ms_per_call']} ms/call "
+             f"(generic {record['calibration_call']['generic_ms_per_call']})")
     if not args.no_slide:
         try:
             record["slide"] = slide_measure(device, max(3, args.steps // 10), args.slide_layers)

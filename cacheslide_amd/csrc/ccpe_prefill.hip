@@ -85,6 +85,7 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
   // of keys [bt_lo, bt_lo + kBtWindow)
   __shared__ int32_t bt_lds[kBtWindow];
   __shared__ int64_t wg_max_pos;
+  __shared__ int32_t quiet_lds[WAVES];  // POLICY: the wave's columns all skip tiles of fixed keys
   // [32 WAVES columns][tab_stride] QE log2(e), fp32
   extern __shared__ __align__(16) float tab[];
 
@@ -390,9 +391,14 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
   };
   // wait until this wave's loads of the current tile have landed, with the
   // next tile's loads (2 kInstr of them) possibly still in flight
-  auto wait_tile = [&](bool next_in_flight) {
-    if (next_in_flight)
+  // (and, with canonical cells fetched after those loads, those 4 as well)
+  auto wait_tile = [&](bool next_in_flight, bool cells_after) {
+    if (next_in_flight && cells_after)
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kInstr + 4));
+    else if (next_in_flight)
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kInstr));
+    else if (cells_after)
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(4));
     else
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   };
@@ -416,15 +422,16 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
   // element offset of this lane's transposed V read within a stage
   const int vrd_off = 512 * h + 32 * (2 * ((lane >> 4) & 1) + ((j16 & 3) >> 1)) + 8 * (j16 >> 2) + 4 * (j16 & 1);
   // Canonical cells of a tile for the columns of fixed rows that are not
-  // selected, issued before the tile's K/V loads so that the wait for them
-  // leaves those loads in flight.  Per run of 4 keys (8 j4 + 4h + 0..3):
+  // selected, issued before the tile's barrier (behind the loads of the next
+  // tile, ahead of those of the tile after) so that their latency overlaps
+  // the barrier and the score MFMAs.  Per run of 4 keys (8 j4 + 4h + 0..3):
   // one 16-byte load when the run is a whole aligned group (cgo >= 0, its
   // first ordinal), else the zero record (the cells are then read key by key).
   const float* zero_f = reinterpret_cast<const float*>(g_zero_record);
-  auto fetch = [&](int t, floatx4 (&cv)[4], int (&cgo)[4]) {
+  auto fetch = [&](int t, floatx4 (&cv)[4], int (&cgo)[4]) -> bool {
     if constexpr (POLICY) {
-      if (!canon_wave || t * kTileN > wmax32) return;
-      if (uniform_load(p.fixed_bits, t) == 0u) return;
+      if (!canon_wave || t * kTileN > wmax32) return false;
+      if (uniform_load(p.fixed_bits, t) == 0u) return false;
 #pragma unroll
       for (int j4 = 0; j4 < 4; ++j4) {
         const int32_t g0 = uniform_load(p.grp, 8 * static_cast<int64_t>(t) + 2 * j4);
@@ -433,7 +440,9 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
         cgo[j4] = go;
         cv[j4] = load_f4_untracked(go >= 0 ? canon_row + go : zero_f);
       }
+      return true;
     }
+    return false;
   };
   // (dma_after: this tile's K/V loads were issued after the canonical cells)
   auto compute = [&](int t, const uint4* kst, const uint4* vst, floatx4 (&cv)[4], const int (&cgo)[4],
@@ -656,6 +665,34 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
         o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[4 * ks + db], ks ? pb1 : pb0, o[db], 0, 0, 0);
   };
 
+  // POLICY: a tile of fixed keys adds nothing once every column of the
+  // workgroup is a selected row with saturated positions (see compute); its
+  // loads are then not issued.  Each wave publishes that state before the
+  // tile barrier and reads every wave's behind it, so the decision, like the
+  // state (carry only grows), holds for the whole workgroup from then on.
+  bool wg_quiet = false;
+  auto publish_quiet = [&]() __attribute__((always_inline)) {
+    if constexpr (POLICY) {
+      const bool q = __all(!row_ok || (sel_col && carry >= top));
+      if (lane == 0) quiet_lds[wave] = q ? 1 : 0;
+    }
+  };
+  auto read_quiet = [&]() __attribute__((always_inline)) {
+    if constexpr (POLICY) {
+      int q = 1;
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) q &= quiet_lds[w];
+      wg_quiet = __builtin_amdgcn_readfirstlane(q) != 0;
+    }
+  };
+  auto load_tile = [&](int u, int stage) __attribute__((always_inline)) -> bool {
+    if constexpr (POLICY) {
+      if (wg_quiet && uniform_load(p.fixed_bits, u) == 0xFFFFFFFFu) return false;
+    }
+    issue(u, stage);
+    return true;
+  };
+
   // ---- main loop: windows of tiles right to left; inside a window, tiles right
   // to left through three LDS stages with the loads two tiles ahead.  Each wave
   // waits for its own loads of a tile before the one barrier of the tile, which
@@ -680,27 +717,35 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
       preload(thi - 1);
     }
     issue(thi - 1, 0);
-    if (thi - 2 >= tlo) issue(thi - 2, 1);
+    bool iss1 = thi - 2 >= tlo;  // the loads of the next tile to compute were issued
+    if (iss1) issue(thi - 2, 1);
     for (int t = thi - 1; t >= tlo; t -= 3) {
-      wait_tile(t - 1 >= tlo);
-      __syncthreads();
       floatx4 cv[4];
       int cgo[4];
-      fetch(t, cv, cgo);
-      if (t - 2 >= tlo) issue(t - 2, 2);
-      compute(t, st0.k, st0.v, cv, cgo, t - 2 >= tlo);
+      bool got = fetch(t, cv, cgo);
+      wait_tile(iss1, got);
+      publish_quiet();
+      __syncthreads();
+      read_quiet();
+      const bool iss2 = t - 2 >= tlo && load_tile(t - 2, 2);
+      compute(t, st0.k, st0.v, cv, cgo, iss2);
       if (t - 1 < tlo) break;
-      wait_tile(t - 2 >= tlo);
+      got = fetch(t - 1, cv, cgo);
+      wait_tile(iss2, got);
+      publish_quiet();
       __syncthreads();
-      fetch(t - 1, cv, cgo);
-      if (t - 3 >= tlo) issue(t - 3, 0);
-      compute(t - 1, st1.k, st1.v, cv, cgo, t - 3 >= tlo);
+      read_quiet();
+      const bool iss3 = t - 3 >= tlo && load_tile(t - 3, 0);
+      compute(t - 1, st1.k, st1.v, cv, cgo, iss3);
       if (t - 2 < tlo) break;
-      wait_tile(t - 3 >= tlo);
+      got = fetch(t - 2, cv, cgo);
+      wait_tile(iss3, got);
+      publish_quiet();
       __syncthreads();
-      fetch(t - 2, cv, cgo);
-      if (t - 4 >= tlo) issue(t - 4, 1);
-      compute(t - 2, st2.k, st2.v, cv, cgo, t - 4 >= tlo);
+      read_quiet();
+      const bool iss4 = t - 4 >= tlo && load_tile(t - 4, 1);
+      compute(t - 2, st2.k, st2.v, cv, cgo, iss4);
+      iss1 = iss4;
     }
     thi = tlo;
   }

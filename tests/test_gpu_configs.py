@@ -306,3 +306,95 @@ def test_reuse_call_16k_mfma_path_matches_generic_kernel(device, monkeypatch):
     assert "cs_ccpe_attention" in called
     assert fast.shape == (rows.numel(), HQ, D) and bool(torch.isfinite(fast.float()).all())
     assert_close_bf16(fast, ref.float().cpu().numpy())
+    # sampled rows against the oracle: fixed rows across the chunks (their own
+    # canonical cell and the keys they still see) and question rows
+    pick = np.unique(np.concatenate([np.arange(0, len(sel), 311), [len(sel) - 1],
+                                     len(sel) + np.array([0, 1, 97, 200, DYN - 1])]))
+    sampled_pos = rows.cpu().numpy()[pick]
+    fixed_ords = [int(p) for p in sampled_pos if p < F]
+    expected = _oracle_sampled(q_all, k, v, cope, sampled_pos, plan, fixed_ords,
+                               lambda o: np.clip((o[:, None] - np.arange(F)[None, :] + 1) * 0.5, 0, P - 1), HQ,
+                               True, sel.numpy(), 64)
+    assert expected[0] == "ok", expected[:3]
+    assert_close_bf16(fast[torch.from_numpy(pick).to(device)], expected[1])
+
+
+def _oracle_sampled(q_all, k, v, cope, sampled_pos, plan, fixed_ords, path_rows, heads, strict, selected, chunk):
+    """The oracle's per-chunk evaluation of the policies (oracle/ccpe.py) for a
+    few query rows at positions ``sampled_pos``: the profile rows they need
+    (fixed ordinals ``fixed_ords``, head-independent ``path_rows(ordinals)`` ->
+    [len, F], or [heads, len, F] when it returns 3 dimensions), causal
+    masking of future keys as the profile's zeros."""
+    from tests.test_gpu_policies import oracle_run
+
+    ords = np.array(sorted(set(fixed_ords)), dtype=np.int64)
+    cells = path_rows(ords).astype(np.float32) if len(ords) else np.zeros((0, len(plan.fixed_indices)), np.float32)
+    if cells.ndim == 2:
+        cells = np.broadcast_to(cells, (heads,) + cells.shape)
+    fixed = np.array(plan.fixed_indices)
+    cells = np.where(fixed[None, None, :] > fixed[ords][None, :, None], np.float32(0), cells)
+    f32 = lambda x: x.float().cpu().numpy()  # noqa: E731
+    e = cope.position_embeddings.detach().float().cpu().numpy()
+    return oracle_run(f32(q_all), f32(k), f32(v), e, np.asarray(sampled_pos), plan, np.ascontiguousarray(cells),
+                      [int(o) for o in ords], strict, selected, chunk)
+
+
+def test_calibration_call_4k_mfma_path_matches_oracle(device, monkeypatch):
+    """The calibration-layer reuse call (runtime.py:448-454, 594-600): every
+    row of the request with a CanonicalPositionPolicy and no selection yet.
+    2 reused chunks x 2048 + a 256-token question, all 4352 rows in order,
+    32q/8kv x 128, bf16, P = 64, a per-head strict profile [32, 4096, 4096]
+    fp32 (head h: 0.4 + 0.01 h per token).  The MFMA path's output is finite,
+    sampled rows equal the oracle's and the whole output equals the generic
+    kernel's, within the bf16 tolerance."""
+    import cacheslide_amd.position as position_module
+    from cacheslide_amd import CCPEProfile, CanonicalPositionPolicy, ChunkIdentity, RequestPlan, cope_attention
+
+    CH, CHUNKS, DYN, HQ, HKV, D, P = 2048, 2, 256, 32, 8, 128, 64
+    F = CH * CHUNKS
+    n = F + DYN
+    spec = [{"id": f"C{i}", "role": "reuse", "start": i * CH, "end": (i + 1) * CH} for i in range(CHUNKS)]
+    spec.append({"id": "question", "role": "recompute", "start": F, "end": n})
+    plan = RequestPlan.parse({"version": 1, "namespace": "test", "task_id": "calibration", "operation": "reuse",
+                              "chunks": spec}, [(11 * i) % 32000 for i in range(n)])
+    gen = torch.Generator(device=device).manual_seed(6206)
+    q = torch.randn((n, HQ, D), generator=gen, device=device).to(torch.bfloat16)
+    k = torch.randn((n, HKV, D), generator=gen, device=device).to(torch.bfloat16)
+    v = torch.randn((n, HKV, D), generator=gen, device=device).to(torch.bfloat16)
+    cope = CoPE(D, P, device=device)
+    with torch.no_grad():
+        cope.position_embeddings.copy_(torch.randn((D, P), generator=torch.Generator().manual_seed(63)) * 0.1)
+    rates = 0.4 + 0.01 * np.arange(HQ)
+    ords = torch.arange(F, device=device, dtype=torch.float32)
+    canon = torch.empty((HQ, F, F), dtype=torch.float32, device=device)
+    for h in range(HQ):
+        canon[h] = ((ords[:, None] - ords[None, :] + 1) * float(rates[h])).clamp_(0, P - 1)
+        canon[h].masked_fill_(ords[None, :] > ords[:, None], 0.0)
+    profile = CCPEProfile(trained_profile_version="v1", checkpoint_id="ckpt",
+                          chunks=tuple(ChunkIdentity(*c) for c in plan.fixed_layout),
+                          query_positions=torch.arange(F), key_positions=torch.arange(F),
+                          canonical_positions=canon, max_positions=P, histogram_bin_width=0.25, sample_count=1)
+    policy = CanonicalPositionPolicy(plan, profile, "ckpt", mode="strict_contextual")
+    rows = torch.arange(n, device=device)
+    called = []
+    real = position_module.call
+
+    def spy(name, *args):
+        called.append(name)
+        return real(name, *args)
+
+    monkeypatch.setattr(position_module, "call", spy)
+    fast = cope_attention(q, k, v, cope, rows, None, positions_transform=policy, query_chunk_size=64)
+    assert "cs_ccpe_attention" not in called, called
+    assert fast.shape == (n, HQ, D) and bool(torch.isfinite(fast.float()).all())
+    pick = np.array([0, 1, 5, 63, 700, CH - 1, CH, CH + 333, F - 2, F - 1, F, F + 1, F + 128, n - 1])
+    expected = _oracle_sampled(
+        q, k, v, cope, pick, plan, [int(p) for p in pick if p < F],
+        lambda o: np.clip((o[None, :, None] - np.arange(F)[None, None, :] + 1) * rates[:, None, None], 0, P - 1),
+        HQ, True, None, 64)
+    assert expected[0] == "ok", expected[:3]
+    assert_close_bf16(fast[torch.from_numpy(pick).to(device)], expected[1])
+    ref = cope_attention(q, k, v, cope, rows, torch.arange(n, device=device), positions_transform=policy,
+                         query_chunk_size=64)
+    assert "cs_ccpe_attention" in called
+    assert_close_bf16(fast, ref.float().cpu().numpy())

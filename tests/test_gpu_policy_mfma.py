@@ -261,3 +261,56 @@ def test_policy_errors_in_chunk_order(device, monkeypatch):
         compare(expected, actual)
         assert actual[0] == "error", (mode, order)
         assert "cs_ccpe_attention" not in called
+
+
+def long_case(seed, *, low_gates=False, a=1200, dyn=160, b=1200):
+    """A calibration-layer call with long key walks: all rows, a
+    mixed_bias_override profile of one path per head (0.3 + 0.05 h per
+    token).  With ``low_gates`` the logits sit near -2.8 (gates ~0.06), so
+    contextual positions stay unsaturated for ~1000 keys."""
+    plan = make_plan(a, dyn, b)
+    n = a + dyn + b
+    rng = np.random.default_rng(seed)
+    if low_gates:
+        q = bf16_normal(rng, (n, HQ, D), 0.05) + 0.5
+        k = bf16_normal(rng, (n, HKV, D), 0.05) - 0.5
+        q = torch.from_numpy(q).to(torch.bfloat16).float().numpy()
+        k = torch.from_numpy(k).to(torch.bfloat16).float().numpy()
+    else:
+        q, k = bf16_normal(rng, (n, HQ, D)), bf16_normal(rng, (n, HKV, D))
+    v = bf16_normal(rng, (n, HKV, D))
+    e = (rng.standard_normal((D, P)) * 0.1).astype(np.float32)
+    nf = len(plan.fixed_indices)
+    rates = (0.3 + 0.05 * np.arange(HQ)).astype(np.float32)
+    o = np.arange(nf, dtype=np.float32)
+    canonical = np.clip((o[None, :, None] - o[None, None, :] + 1) * rates[:, None, None], 0, P - 1)
+    canonical = np.where(o[None, None, :] > o[None, :, None], np.float32(0), canonical).astype(np.float32)
+    return q, k, v, e, plan, canonical, list(range(nf))
+
+
+@pytest.mark.parametrize("low_gates", [False, True])
+def test_long_calibration_call_matches_generic_and_oracle(device, monkeypatch, low_gates):
+    """A 2560-token calibration-layer call (2 x 1200 fixed + 160 recomputed,
+    every row): the MFMA path equals the generic kernel on every row and the
+    oracle on sampled rows, with saturating and with slowly rising positions."""
+    q, k, v, e, plan, canonical, ordinals = long_case(60 + int(low_gates), low_gates=low_gates)
+    n = q.shape[0]
+    rows = np.arange(n)
+    profile = profile_for(plan, canonical, ordinals)
+    actual, called = device_run(q, k, v, e, rows, plan, profile, "mixed_bias_override", None, 64, device,
+                                monkeypatch)
+    assert actual[0] == "ok" and "cs_ccpe_attention" not in called, called
+    cope = CoPE(D, P, device=device)
+    with torch.no_grad():
+        cope.position_embeddings.copy_(torch.from_numpy(e))
+    as_bf16 = lambda x: torch.from_numpy(x).to(device=device, dtype=torch.bfloat16)  # noqa: E731
+    policy = CanonicalPositionPolicy(plan, profile, "ckpt", mode="mixed_bias_override")
+    ref = cope_attention(as_bf16(q), as_bf16(k), as_bf16(v), cope, torch.from_numpy(rows).to(device),
+                         torch.arange(n, device=device), positions_transform=policy, query_chunk_size=64)
+    assert_close_bf16(actual[1], ref.float().cpu().numpy())
+    pick = np.array([0, 700, 1199, 1200, 1300, 1359, 1360, 1800, 2400, n - 1])
+    fixed = np.array(plan.fixed_indices)
+    ords = sorted({int(np.searchsorted(fixed, p)) for p in pick if p in set(fixed.tolist())})
+    expected = oracle_run(q, k, v, e, pick, plan, canonical[:, ords], ords, False, None, 64)
+    assert expected[0] == "ok"
+    assert_close_bf16(actual[1][torch.from_numpy(pick).to(device)], expected[1])
