@@ -25,6 +25,7 @@ Prints one JSON line.  Only one GPU is used: --gpus above 1 exits.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -442,6 +443,11 @@ def read_ceilings(cache, table, B: int, HKV: int, BS: int, D: int, device) -> di
     from cacheslide_amd import _hip
 
     lib = _hip.load()
+    # the probe is measurement support: bound here, not in the package's binding
+    probe = lib.cs_read_probe
+    probe.restype = ctypes.c_int
+    probe.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32,
+                      ctypes.c_int32, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
     per = table.shape[1]
     chunk = BS * 2 * D * 2                                  # one KV head's records of a block
     splits = (per + 63) // 64
@@ -455,12 +461,12 @@ def read_ceilings(cache, table, B: int, HKV: int, BS: int, D: int, device) -> di
     stream = _hip.stream_of(device)
 
     def streamed():
-        _hip.check(lib.cs_read_probe(_hip.ptr(cache), nbytes, None, 0, 0, 0, _hip.ptr(sink), sink.numel(),
-                                     stream), "cs_read_probe")
+        _hip.check(probe(_hip.ptr(cache), nbytes, None, 0, 0, 0, _hip.ptr(sink), sink.numel(), stream),
+                   "cs_read_probe")
 
     def pattern():
-        _hip.check(lib.cs_read_probe(_hip.ptr(cache), nbytes, _hip.ptr(offsets), offsets.numel(), 64, chunk,
-                                     _hip.ptr(sink), sink.numel(), stream), "cs_read_probe")
+        _hip.check(probe(_hip.ptr(cache), nbytes, _hip.ptr(offsets), offsets.numel(), 64, chunk,
+                         _hip.ptr(sink), sink.numel(), stream), "cs_read_probe")
 
     ms_stream = time_steps(streamed, 10, 3)
     ms_pattern = time_steps(pattern, 10, 3)

@@ -178,7 +178,6 @@ SIGNATURES = {
     "cs_check_positions": (_I32, [_P, _I64, _I32, _P, _P]),
     "cs_check_bias_positions": (_I32, [_VP, _I64, _P, _P]),
     "cs_ccpe_attention": (_I32, [ctypes.POINTER(CsCcpeArgs), _P]),
-    "cs_read_probe": (_I32, [_P, _I64, _P, _I64, _I32, _I32, _P, _I64, _P]),
     "cs_ccpe_prefill_policy_workspace_bytes": (_I64, [_I32, _I32, _I64]),
     "cs_ccpe_prefill_policy_bf16": (_I32, [ctypes.POINTER(CsCcpeArgs), _P, _I64, _P]),
     "cs_cope_positional_bias": (_I32, [_VP, _VP, _VP, _VP, _P, _P]),

@@ -2,6 +2,17 @@
 // streamed once, and a set of chunks in a given order (the access pattern of
 // a kernel under study, e.g. the decode's block-table reads).  Each thread
 // folds what it read into one word of `sink`, so the loads are kept.
+//
+// Measurement support with no counterpart in the reference, exported for the
+// benchmark's own binding and not declared in the library's header:
+//   int cs_read_probe(const void* base, int64_t bytes, const int64_t* chunks,
+//                     int64_t n_chunks, int32_t per_wg, int32_t chunk_bytes,
+//                     uint32_t* sink, int64_t sink_words, void* stream);
+// reads a buffer streamed once (chunks == NULL), or chunks of chunk_bytes at
+// the byte offsets chunks[0 .. n_chunks), per_wg chunks per 256-thread
+// workgroup in order (a chunk outside the buffer or not 16-byte aligned is
+// skipped); sink holds one uint32 device word per thread (at most 16384 x 256
+// in streaming mode).
 
 #include "common.h"
 

@@ -287,10 +287,13 @@ int cs_ccpe_prefill_bf16(const void* q, int64_t q_s_batch, int64_t q_s_tok, int6
 /* cope_attention for one query row per request (position.py:404-560 as the
  * decode step calls it, runtime.py:489-508 over the paged.py:433-472 gather).
  * Decode (q = 1 row per request at position nk[b]-1) with speculative
- * split-K: splits are aligned to the last key; a split whose right-hand gate
- * mass is below P-1 is recomputed exactly by the last workgroup of its
- * (request, KV head) to finish, which also merges the splits (two launches:
- * a clear of the arrival counters, then the splits).  workspace must hold
+ * split-K: splits are aligned to the last key, split 0 is exact and every
+ * other split assumes the gate mass to its right has reached P-1, recording
+ * its own gate total (decode_main_kernel).  A second launch, one workgroup
+ * per (request, KV head), forms the splits' true carries from the right,
+ * recomputes exactly the splits whose carry is below P-1 and merges the
+ * splits' (max, sum, accumulator) states into the output rows
+ * (decode_finish_kernel).  workspace must hold
  * cs_ccpe_decode_workspace_bytes(batch, hq, max_nk, split) bytes, with any
  * contents; the call refuses a smaller workspace_bytes.  Calls that share a
  * workspace must be ordered (one stream).  A request with nk[b] < 1 sets
@@ -602,17 +605,6 @@ int cs_copy_async(void* dst, const void* src, int64_t bytes, int32_t kind, void*
  * equal to src) checks only.  Both views contiguous, floating point. */
 int cs_snapshot_convert(const cs_view* src, const cs_view* dst, int32_t bit, int32_t* flags,
                         void* stream);
-
-/* ------------------------------------------------------------------------ *
- * Measurement support (no reference counterpart): the read rate of this
- * device for a buffer streamed once (chunks == NULL), or for chunks of
- * chunk_bytes at the byte offsets chunks[0 .. n_chunks), per_wg chunks per
- * 256-thread workgroup in order (an access pattern under study; a chunk
- * outside the buffer or not 16-byte aligned is skipped).  sink: uint32 device
- * words, one per thread (at most 16384 x 256 in streaming mode). */
-int cs_read_probe(const void* base, int64_t bytes, const int64_t* chunks, int64_t n_chunks,
-                  int32_t per_wg, int32_t chunk_bytes, uint32_t* sink, int64_t sink_words,
-                  void* stream);
 
 #ifdef __cplusplus
 }
