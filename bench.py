@@ -698,6 +698,74 @@ def calibration_measure(device, steps: int = 5) -> dict:
     }
 
 
+def tiny_e2e_measure(device) -> dict:
+    """The tiny end-to-end flow (the reference's CPU smoke, workflow_smoke.py:
+    117-324): a 2-layer random decoder (d_model 64, 4 heads x 16, vocab 512,
+    CoPE P = 64) on SelectiveRuntime with SLIDE arenas on paged caches;
+    profiles calibrated from the model's own forward, then populate,
+    recompute, same-context reuse, a shifted chunk under strict CCPE (fallback)
+    and under mixed_bias_override (reuse), each a prefill and 5 greedy decode
+    steps.  Wall clock per case, device synchronized around it, on a second
+    pass with a fresh store and runtimes (the first pass pays the one-time
+    costs)."""
+    import pathlib
+    import tempfile
+
+    import torch
+
+    from tests._e2e import CASES, device_runtimes, invoke, tiny_plan
+
+    plan = tiny_plan(32)
+    with tempfile.TemporaryDirectory() as root:
+        for tag in ("warm", "timed"):
+            store, runtimes = device_runtimes(device, pathlib.Path(root), plan, layers=2, calibration_layer=0,
+                                              tag=tag)
+            times, receipts, tokens = [], [], []
+            for i, (op, dyn, mode) in enumerate(CASES):
+                rt, model = runtimes[mode]
+                torch.cuda.synchronize(device)
+                t0 = time.perf_counter()
+                _, ids, receipt = invoke(rt, model, tiny_plan(dyn), op, f"req-{i}")
+                torch.cuda.synchronize(device)
+                times.append((time.perf_counter() - t0) * 1e3)
+                receipts.append(receipt)
+                tokens.append(ids)
+            for rt, _ in runtimes.values():
+                rt.close()
+            store.close()
+    return {
+        "workload": "tiny end-to-end: 2-layer random decoder (d_model 64, 4 heads x 16, vocab 512, CoPE P=64), "
+                    "5 cases (populate, recompute, reuse, shifted strict -> fallback, shifted mixed -> reuse), "
+                    "each a prefill + 5 greedy decode steps, paged SLIDE arenas",
+        "cases": [f"{op}/{dyn}/{mode}" for op, dyn, mode in CASES],
+        "wall_ms_per_case": [round(t, 2) for t in times],
+        "decisions": [{"cache_hit": r["cache_hit"], "fallback": r["fallback"],
+                       "position_policy_fallback": r["position_policy_fallback"]} for r in receipts],
+        "tokens": tokens,
+    }
+
+
+def cpu_tiny_e2e_leg(gpu_tokens) -> dict:
+    """The oracle runtime (oracle/runtime.py) on the host, driven through the
+    same five cases on the same model and plans: wall clock per case (after a
+    first pass), and whether its greedy tokens equal the device run's."""
+    from tests._e2e import CASES, invoke, oracle_runtimes, tiny_plan
+
+    plan = tiny_plan(32)
+    for _ in range(2):
+        runtimes = oracle_runtimes(plan, layers=2, calibration_layer=0)
+        times, tokens = [], []
+        for i, (op, dyn, mode) in enumerate(CASES):
+            rt, model = runtimes[mode]
+            t0 = time.perf_counter()
+            _, ids, _ = invoke(rt, model, tiny_plan(dyn), op, f"req-{i}")
+            times.append((time.perf_counter() - t0) * 1e3)
+            tokens.append(ids)
+    return {"value": round(sum(times), 1), "unit": "ms for the 5 cases", "cores": 1, "kind": "port",
+            "sample": "the whole workload", "wall_ms_per_case": [round(t, 1) for t in times],
+            "tokens_equal_device": tokens == gpu_tokens}
+
+
 def note(message: str) -> None:
     """Progress line on stderr (stdout carries only the JSON record)."""
     print(f"bench: {message}", file=sys.stderr, flush=True)
@@ -1171,6 +1239,9 @@ def main() -> int:
     if not args.no_e2e:
         record["decode_e2e"] = decode_e2e_measure(device, args.e2e_tokens)
         note(f"decode e2e: {record['decode_e2e']['tok_per_s']} tok/s")
+    if not args.no_e2e:
+        record["tiny_e2e"] = tiny_e2e_measure(device)
+        note(f"tiny e2e: {record['tiny_e2e']['wall_ms_per_case']} ms per case")
     if not args.no_reuse:
         record["reuse"] = reuse_measure(device)
         note(f"reuse: {record['reuse']['ms_per_call']} ms/call (generic {record['reuse']['generic_ms_per_call']})")
@@ -1207,6 +1278,9 @@ def main() -> int:
         if "wca" in record:
             note("cpu baseline: wca")
             record["wca"]["cpu_baseline"] = cpu_wca_leg()
+        if "tiny_e2e" in record:
+            note("cpu baseline: tiny e2e")
+            record["tiny_e2e"]["cpu_baseline"] = cpu_tiny_e2e_leg(record["tiny_e2e"]["tokens"])
     print(json.dumps(record), flush=True)
     return 0
 

@@ -115,6 +115,49 @@ def test_decode_steps_match_float32_reference(device):
             torch.testing.assert_close(rec[n:], kv[li][b][n:].to(torch.bfloat16).float(), atol=2e-2, rtol=2e-2)
 
 
+MISTRAL_LENS = [600, 250]
+
+
+@pytest.mark.gpu
+def test_mistral_shaped_decode_steps_match_float32_reference(device):
+    """The Mistral-7B layer shape (hidden 4096, 32 query / 8 KV heads, FFN
+    14336, vocab 32000) at 2 layers: two requests with contexts of 600 and
+    250 keys, 2 decode steps teacher-forced with the device's tokens, against
+    the float32 restatement.  Tolerance 6e-2 absolute and relative on the
+    logits: bf16 activations between the GEMMs of a 4096-wide model against
+    float32 throughout."""
+    shape = DecoderShape(layers=2)
+    steps = 2
+    model = PagedDecoder(shape, device, seed=23)
+    gen = torch.Generator().manual_seed(405)
+    per = [(n + steps + BS - 1) // BS for n in MISTRAL_LENS]
+    perm = torch.randperm(sum(per), generator=gen)
+    table = torch.zeros((len(MISTRAL_LENS), max(per)), dtype=torch.int32)
+    at = 0
+    for b, p in enumerate(per):
+        table[b, :p] = perm[at:at + p].to(torch.int32)
+        at += p
+    table = table.to(device)
+    caches = model.new_caches(sum(per), BS)
+    dgen = torch.Generator(device=device).manual_seed(24)
+    for c in caches:
+        c.normal_(generator=dgen)
+    kv = [[gathered(c, table[b], n) for b, n in enumerate(MISTRAL_LENS)] for c in caches]
+    max_context = max(MISTRAL_LENS) + steps
+    ws = decode_workspace(len(MISTRAL_LENS), shape.heads, max_context, 1024, device)
+    flags = _hip.new_flags(device)
+    ids = torch.tensor([7, 31999], device=device)
+    positions = torch.tensor(MISTRAL_LENS, dtype=torch.long, device=device)
+    for step in range(steps):
+        got = model.step(ids, positions, caches, table, max_context=max_context, workspace=ws, flags=flags)
+        want = reference_step(model, ids, kv, shape.heads, shape.kv_heads)
+        assert bool(torch.isfinite(got.float()).all())
+        torch.testing.assert_close(got.float().cpu(), want, atol=6e-2, rtol=6e-2, msg=f"step {step}")
+        ids = got.argmax(-1)
+        positions += 1
+    raise_flags(flags)
+
+
 @pytest.mark.gpu
 def test_generate_is_greedy_over_step_and_checks_flags_once(device):
     model = PagedDecoder(SHAPE, device, seed=19)

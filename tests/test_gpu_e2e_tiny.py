@@ -18,113 +18,13 @@ recomputed ones and the strict fallback equals the dense forward
 
 from __future__ import annotations
 
-import hashlib
-
 import pytest
 import torch
 
-from cacheslide_amd import CoPE, NativePagedKV, PageStore, cope_attention
 from cacheslide_amd.policy import WCAConfig
-from cacheslide_amd.profiles import ProfileBundle, calibrate_from_forward
-from cacheslide_amd.selective import RuntimeOptions, SelectiveRuntime
-from oracle.runtime import OracleRuntime
-from tests._e2e import invoke, tiny_plan
-from tests._tiny_decoder import HEAD_DIM, HEADS, HIDDEN, KV_HEADS, NPOS, TinyDecoder
+from tests._e2e import CASES, device_runtimes, oracle_runtimes, run_cases, tiny_plan
 
 pytestmark = pytest.mark.gpu
-
-IDENTITY = hashlib.sha256(b"tiny-e2e").hexdigest()
-BLOCK = 4
-
-
-def cope_factory(device):
-    def make(table):
-        cope = CoPE(HEAD_DIM, NPOS, device=device)
-        with torch.no_grad():
-            cope.position_embeddings.copy_(table)
-        return cope
-    return make
-
-
-class BlockPool:
-    """Paged caches per layer ([blocks, KV heads, 4, 2 x 16], a strided view
-    like the reference smoke's) and one reversed block table for every arena."""
-
-    def __init__(self, layers: int, capacity: int, device):
-        blocks = (capacity + BLOCK - 1) // BLOCK
-        self.row = list(reversed(range(blocks)))
-        self.caches = [torch.full((blocks, KV_HEADS, BLOCK, 4 * HEAD_DIM), -999.0, device=device)[..., ::2]
-                       for _ in range(layers)]
-
-    def __call__(self, layer, prompt_length, max_selected, *, existing=None):
-        if existing is not None:
-            existing.update_block_table(self.row)
-            return existing
-        return NativePagedKV(self.caches[layer], self.row, prompt_length, max_selected,
-                             request_id="tiny", layer_index=layer)
-
-
-def calibrated_profiles(device, plan, layers, tmp_path):
-    model = TinyDecoder(device, None, cope_factory=cope_factory(device), layers=layers)
-
-    def forward(p, observer):
-        def handler(layer, positions, q, k, v, cope):
-            observer(layer, q, k, cope)
-            return cope_attention(q, k, v, cope, positions, key_positions=positions, query_chunk_size=64)
-        model.handler = handler
-        model.forward(torch.tensor(p.token_ids))
-
-    path = calibrate_from_forward(forward, [plan], tmp_path / "profiles", adapter_identity=IDENTITY,
-                                  num_layers=layers, query_heads=HEADS, kv_heads=KV_HEADS, head_dim=HEAD_DIM,
-                                  max_positions=NPOS)
-    return ProfileBundle(path, IDENTITY, max_elements=1_000_000)
-
-
-def device_runtimes(device, tmp_path, plan, layers, calibration_layer, paged=True, tag="a",
-                    wca=WCAConfig()):
-    store = PageStore(tmp_path / f"pages-{tag}", cpu_budget_bytes=1 << 26, disk_budget_bytes=1 << 28)
-    profiles = calibrated_profiles(device, plan, layers, tmp_path / tag)
-    pool = BlockPool(layers, len(plan.token_ids) + 64, device) if paged else None
-    out = {}
-    for mode in ("strict_contextual", "mixed_bias_override"):
-        options = RuntimeOptions(calibration_layer=calibration_layer, wca=wca, ccpe_position_policy=mode)
-        rt = SelectiveRuntime(layers=layers, kv_heads=KV_HEADS, head_dim=HEAD_DIM, hidden_size=HIDDEN,
-                              store=store, profiles=profiles, identity=IDENTITY, checkpoint_id=IDENTITY,
-                              options=options, arena_factory=pool)
-        model = TinyDecoder(device, rt.attention, cope_factory=cope_factory(device), layers=layers)
-        out[mode] = (rt, model)
-    return store, out
-
-
-def oracle_runtimes(plan, layers, calibration_layer, wca=WCAConfig()):
-    out = {}
-    shared = None
-    for mode in ("strict_contextual", "mixed_bias_override"):
-        rt = OracleRuntime(layers=layers, identity=IDENTITY,
-                           options=RuntimeOptions(calibration_layer=calibration_layer, ccpe_position_policy=mode),
-                           fraction=wca.correction_fraction, gate_interval=wca.gate_interval,
-                           threshold=wca.convergence_threshold, mode=wca.convergence_mode)
-        if shared is None:
-            shared = rt
-        else:
-            rt.store, rt.profiles = shared.store, shared.profiles
-        out[mode] = (rt, TinyDecoder("cpu", rt.attention, layers=layers))
-    shared_rt, shared_model = out["strict_contextual"]
-    shared_rt.calibrate(shared_model, plan)
-    return out
-
-
-CASES = [("populate", 32, "strict_contextual"), ("recompute", 32, "strict_contextual"),
-         ("reuse", 32, "strict_contextual"), ("reuse", 40, "strict_contextual"),
-         ("reuse", 40, "mixed_bias_override")]
-
-
-def run_cases(runtimes, cases=CASES):
-    results = []
-    for i, (op, dyn, mode) in enumerate(cases):
-        rt, model = runtimes[mode]
-        results.append(invoke(rt, model, tiny_plan(dyn), op, f"req-{i}"))
-    return results
 
 
 def test_tiny_decoder_end_to_end_matches_oracle(device, tmp_path):
