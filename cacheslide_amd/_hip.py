@@ -180,6 +180,7 @@ SIGNATURES = {
     "cs_ccpe_attention": (_I32, [ctypes.POINTER(CsCcpeArgs), _P]),
     "cs_ccpe_prefill_policy_workspace_bytes": (_I64, [_I32, _I32, _I64]),
     "cs_ccpe_prefill_policy_bf16": (_I32, [ctypes.POINTER(CsCcpeArgs), _P, _I64, _P]),
+    "cs_prepare_device": (_I32, []),
     "cs_cope_positional_bias": (_I32, [_VP, _VP, _VP, _VP, _P, _P]),
     "cs_contextual_positions": (_I32, [_VP, _VP, _I64, _VP, _P, _P]),
     "cs_ccpe_logits": (_I32, [_VP, _VP, _VP, _P, _P]),
@@ -292,7 +293,21 @@ def require_device(*tensors: torch.Tensor | None) -> torch.device:
             raise ValueError("all tensors must be on the same HIP device")
     if device is None:
         raise ValueError("no device tensor given")
+    if device.index not in _PREPARED:
+        _prepare(device)
     return device
+
+
+# Devices whose helper stream exists (cs_prepare_device): made at the first
+# use of a device, before the caller's process has created many streams, so
+# that the HIP runtime gives it a hardware queue other than the caller's.
+_PREPARED: set = set()
+
+
+def _prepare(device: torch.device) -> None:
+    with torch.cuda.device(device):
+        call("cs_prepare_device")
+    _PREPARED.add(device.index)
 
 
 def stream_of(device: torch.device) -> ctypes.c_void_p:

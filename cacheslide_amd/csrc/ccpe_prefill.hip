@@ -1166,6 +1166,12 @@ extern "C" int cs_ccpe_prefill_bf16(const void* q, int64_t q_s_batch, int64_t q_
   return CS_OK;
 }
 
+extern "C" int cs_prepare_device(void) {
+  std::lock_guard<std::mutex> lock(g_side_mutex);
+  side_lane* side = nullptr;
+  return side_lane_of_current(&side);
+}
+
 extern "C" int64_t cs_ccpe_prefill_policy_workspace_bytes(int32_t nq, int32_t hq, int64_t nk) {
   if (nq < 0 || hq <= 0 || nk < 0) return 0;
   return carve_policy(nullptr, nq, hq, nk).bytes;

@@ -182,10 +182,22 @@ int cs_ccpe_attention(const cs_ccpe_args* args, void* stream);
  * CS_FLAG_POLICY_GENERIC in *flags and the caller runs cs_ccpe_attention
  * instead.  workspace: at least
  * cs_ccpe_prefill_policy_workspace_bytes(nq, Hq, nk) bytes, 256-byte aligned,
- * any contents. */
+ * any contents.  The checker runs on a helper stream of the device, forked
+ * from and joined back into `stream`, so that it overlaps the attention. */
 int64_t cs_ccpe_prefill_policy_workspace_bytes(int32_t nq, int32_t hq, int64_t nk);
 int cs_ccpe_prefill_policy_bf16(const cs_ccpe_args* args, void* workspace, int64_t workspace_bytes,
                                 void* stream);
+
+/* No counterpart in the reference (an implementation helper).  Creates, for
+ * the current device, the helper stream of cs_ccpe_prefill_policy_bf16, which
+ * is otherwise created at that entry point's first call.  The HIP runtime
+ * gives a new stream a hardware queue of its own only while the device has
+ * fewer queues than GPU_MAX_HW_QUEUES (4 by default) and then shares them;
+ * a helper stream that shares the caller's queue runs the checker and the
+ * attention one after the other.  Calling this once per device before the
+ * process creates other streams (the Python package does so at its first use
+ * of a device) keeps them apart.  Idempotent. */
+int cs_prepare_device(void);
 
 /* CoPE.contextual_positions (position.py:295-307) on explicit logits [H,q,k]
  * and a gate mask allowed [Hm,q,k] uint8: sigmoid gates, fp64 reverse cumulative
