@@ -145,3 +145,13 @@ def test_decode_refuses_a_small_workspace_without_a_device():
     slot_src.slots_cols = 1000
     assert lib.cs_ccpe_decode_bf16(*args, need, *tail) == _hip.CS_EINVAL
     assert b"sidecar rows must be 16-byte aligned" in lib.cs_last_error()
+
+
+def test_prepare_device_reports_a_missing_device():
+    """Without a HIP device the call returns an error status and names the
+    failing runtime call instead of crashing (on a GPU host it succeeds)."""
+    if torch.cuda.is_available():
+        return
+    lib = _hip.load()
+    assert lib.cs_prepare_device() != _hip.CS_OK
+    assert lib.cs_last_error()

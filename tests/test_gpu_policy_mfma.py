@@ -8,8 +8,10 @@ Checked against the oracle's per-chunk evaluation of the two policies
 (oracle/ccpe.py canonical_policy, selected_visibility, cope_attention): the
 same decision (accept, or the same error type and message from the same
 chunk) and, when accepted, outputs within the bf16 tolerance (2e-2 absolute,
-1e-2 relative).  Each test also checks which kernel ran: the MFMA path, or the
-generic kernel when some fixed query row is not selected.
+1e-2 relative).  Each test also checks which kernel ran: the MFMA path (also
+for fixed query rows that are not selected, whose canonical cells it reads
+tile by tile), or the generic kernel when the plan holds more dynamic keys
+beside fixed keys than the checker does.
 
 Layout: reused chunk A, a recomputed chunk, reused chunk B (make_plan);
 8 query heads over 2 KV heads; CoPE P = 64, table N(0, 0.1).  The profile is
@@ -314,3 +316,17 @@ def test_long_calibration_call_matches_generic_and_oracle(device, monkeypatch, l
     expected = oracle_run(q, k, v, e, pick, plan, canonical[:, ords], ords, False, None, 64)
     assert expected[0] == "ok"
     assert_close_bf16(actual[1][torch.from_numpy(pick).to(device)], expected[1])
+
+
+def test_prepare_device_is_idempotent_and_made_at_first_use(device):
+    """cs_prepare_device creates the device's helper stream once; later calls
+    return CS_OK and change nothing, and the package has made the call by the
+    time it validated a tensor of the device."""
+    from cacheslide_amd import _hip
+
+    _hip.require_device(torch.zeros(1, device=device))
+    assert device.index in _hip._PREPARED
+    lib = _hip.load()
+    with torch.cuda.device(device):
+        assert lib.cs_prepare_device() == _hip.CS_OK
+        assert lib.cs_prepare_device() == _hip.CS_OK
