@@ -117,7 +117,8 @@ __global__ void __launch_bounds__(64 * kWaves) policy_check_kernel(policy_check_
       for (int i = 0; i < 4; ++i) code[i] = j0 + i < a.nk ? a.code[j0 + i] : -1;
     }
   };
-  auto check_block = [&](int64_t t, const int32_t* code, const float* pcell) {
+  // (all_fixed: every key of the block is fixed, descriptor >= 0)
+  auto check_block = [&](int64_t t, const int32_t* code, const float* pcell, bool all_fixed) {
     const int64_t j0 = t * 256 + 4 * lane;
     float pv[4];
 #pragma unroll
@@ -129,6 +130,37 @@ __global__ void __launch_bounds__(64 * kWaves) policy_check_kernel(policy_check_
     if (t * 256 >= kend) {  // no causal key in the block
       prev_known = false;
       return;
+    }
+    if (all_fixed && (t + 1) * 256 <= kend) {
+      // Every key of the block fixed and causal: every cell is checked and
+      // paired with its right-hand neighbour (lane 63's last cell with the
+      // block to the right, when that key is checked).  A cell with p >= 0,
+      // p <= q - k + 1 and, paired, 0 <= p - p_right <= 1 passes every test of
+      // path_violations_unit, whose tolerances are all >= 0 (so its bounds
+      // are these or looser, in the same float arithmetic); only a block in
+      // which some cell misses this screen takes the exact checks below.
+      float right = __shfl_down(pv[0], 1, 64);
+      bool right_pair = true;
+      if (lane == 63) {
+        right = prev_p;
+        right_pair = prev_known;
+      }
+      bool ok = true;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float pr = i < 3 ? pv[i + 1] : right;
+        const bool paired = i < 3 ? true : right_pair;
+        const float d = pv[i] - pr;
+        // q - k + 1 exactly as path_violations_unit forms it
+        const float available = static_cast<float>(static_cast<int32_t>(qp - (j0 + i))) + 1.f;
+        ok = ok && pv[i] >= 0.f && pv[i] <= available && (!paired || (d >= 0.f && d <= 1.f));
+      }
+      if (__all(ok)) {
+        prev_p = __shfl(pv[0], 0, 64);
+        prev_known = true;
+        prev_fixed = true;
+        return;
+      }
     }
     bool known[4], fixed[4];
 #pragma unroll
@@ -201,7 +233,7 @@ __global__ void __launch_bounds__(64 * kWaves) policy_check_kernel(policy_check_
     for (int g = 0; g < kGroup; ++g) fetch(t0 - kGroup - g, ndesc[g], next[g]);
 #pragma unroll
     for (int g = 0; g < kGroup; ++g)
-      if (t0 - g >= 0) check_block(t0 - g, codes[g], cells[g]);
+      if (t0 - g >= 0) check_block(t0 - g, codes[g], cells[g], desc[g] >= 0);
 #pragma unroll
     for (int g = 0; g < kGroup; ++g) {
       desc[g] = ndesc[g];

@@ -1263,6 +1263,10 @@ extern "C" int cs_ccpe_prefill_policy_bf16(const cs_ccpe_args* a, void* workspac
     p.grp = w.grp;
     p.code = w.code;
   }
+  // The attention kernel is queued first, so that its longest workgroups
+  // (rows whose walks cover every causal key) are dispatched at once; the
+  // checker, forked after the lowering kernels, then fills the compute units
+  // the attention's short workgroups leave.
   std::unique_lock<std::mutex> side_lock(g_side_mutex, std::defer_lock);
   side_lane* side = nullptr;
   if (canon) {
@@ -1275,6 +1279,16 @@ extern "C" int cs_ccpe_prefill_policy_bf16(const cs_ccpe_args* a, void* workspac
       set_error("policy check fork: %s", hipGetErrorString(err));
       return CS_ELAUNCH;
     }
+  }
+  const dim3 grid(p.total_wg), block(64 * waves);
+  if (waves == 8)
+    hipLaunchKernelGGL((ccpe_prefill_kernel<0, 8, true>), grid, block, smem, s, p);
+  else if (waves == 2)
+    hipLaunchKernelGGL((ccpe_prefill_kernel<0, 2, true>), grid, block, smem, s, p);
+  else
+    hipLaunchKernelGGL((ccpe_prefill_kernel<0, 4, true>), grid, block, smem, s, p);
+  CS_LAUNCH_CHECK("ccpe_prefill_policy");
+  if (canon) {
     cs::policy_check_args c{};
     c.q = static_cast<const uint16_t*>(qv.data);
     c.q_s_tok = qv.stride[0];
@@ -1306,22 +1320,8 @@ extern "C" int cs_ccpe_prefill_policy_bf16(const cs_ccpe_args* a, void* workspac
                          side->stream, w.code, static_cast<int64_t>(nk), w.blk);
     const int cst = cs::launch_policy_check(c, side->stream);
     if (cst) return cst;
-    err = hipEventRecord(side->join, side->stream);
-    if (err != hipSuccess) {
-      set_error("policy check join: %s", hipGetErrorString(err));
-      return CS_ELAUNCH;
-    }
-  }
-  const dim3 grid(p.total_wg), block(64 * waves);
-  if (waves == 8)
-    hipLaunchKernelGGL((ccpe_prefill_kernel<0, 8, true>), grid, block, smem, s, p);
-  else if (waves == 2)
-    hipLaunchKernelGGL((ccpe_prefill_kernel<0, 2, true>), grid, block, smem, s, p);
-  else
-    hipLaunchKernelGGL((ccpe_prefill_kernel<0, 4, true>), grid, block, smem, s, p);
-  CS_LAUNCH_CHECK("ccpe_prefill_policy");
-  if (side) {
-    const hipError_t err = hipStreamWaitEvent(s, side->join, 0);
+    hipError_t err = hipEventRecord(side->join, side->stream);
+    if (err == hipSuccess) err = hipStreamWaitEvent(s, side->join, 0);
     if (err != hipSuccess) {
       set_error("policy check join: %s", hipGetErrorString(err));
       return CS_ELAUNCH;
