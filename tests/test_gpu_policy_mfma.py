@@ -330,3 +330,28 @@ def test_prepare_device_is_idempotent_and_made_at_first_use(device):
     with torch.cuda.device(device):
         assert lib.cs_prepare_device() == _hip.CS_OK
         assert lib.cs_prepare_device() == _hip.CS_OK
+
+
+@pytest.mark.parametrize("drop, want", [(0.5, "error"), ("ulp", "ok")])
+def test_single_cell_drop_inside_a_fixed_block(device, monkeypatch, drop, want):
+    """One canonical cell of a selected row, in the block of keys 0..255 (all
+    fixed and far below the row, where every cell is P-1), set below its
+    right-hand neighbour: by 0.5 it breaks 'nonincreasing'; by one ulp it
+    stays within the pair tolerance (1e-6 plus the rounding terms) and
+    passes.  The checker screens such blocks with plain bounds and takes its
+    exact checks only where a cell misses them, so both decisions must equal
+    the oracle's."""
+    q, k, v, e, rows, plan, canonical, ordinals, sel = scenario(61, **BIG)
+    canonical = canonical.copy()
+    fixed = list(plan.fixed_indices)
+    r = fixed.index(int(sel[-1]))            # a selected row in the second chunk
+    h, c = 3, 100
+    right = np.float32(canonical[h, r, c + 1])
+    assert right == P - 1
+    canonical[h, r, c] = right - np.float32(0.5) if drop != "ulp" else np.nextafter(right, np.float32(0))
+    expected = oracle_run(q, k, v, e, rows, plan, canonical, ordinals, True, sel, 64)
+    assert expected[0] == want, expected[:3] if expected[0] == "error" else "ok"
+    actual, called = device_run(q, k, v, e, rows, plan, profile_for(plan, canonical, ordinals), "strict_contextual",
+                                sel, 64, device, monkeypatch)
+    compare(expected, actual)
+    assert "cs_ccpe_attention" not in called, called
