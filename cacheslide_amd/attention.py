@@ -43,6 +43,24 @@ def _fixed_positions(fixed: tuple[int, ...]) -> Tensor:
     return tensor
 
 
+_FIXED_DEVICE: dict[tuple, tuple] = {}
+
+
+def _fixed_on(fixed: tuple[int, ...], device) -> Tensor:
+    """The plan's fixed positions sorted on ``device`` (read only), cached per
+    tuple and device like ``_fixed_positions``: one host-to-device copy and
+    sort per plan, not per call."""
+    key = (id(fixed), str(device))
+    hit = _FIXED_DEVICE.get(key)
+    if hit is not None and hit[0] is fixed:
+        return hit[1]
+    tensor = torch.sort(_fixed_positions(fixed).to(device)).values
+    if len(_FIXED_DEVICE) >= 8:
+        _FIXED_DEVICE.clear()
+    _FIXED_DEVICE[key] = (fixed, tensor)
+    return tensor
+
+
 def _memo_of(profile, fallback: dict) -> dict:
     """A memo dict kept on the profile object (immutable calibration data),
     or ``fallback`` for a profile that takes no attributes."""
@@ -216,8 +234,7 @@ class SelectedAssociationPolicy:
         fixed_indices = self.fixed_indices
         if not isinstance(fixed_indices, tuple):
             fixed_indices = tuple(fixed_indices)
-        fixed = _fixed_positions(fixed_indices).to(device)
-        fixed = torch.sort(fixed).values
+        fixed = _fixed_on(fixed_indices, device)
         selected = self.selected_indices.to(device=device, dtype=torch.long).reshape(-1)
         return fixed, torch.sort(selected).values
 

@@ -618,7 +618,10 @@ def cope_attention(
         args.k_ord = ptr(lowered.k_ord)
         args.strict = 1 if canonical.mode == "strict_contextual" else 0
         n_chunks = (nq + query_chunk_size - 1) // query_chunk_size
-        chunk_flags = _hip.new_flags(device, n_chunks)
+        # one word more: on the MFMA path the flags word is copied behind the
+        # chunk flags, so one readback returns both
+        chunk_buf = _hip.new_flags(device, n_chunks + 1)
+        chunk_flags = chunk_buf[:n_chunks]
         args.chunk_rows = query_chunk_size
         args.chunk_flags = ptr(chunk_flags)
     if selected is not None:
@@ -627,14 +630,21 @@ def cope_attention(
         args.sel_rows = ptr(sel_rows)
         args.fixed_keys = ptr(fixed_keys)
     # The MFMA reuse-call path (a SelectedAssociationPolicy, a canonical
-    # profile or both); the flags word it leaves is read once here and serves
-    # every check below (one wait for the device per call).
+    # profile or both); the flags word it leaves (with the chunk flags, when
+    # there are any) is read once here and serves every check below (one wait
+    # for the device per call).
     flags_value = None
+    chunk_values = None
     if ((selected is not None or canonical is not None) and default_keys
             and _policy_fast_ok(query, key, value, e, cope, amask, visibility_mask, fixed_positions,
                                 return_positions, lowered if canonical is not None else None)
             and _policy_prefill(args, query, key, ck)):
-        flags_value = _hip.read_flags(ck.flags)[0]
+        if chunk_flags is not None:
+            chunk_buf[n_chunks:].copy_(ck.flags)
+            values = _hip.read_flags(chunk_buf)
+            flags_value, chunk_values = values[-1], values[:-1]
+        else:
+            flags_value = _hip.read_flags(ck.flags)[0]
         if flags_value & _hip.FLAG_POLICY_GENERIC:
             # more fixed/dynamic boundary keys than the path checker holds: the
             # generic kernel runs the call
@@ -642,6 +652,7 @@ def cope_attention(
             if chunk_flags is not None:
                 chunk_flags.zero_()
             flags_value = None
+            chunk_values = None
             call("cs_ccpe_attention", args, ck.stream)
     else:
         call("cs_ccpe_attention", args, ck.stream)
@@ -649,7 +660,7 @@ def cope_attention(
     ck.device_step(_hip.FLAG_POS_INVALID, ValueError, "positions must be bounded query-dependent [head,query,key]")
     ck.device_step(_hip.FLAG_SCORE_NONFINITE, ValueError, "contextual attention logits are not finite")
     if chunk_flags is not None:
-        _raise_policy_errors(ck, chunk_flags, lowered, flags_value)
+        _raise_policy_errors(ck, chunk_flags, lowered, flags_value, chunk_values)
     ck.finish(value=flags_value)
     if return_positions:
         return output, trace
@@ -660,14 +671,17 @@ _TRANSFORM_BOUNDS_MESSAGE = ("positions_transform must return bounded finite pos
                              "with the contextual shape, dtype and device")
 
 
-def _raise_policy_errors(ck: _Checks, chunk_flags: Tensor, lowered, flags_value: int | None = None) -> None:
+def _raise_policy_errors(ck: _Checks, chunk_flags: Tensor, lowered, flags_value: int | None = None,
+                         values: list[int] | None = None) -> None:
     """In chunk order, the first chunk holding a fixed query row that fails:
     profile lookup, then the strict path checks, then the bounds of the
-    substituted positions (position.py:485-516 with attention.py:32-57)."""
+    substituted positions (position.py:485-516 with attention.py:32-57).
+    ``values``: the chunk flags already read with the flags word."""
     from .attention import CHUNK_CANON_OUT_OF_RANGE, CHUNK_HAS_FIXED_ROW
 
     ck.finish(value=flags_value)
-    values = _hip.read_flags(chunk_flags)
+    if values is None:
+        values = _hip.read_flags(chunk_flags)
     for value in values:
         if not value & CHUNK_HAS_FIXED_ROW:
             continue
