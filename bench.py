@@ -1210,7 +1210,7 @@ def main() -> int:
     ap.add_argument("--no-snapshot", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
+        print("bench.py measures one GPU only: cacheslide_amd has no multi-GPU path "
               "(run with --gpus 1)", file=sys.stderr)
         return 2
     import torch

@@ -106,7 +106,7 @@ class _LoweredCanonical:
 
     def __init__(self, policy: "CanonicalPositionPolicy", device, query_positions, key_positions):
         # the call-independent part (position -> profile row / fixed ordinal
-        # tables, the profile lookup's verdict) once per profile, plan and
+        # tables, the profile lookup's decision) once per profile, plan and
         # device: the runtime builds a new policy per call around the same
         # profile and plan
         fixed = policy.plan.fixed_indices
