@@ -1265,11 +1265,17 @@ extern "C" int cs_ccpe_prefill_policy_bf16(const cs_ccpe_args* a, void* workspac
   }
   // The attention kernel is queued first, so that its longest workgroups
   // (rows whose walks cover every causal key) are dispatched at once; the
-  // checker, forked after the lowering kernels, then fills the compute units
-  // the attention's short workgroups leave.
+  // checker, forked after the lowering kernels and the checker's block
+  // descriptors (queued here, ahead of the attention, so that they do not
+  // wait behind it for compute units), then fills the compute units the
+  // attention's short workgroups leave.
   std::unique_lock<std::mutex> side_lock(g_side_mutex, std::defer_lock);
   side_lane* side = nullptr;
   if (canon) {
+    const int64_t nb = (static_cast<int64_t>(nk) + 255) / 256;
+    if (nb > 0)
+      hipLaunchKernelGGL(policy_blocks_kernel, dim3(static_cast<uint32_t>((nb + 3) / 4)), dim3(256), 0, s,
+                         w.code, static_cast<int64_t>(nk), w.blk);
     side_lock.lock();
     const int sst = side_lane_of_current(&side);
     if (sst) return sst;
@@ -1314,10 +1320,6 @@ extern "C" int cs_ccpe_prefill_policy_bf16(const cs_ccpe_args* a, void* workspac
     c.strict = a->strict;
     c.chunk_rows = a->chunk_rows;
     c.chunk_flags = a->chunk_flags;
-    const int64_t nb = (static_cast<int64_t>(nk) + 255) / 256;
-    if (nb > 0)
-      hipLaunchKernelGGL(policy_blocks_kernel, dim3(static_cast<uint32_t>((nb + 3) / 4)), dim3(256), 0,
-                         side->stream, w.code, static_cast<int64_t>(nk), w.blk);
     const int cst = cs::launch_policy_check(c, side->stream);
     if (cst) return cst;
     hipError_t err = hipEventRecord(side->join, side->stream);
