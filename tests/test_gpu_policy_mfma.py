@@ -355,3 +355,40 @@ def test_single_cell_drop_inside_a_fixed_block(device, monkeypatch, drop, want):
                                 sel, 64, device, monkeypatch)
     compare(expected, actual)
     assert "cs_ccpe_attention" not in called, called
+
+
+# 600 fixed + 100 recomputed + 600 fixed: the 256-key blocks of both chunks
+# hold consecutive ordinals at offsets that are multiples of 4, so their cells
+# are read 16 bytes per lane and screened
+EDGE = dict(a=600, dyn=100, b=600, n_sel=40)
+
+
+@pytest.mark.parametrize("case, mode, want", [
+    ("out_of_range", "strict_contextual", "error"),
+    ("nan", "strict_contextual", "error"),
+    ("negative_zero", "strict_contextual", "ok"),
+    ("out_of_range", "mixed_bias_override", "error"),
+    ("negative_zero", "mixed_bias_override", "ok"),
+])
+def test_screened_block_after_the_row(device, monkeypatch, case, mode, want):
+    """One canonical cell of fixed row 100, at key 300: in the block of keys
+    256..511, all fixed and all after the row, which only the bounds check
+    covers.  P + 2 and NaN must raise the bounds error; -0.0 (the cell's
+    calibrated value is 0) passes the reference's p >= 0 although its bit
+    pattern is not that of a value in [+0, P-1], so the checker's screen
+    sends the block to the exact checks, which must accept it."""
+    q, k, v, e, rows, plan, canonical, ordinals, sel = scenario(62, **EDGE)
+    canonical = canonical.copy()
+    r, h, c = 100, 5, 300                    # ordinals = positions in chunk A
+    assert canonical[h, r, c] == 0.0
+    canonical[h, r, c] = {"out_of_range": np.float32(P + 2), "nan": np.float32(np.nan),
+                          "negative_zero": np.float32(-0.0)}[case]
+    sel = np.unique(np.concatenate([sel, [r]]))
+    rows = np.unique(np.concatenate([rows, [r]]))
+    strict = mode == "strict_contextual"
+    expected = oracle_run(q, k, v, e, rows, plan, canonical, ordinals, strict, sel, 64)
+    assert expected[0] == want, expected[:3] if expected[0] == "error" else "ok"
+    actual, called = device_run(q, k, v, e, rows, plan, profile_for(plan, canonical, ordinals), mode, sel, 64,
+                                device, monkeypatch)
+    compare(expected, actual)
+    assert "cs_ccpe_attention" not in called, called
