@@ -602,6 +602,19 @@ def reuse_measure(device, steps: int = 5) -> dict:
     causal = float((rows.double() + 1).sum())
     flops = 4.0 * HQ * D * causal + 2.0 * HQ * D * P * len(rows)
     canon_bytes = n_sel * HQ * F * 4
+    # the same rows on a layer without a profile (SelectedAssociationPolicy
+    # alone): no checker runs beside the attention, whose row blocks that walk
+    # every causal key (the question rows) are then split over the keys
+    def run_selected():
+        return cope_attention(q, k, v, cope, rows, None, visibility_transform=visibility, query_chunk_size=64)
+
+    run_selected()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        run_selected()
+    torch.cuda.synchronize()
+    ms_selected = (time.perf_counter() - t0) * 1e3 / steps
     del profile, policy
     # the same call with a per-head profile in HBM (head h: a path of
     # 0.4 + 0.01 h per token, 33.3 GB), so every canonical row the call reads
@@ -639,11 +652,13 @@ def reuse_measure(device, steps: int = 5) -> dict:
         "reference_equivalent_TFLOPs": round(flops / (ms * 1e-3) / 1e12, 1),
         "canonical_bytes_checked": canon_bytes,
         "canonical_GBs_whole_call": round(canon_bytes / (ms * 1e-3) / 1e9, 1),
+        "selected_only_ms_per_call": round(ms_selected, 3),
         "per_head_profile_ms_per_call": round(ms_per_head, 3),
         "per_head_profile_canonical_GBs_whole_call": round(canon_bytes / (ms_per_head * 1e-3) / 1e9, 1),
         "note": "the timed profile is one [16128, 16128] path broadcast to the 32 heads (its canonical rows are "
                 "re-read from L2); per_head_profile_* times the same call with a [32, 16128, 16128] profile "
-                "stored per head (33.3 GB in HBM, head h's path 0.4 + 0.01 h per token)",
+                "stored per head (33.3 GB in HBM, head h's path 0.4 + 0.01 h per token); selected_only_* the "
+                "same rows on a layer without a profile (no checker; the question rows' blocks split over the keys)",
     }
 
 

@@ -57,6 +57,20 @@ struct prefill_params {
   int64_t c_s0, c_s1, c_s2;
   const int32_t* grp;
   const int32_t* code;
+  // the lowest tile whose 32 keys are not all fixed (INT32_MAX: none)
+  const int32_t* dyn_floor;
+  // Key splits of the POLICY variant (split_role 0: none).  Role 1, the
+  // attention launch: workgroups [0, split_extra) run the extra parts listed
+  // in split_items (-1: unused), the others the row blocks in the usual
+  // order, part 0 of a split block.  Role 2, the fix-up launch: workgroup i
+  // walks split block split_blocks[i] (-1: none) unsplit when its part 0 left
+  // a column's positions below P-1, and writes the output.
+  int32_t split_role, split_extra;
+  const int32_t* split_plan;    // per logical workgroup: parts, first slot, split tile
+  const int32_t* split_items;   // extra parts: logical workgroup * 16 + part
+  const int32_t* split_blocks;  // logical workgroups that are split
+  float* part_o;                // [slot][128 dims][256 columns] unnormalised output
+  float* part_ml;               // [slot][3][256 columns] running max, sum, carry
 };
 
 namespace {
@@ -152,18 +166,23 @@ __device__ inline uint32_t lds_address(const void* p) {
       static_cast<uint32_t>(reinterpret_cast<uintptr_t>((CS_LDS const void*)p)));
 }
 
-// Flat workgroup id -> (batch, kv head, row block).  Dispatch is round-robin
-// over the 8 XCDs by id, so contiguous logical ranges are spread as one per
-// XCD: a (batch, kv head)'s K/V stays in one XCD's L2.  The heaviest
-// (right-most) row blocks go first.
-__device__ inline void decode_wg(const prefill_params& p, int& b, int& kvh, int& rb) {
-  const int id = blockIdx.x;
-  int logical = id;
-  if (p.total_wg % 8 == 0) logical = (id % 8) * (p.total_wg / 8) + id / 8;
+// Flat workgroup id -> logical workgroup -> (batch, kv head, row block).
+// Dispatch is round-robin over the 8 XCDs by id, so contiguous logical
+// ranges are spread as one per XCD: a (batch, kv head)'s K/V stays in one
+// XCD's L2.  The heaviest (right-most) row blocks go first.
+__device__ inline int logical_wg(const prefill_params& p, int id) {
+  return p.total_wg % 8 == 0 ? (id % 8) * (p.total_wg / 8) + id / 8 : id;
+}
+
+__device__ inline void decode_logical(const prefill_params& p, int logical, int& b, int& kvh, int& rb) {
   rb = p.row_blocks - 1 - (logical % p.row_blocks);
   const int rest = logical / p.row_blocks;
   kvh = rest % p.hkv;
   b = rest / p.hkv;
+}
+
+__device__ inline void decode_wg(const prefill_params& p, int& b, int& kvh, int& rb) {
+  decode_logical(p, logical_wg(p, static_cast<int>(blockIdx.x)), b, kvh, rb);
 }
 
 struct stage_t {

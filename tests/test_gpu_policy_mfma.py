@@ -392,3 +392,41 @@ def test_screened_block_after_the_row(device, monkeypatch, case, mode, want):
                                 device, monkeypatch)
     compare(expected, actual)
     assert "cs_ccpe_attention" not in called, called
+
+
+@pytest.mark.parametrize("low_gates", [False, True])
+def test_key_split_selected_call_matches_generic_and_oracle(device, monkeypatch, low_gates):
+    """A call long enough for the key splits, on a layer without a profile
+    (SelectedAssociationPolicy alone, so no checker runs beside the
+    attention): 4800 fixed keys, 256 recomputed (the question rows), 32 more
+    fixed; the rows are 200 selected fixed rows of the first chunk and the 256
+    question rows.  The question rows walk every causal key, so their row
+    blocks are split into parts over the keys.  With saturating positions the
+    parts' states are merged; with low gates (positions still rising ~1000
+    keys below the diagonal) part 0 ends unsaturated and the block is walked
+    again unsplit.  Both must equal the generic kernel on every row and the
+    oracle on sampled rows."""
+    a, dyn, b = 4800, 256, 32
+    q, k, v, e, plan, _, _ = long_case(70 + int(low_gates), low_gates=low_gates, a=a, dyn=dyn, b=b)
+    n = q.shape[0]
+    fixed = list(plan.fixed_indices)
+    sel = np.sort(np.random.default_rng(71).choice(np.arange(a), 200, replace=False))
+    rows = np.concatenate([sel, np.arange(a, a + dyn)])
+    actual, called = device_run(q, k, v, e, rows, plan, None, "strict_contextual", sel, 64, device, monkeypatch)
+    assert actual[0] == "ok" and "cs_ccpe_attention" not in called, (actual[:3], called)
+    cope = CoPE(D, P, device=device)
+    with torch.no_grad():
+        cope.position_embeddings.copy_(torch.from_numpy(e))
+    as_bf16 = lambda x: torch.from_numpy(x).to(device=device, dtype=torch.bfloat16)  # noqa: E731
+    visibility = SelectedAssociationPolicy(plan.fixed_indices, torch.tensor(sel, device=device))
+    ref = cope_attention(as_bf16(q[rows]), as_bf16(k), as_bf16(v), cope, torch.from_numpy(rows).to(device),
+                         torch.arange(n, device=device), visibility_transform=visibility, query_chunk_size=64)
+    assert_close_bf16(actual[1], ref.float().cpu().numpy())
+    pick = np.array([0, 57, 123, 199, 200, 201, 300, 383, 455])  # indices into rows
+
+    def oracle_visibility(qpos, kpos):
+        return orc.selected_visibility(qpos, kpos, fixed, sel)
+
+    want = orc.cope_attention(q[rows[pick]], k, v, e, rows[pick], visibility_transform=oracle_visibility,
+                              query_chunk_size=64)
+    assert_close_bf16(actual[1][torch.from_numpy(pick).to(device)], want)
