@@ -488,6 +488,7 @@ def decode_e2e_measure(device, tokens: int = 128, warmup: int = 4) -> dict:
     the fused decode), after ``warmup`` untimed steps."""
     import torch
 
+    from cacheslide_amd.ccpe import SharedRuns
     from cacheslide_amd.decode_model import MISTRAL_7B, PagedDecoder
 
     B, CTX, CHUNKS, BS = 64, 32768, 16, 16
@@ -514,6 +515,37 @@ def decode_e2e_measure(device, tokens: int = 128, warmup: int = 4) -> dict:
     out = model.generate(first, lengths, caches, table, tokens, max_context=max_context)
     torch.cuda.synchronize()
     seconds = time.perf_counter() - t0
+    # the same generation with the shared chunks read once per step for the
+    # batch (ccpe_decode_shared): runs = the 16 chunks, each request's slots
+    # its rotation; the last 256 shared keys and the request's own keys exact
+    runs = SharedRuns(table, torch.arange(shared, dtype=torch.int32).view(CHUNKS, chunk_blocks), rotation, BS,
+                      margin=256, pieces=2)
+    model.generate(first, lengths, caches, table, warmup, max_context=max_context, shared=runs)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    out_shared = model.generate(first, lengths, caches, table, tokens, max_context=max_context, shared=runs)
+    torch.cuda.synchronize()
+    seconds_shared = time.perf_counter() - t0
+    # one step from the same state both ways: the logits agree to the bf16
+    # level (greedy runs of a random-weight model then part at near-ties)
+    from cacheslide_amd import _hip
+    from cacheslide_amd.ccpe import decode_shared_workspace, decode_workspace
+    flags = _hip.new_flags(device)
+    pos = lengths.to(torch.long)
+    la = model.step(first, pos, caches, table, max_context=max_context, flags=flags,
+                    workspace=decode_workspace(B, shape.heads, max_context, 1024, device)).float()
+    lb = model.step(first, pos, caches, table, max_context=max_context, flags=flags, shared=runs,
+                    workspace=decode_shared_workspace(B, shape.heads, runs, max_context, 1024, device)).float()
+    # control: the exact per-request decode against itself with another split
+    # (only the summation order of the attention differs)
+    lc = model.step(first, pos, caches, table, max_context=max_context, flags=flags, split=512,
+                    workspace=decode_workspace(B, shape.heads, max_context, 512, device)).float()
+    logit_rel = float((la - lb).abs().max() / la.abs().max())
+    control_rel = float((la - lc).abs().max() / la.abs().max())
+    top1 = float((la.argmax(-1) == lb.argmax(-1)).float().mean())
+    control_top1 = float((la.argmax(-1) == lc.argmax(-1)).float().mean())
+    top2_gap = float((la.topk(2, dim=-1).values.diff(dim=-1).abs() / la.abs().max()).median())
+    del out_shared
     kv_bytes_step = sum(B * (CTX + t + 1) * shape.kv_heads * 128 * 2 * 2 for t in range(tokens)) / tokens
     hbm_ideal_ms = (shape.layers * kv_bytes_step + 2 * shape.parameters) / PEAK_HBM_GBS / 1e6
     distinct = len(set(out[:, 0].tolist()))
@@ -532,6 +564,19 @@ def decode_e2e_measure(device, tokens: int = 128, warmup: int = 4) -> dict:
         "note": "the ideal counts every K/V byte from HBM; the 16 shared chunks are 134 MB per layer, "
                 "so most K/V reads can hit the 256 MB Infinity Cache",
         "distinct_tokens_request_0": distinct,
+        "shared_runs": {
+            "seconds": round(seconds_shared, 3),
+            "ms_per_step": round(seconds_shared * 1e3 / tokens, 3),
+            "tok_per_s": round(B * tokens / seconds_shared, 1),
+            "one_step_logits_max_rel_diff": round(logit_rel, 6),
+            "one_step_argmax_equal": round(top1, 4),
+            "control_split_512_logits_max_rel_diff": round(control_rel, 6),
+            "control_split_512_argmax_equal": round(control_top1, 4),
+            "one_step_median_top2_gap_rel": round(top2_gap, 6),
+            "note": "ccpe_decode_shared: each of the 16 chunks read once per layer and step for the 64 requests "
+                    "(positions P-1), every request's last 256 chunk keys and own keys with exact positions, the "
+                    "two softmax states merged; the exact decode runs where a tail's gate mass stays below P-1",
+        },
     }
 
 

@@ -165,6 +165,35 @@ class CsKvSource(ctypes.Structure):
     ]
 
 
+class CsDecodeSharedArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("q_s_batch", ctypes.c_int64),
+        ("q_s_head", ctypes.c_int64),
+        ("batch", ctypes.c_int32),
+        ("hq", ctypes.c_int32),
+        ("hkv", ctypes.c_int32),
+        ("nk", ctypes.c_void_p),
+        ("max_nk", ctypes.c_int32),
+        ("kv", ctypes.POINTER(CsKvSource)),
+        ("e", ctypes.c_void_p),
+        ("max_positions", ctypes.c_int32),
+        ("split", ctypes.c_int32),
+        ("head_table", ctypes.c_void_p),
+        ("head_items", ctypes.c_int32),
+        ("head_blocks", ctypes.c_int32),
+        ("head_nk", ctypes.c_void_p),
+        ("head_qpos", ctypes.c_void_p),
+        ("tail_table", ctypes.c_void_p),
+        ("tail_stride", ctypes.c_int64),
+        ("tail_cols", ctypes.c_int32),
+        ("tail_nk", ctypes.c_void_p),
+        ("tail_qpos", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("flags", ctypes.c_void_p),
+    ]
+
+
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _I32 = ctypes.c_int32
@@ -199,6 +228,8 @@ SIGNATURES = {
         [_P, _I64, _I64, _I32, _I32, _I32, _P, _I32, ctypes.POINTER(CsKvSource), _P,
          _I32, _I32, _P, _I64, _P, _P, _P],
     ),
+    "cs_ccpe_decode_shared_workspace_bytes": (_I64, [_I32, _I32, _I32, _I32, _I32]),
+    "cs_ccpe_decode_shared_bf16": (_I32, [ctypes.POINTER(CsDecodeSharedArgs), _P, _I64, _P]),
     "cs_ccpe_decode_bf16_noalloc": (
         _I32,
         [_P, _I64, _I64, _I32, _I32, _I32, _P, _I32, ctypes.POINTER(CsKvSource), _P,

@@ -19,9 +19,14 @@ positions 0..nk-1.  Key j of a request is addressed either
 * ``ccpe_prefill_paged``: many query rows per request (MFMA kernel).
 * ``ccpe_decode_paged``: one new row per request at position nk-1 (split-K
   kernel with speculative saturation).
+* ``ccpe_decode_shared``: the same decode when the requests' block tables
+  start with runs of blocks that several requests share (reused chunks,
+  ``SharedRuns``): each run is read once for the whole batch.
 """
 
 from __future__ import annotations
+
+import ctypes
 
 import torch
 from torch import Tensor
@@ -297,6 +302,168 @@ def ccpe_decode_arena(query: Tensor, arena, cope, *, split: int = 1024, check: b
         return ccpe_decode_paged(query, arena.cache, None, lens, cope, slots=slots.unsqueeze(0),
                                  side_k=side_k, side_v=side_v, max_context=max(n, 1), split=split,
                                  check=check)
+
+
+class SharedRuns:
+    """Requests whose block tables start with runs of shared blocks.
+
+    ``runs`` (int [R, run_blocks]) names the blocks of each shared run (a
+    reused chunk), ``request_runs`` (int [B, S]) the run at each of request
+    b's first S run slots, in key order: ``block_table[b, :S * run_blocks]``
+    must be those runs' blocks one after the other (checked here, once).  A
+    request holds a run at most once.  The last ``margin`` keys of every
+    request's shared part (a multiple of the block size, at least one block)
+    and its keys after it form its tail, computed with exact contextual
+    positions; the rest of the shared part is read run by run for the whole
+    batch with every position P-1, which holds when the tail's gate mass
+    reaches P-1 and is checked on the device each call (``ccpe_decode_shared``
+    runs the exact decode where it does not).  Each run is cut into
+    ``pieces`` equal parts, the units of work of the shared read.
+    """
+
+    def __init__(self, block_table: Tensor, runs, request_runs, block_size: int, *, margin: int = 256,
+                 pieces: int = 2):
+        runs = torch.as_tensor(runs, dtype=torch.int32).cpu()
+        request_runs = torch.as_tensor(request_runs, dtype=torch.int64).cpu()
+        if runs.ndim != 2 or request_runs.ndim != 2 or runs.shape[1] < 1:
+            raise ValueError("runs must be [R, run_blocks] and request_runs [B, S]")
+        if block_table.ndim != 2 or block_table.dtype != torch.int32 or block_table.stride(1) != 1:
+            raise ValueError("block_table must be int32 [batch, max_blocks] with contiguous rows")
+        n_runs, run_blocks = runs.shape
+        b, n_slots = request_runs.shape
+        if b != block_table.shape[0]:
+            raise ValueError("request_runs must have one row per request")
+        if n_slots < 1 or bool((request_runs < 0).any()) or bool((request_runs >= n_runs).any()):
+            raise ValueError("request_runs must name runs, at least one per request")
+        if any(len(set(row.tolist())) != n_slots for row in request_runs):
+            raise ValueError("a request holds a run at most once")
+        if type(margin) is not int or margin < block_size or margin % block_size:
+            raise ValueError("margin must be a positive multiple of the block size")
+        if type(pieces) is not int or pieces < 1 or run_blocks % pieces:
+            raise ValueError("pieces must divide the run's blocks")
+        shared_blocks = n_slots * run_blocks
+        run_keys = run_blocks * block_size
+        if margin >= shared_blocks * block_size:
+            raise ValueError("margin must leave keys of the shared part outside the tail")
+        if shared_blocks > block_table.shape[1]:
+            raise ValueError("block_table is shorter than the requests' shared parts")
+        expect = runs[request_runs].reshape(b, shared_blocks)
+        if not torch.equal(block_table[:, :shared_blocks].cpu(), expect):
+            raise ValueError("block_table does not start with the requests' runs")
+        piece_blocks = run_blocks // pieces
+        piece_keys = piece_blocks * block_size
+        device = block_table.device
+        self.block_size = block_size
+        self.head_items = n_runs * pieces
+        self.head_blocks = piece_blocks
+        self.head_table = runs.view(n_runs * pieces, piece_blocks).contiguous().to(device)
+        self.head_nk = torch.full((self.head_items,), piece_keys, dtype=torch.int32, device=device)
+        # request b sees keys [0, limit) of its slot s's run, limit = run_keys
+        # except in the slots the tail reaches into
+        tail_key = shared_blocks * block_size - margin        # first tail key of every request
+        qpos = torch.full((self.head_items, b), -1, dtype=torch.int64)
+        for slot in range(n_slots):
+            limit = min(run_keys, max(tail_key - slot * run_keys, 0))
+            for k in range(pieces):
+                visible = min(max(limit - k * piece_keys, 0), piece_keys)
+                items = request_runs[:, slot] * pieces + k
+                qpos[items, torch.arange(b)] = visible - 1
+        self.head_qpos = qpos.to(device)
+        self.tail_block = tail_key // block_size              # first block of the tail
+        self.tail_table = block_table[:, self.tail_block:]
+        self.batch = b
+
+    def tail_lens(self, context_lens: Tensor) -> tuple[Tensor, Tensor]:
+        """Key counts of the tails (int32) and their query keys (int64)."""
+        tail_nk = context_lens - self.tail_block * self.block_size
+        return tail_nk, (tail_nk - 1).to(torch.int64)
+
+
+def decode_shared_workspace(batch: int, heads: int, shared: SharedRuns, max_context: int, split: int,
+                            device) -> Tensor:
+    nbytes = int(_hip.load().cs_ccpe_decode_shared_workspace_bytes(batch, heads, shared.head_items, max_context,
+                                                                      split))
+    return torch.empty(max(nbytes, 256) + 256, dtype=torch.uint8, device=device)
+
+
+def ccpe_decode_shared(
+    query: Tensor,
+    cache: Tensor,
+    block_table: Tensor,
+    context_lens: Tensor,
+    cope,
+    shared: SharedRuns,
+    *,
+    max_context: int,
+    split: int = 1024,
+    tail: tuple[Tensor, Tensor] | None = None,
+    workspace: Tensor | None = None,
+    out: Tensor | None = None,
+    flags: Tensor | None = None,
+    check: bool = True,
+) -> Tensor:
+    """``ccpe_decode_paged`` over ``block_table`` (same arguments and result)
+    with the requests' shared runs (``shared``, built on this block table)
+    read once for the batch.  Every request's context must extend past its
+    shared part's tail start (``context_lens > shared.tail_block * block
+    size``).  ``tail``: ``shared.tail_lens(context_lens)`` when the caller has
+    it; ``workspace``: ``decode_shared_workspace(...)`` bytes."""
+    device = _hip.require_device(query, cache, context_lens, block_table)
+    if query.ndim != 3 or query.dtype != torch.bfloat16 or query.shape[2] != 128 or query.stride(2) != 1:
+        raise ValueError("query must be bf16 [batch, heads, 128] with contiguous rows")
+    b, hq = query.shape[0], query.shape[1]
+    hkv = cache.shape[1]
+    if hq % hkv or hq // hkv > 8:
+        raise ValueError("decode supports GQA groups of at most 8 query heads per KV head")
+    if context_lens.shape != (b,) or context_lens.dtype != torch.int32:
+        raise ValueError("context_lens must be int32 [batch]")
+    if shared.batch != b or shared.block_size != cache.shape[2]:
+        raise ValueError("shared runs were built for another batch or block size")
+    if type(max_context) is not int or max_context < 1:
+        raise ValueError("max_context must be a positive integer")
+    e = _check_e(cope, device)
+    src = _paged_source(cache, block_table)
+    tail_nk, tail_qpos = shared.tail_lens(context_lens) if tail is None else tail
+    nbytes = int(_hip.load().cs_ccpe_decode_shared_workspace_bytes(b, hq, shared.head_items, max_context, split))
+    if workspace is None:
+        workspace = decode_shared_workspace(b, hq, shared, max_context, split, device)
+    start = (-workspace.data_ptr()) % 256
+    have = workspace.numel() * workspace.element_size() - start
+    if workspace.device != device or have < nbytes:
+        raise ValueError(f"decode workspace holds {have} bytes after alignment, the call needs {nbytes}")
+    if flags is None:
+        flags = _hip.new_flags(device)
+    if out is None:
+        out = torch.empty((b, hq, 128), dtype=torch.bfloat16, device=device)
+    elif (out.shape != (b, hq, 128) or out.dtype != torch.bfloat16 or out.device != device
+          or not out.is_contiguous()):
+        raise ValueError("out must be a contiguous bf16 [batch, heads, 128] tensor on the query device")
+    args = _hip.CsDecodeSharedArgs()
+    args.q = query.data_ptr()
+    args.q_s_batch, args.q_s_head = query.stride(0), query.stride(1)
+    args.batch, args.hq, args.hkv = b, hq, hkv
+    args.nk = context_lens.data_ptr()
+    args.max_nk = max_context
+    args.kv = ctypes.pointer(src)
+    args.e = e.data_ptr()
+    args.max_positions = cope.max_positions
+    args.split = split
+    args.head_table = shared.head_table.data_ptr()
+    args.head_items, args.head_blocks = shared.head_items, shared.head_blocks
+    args.head_nk = shared.head_nk.data_ptr()
+    args.head_qpos = shared.head_qpos.data_ptr()
+    args.tail_table = shared.tail_table.data_ptr()
+    args.tail_stride = shared.tail_table.stride(0)
+    args.tail_cols = shared.tail_table.shape[1]
+    args.tail_nk = tail_nk.data_ptr()
+    args.tail_qpos = tail_qpos.data_ptr()
+    args.out = out.data_ptr()
+    args.flags = flags.data_ptr()
+    call("cs_ccpe_decode_shared_bf16", ctypes.byref(args), workspace.data_ptr() + start, have,
+         _hip.stream_of(device))
+    if check:
+        raise_flags(flags)
+    return out
 
 
 def raise_flags(flags: Tensor) -> None:

@@ -30,6 +30,7 @@
 // block table or the per-token slot map (native slot or sidecar row).
 
 #include "common.h"
+#include "ccpe_path.h"
 
 #include <mutex>
 
@@ -90,6 +91,9 @@ struct decode_params {
   float* acc;          // [B, hq, smax, 128]
   uint16_t* out;
   int32_t* flags;
+  // when non-null, the call runs only if *gate != 0 (read by every
+  // workgroup): the exact fallback of a shared-chunk decode
+  const int32_t* gate;
 };
 
 __device__ inline int64_t ws_index(const decode_params& p, int b, int h, int r) {
@@ -824,6 +828,7 @@ __device__ void combine_pair(const decode_params& p, smem_t<G>& s, int b, int ha
 template <int G, bool PAGED>
 __global__ void __launch_bounds__(kThreads) decode_main_kernel(decode_params p) {
   __shared__ smem_t<G> s;
+  if (p.gate != nullptr && __builtin_amdgcn_readfirstlane(*p.gate) == 0) return;  // before any barrier
   const int per_r = p.hkv * p.batch;
   const int id = blockIdx.x;
   const int r = id / per_r, rem = id % per_r;
@@ -850,6 +855,7 @@ __global__ void __launch_bounds__(kThreads) decode_main_kernel(decode_params p) 
 template <int G, bool PAGED>
 __global__ void __launch_bounds__(kThreads) decode_finish_kernel(decode_params p) {
   __shared__ smem_t<G> s;
+  if (p.gate != nullptr && __builtin_amdgcn_readfirstlane(*p.gate) == 0) return;  // before any barrier
   const int b = blockIdx.x / p.hkv, kvh = blockIdx.x % p.hkv;
   const int h0 = kvh * G;
   int splits = (keys_of(p, b) + p.split - 1) / p.split;
@@ -1099,4 +1105,172 @@ extern "C" int cs_ccpe_decode_bf16(const void* q, int64_t q_s_batch, int64_t q_s
              static_cast<long long>(workspace_bytes), static_cast<long long>(need));
   CS_REQUIRE((reinterpret_cast<uintptr_t>(workspace) % 16) == 0, "workspace must be aligned");
   return launch_decode(p, workspace, stream);
+}
+
+// ---- decode over shared runs of blocks ---------------------------------------
+namespace {
+
+// One workgroup per (request, KV head), one thread per (head of the group,
+// dim): the tail state and the head_items run states of each head combined
+// against their common maximum (raw scores q.k, shifted bias: the two
+// launches share the convention).  The (max, sum) pairs go through LDS first,
+// so that each thread's output loads are independent of each other.  A head
+// whose tail gate mass is below P-1 (or NaN) sets *gate: the caller's exact
+// fallback then runs.
+constexpr int kMergeItems = 64;  // run pieces merged at once
+__global__ void __launch_bounds__(1024) shared_merge_kernel(const float* tail_o, const float* tail_ml,
+                                                            const float* head_o, const float* head_ml,
+                                                            int32_t batch, int32_t hq, int32_t group,
+                                                            int32_t items, float top, uint16_t* out,
+                                                            int32_t* gate) {
+  __shared__ float wgt[8][kMergeItems + 1];
+  __shared__ float sums[8];
+  const int b = blockIdx.x / (hq / group), kvh = blockIdx.x % (hq / group);
+  const int hl = threadIdx.x / kD, d = threadIdx.x % kD;
+  const bool live = hl < group;
+  const int h = kvh * group + (live ? hl : 0);
+  constexpr float kC = kInvSqrtD * kLog2e;
+  const int64_t th = static_cast<int64_t>(b) * hq + h;  // tail state [B, 1, Hq]
+  float o = 0.f, l_all = 0.f;
+  float mx = -INFINITY;
+  // the common maximum over the tail and every piece
+  if (live && d == 0) {
+    mx = tail_ml[3 * th];
+    for (int i = 0; i < items; ++i) mx = fmaxf(mx, head_ml[3 * ((static_cast<int64_t>(i) * batch + b) * hq + h)]);
+    if (!(tail_ml[3 * th + 2] >= top)) atomicOr(gate, 1);
+  }
+  for (int i0 = -1; i0 < items; i0 += kMergeItems) {
+    // weights of states i0 .. i0 + kMergeItems - 1 (state -1: the tail)
+    if (live && d == 0) {
+      float lsum = 0.f;
+      for (int j = 0; j < kMergeItems && i0 + j < items; ++j) {
+        const int i = i0 + j;
+        const float* ml = i < 0 ? tail_ml + 3 * th : head_ml + 3 * ((static_cast<int64_t>(i) * batch + b) * hq + h);
+        const float w = mx == -INFINITY || ml[0] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((ml[0] - mx) * kC);
+        wgt[hl][j] = w;
+        lsum += w * ml[1];
+      }
+      sums[hl] = lsum;
+      wgt[hl][kMergeItems] = mx;
+    }
+    __syncthreads();
+    if (live) {
+      l_all += sums[hl];
+      mx = wgt[hl][kMergeItems];
+      const int n = items - i0 < kMergeItems ? items - i0 : kMergeItems;
+      int j = 0;
+      for (; j + 8 <= n; j += 8) {
+        float a[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int i = i0 + j + u;
+          a[u] = i < 0 ? tail_o[th * kD + d] : head_o[((static_cast<int64_t>(i) * batch + b) * hq + h) * kD + d];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) o += wgt[hl][j + u] * a[u];
+      }
+      for (; j < n; ++j) {
+        const int i = i0 + j;
+        o += wgt[hl][j] * (i < 0 ? tail_o[th * kD + d] : head_o[((static_cast<int64_t>(i) * batch + b) * hq + h) * kD + d]);
+      }
+    }
+    __syncthreads();
+  }
+  if (live) out[th * kD + d] = float_to_bf16(l_all > 0.f ? o / l_all : 0.f);
+}
+
+struct shared_ws {
+  float* head_o;
+  float* head_ml;
+  float* tail_o;
+  float* tail_ml;
+  int32_t* gate;
+  void* decode;
+  int64_t decode_bytes;
+  int64_t bytes;
+};
+
+shared_ws carve_shared(char* base, int32_t batch, int32_t hq, int32_t items, int32_t max_nk, int32_t split) {
+  shared_ws w{};
+  int64_t off = 0;
+  auto take = [&](int64_t bytes) {
+    char* at = base ? base + off : nullptr;
+    off += (bytes + 255) / 256 * 256;
+    return at;
+  };
+  const int64_t rows_h = static_cast<int64_t>(items) * batch * hq, rows_t = static_cast<int64_t>(batch) * hq;
+  w.head_o = reinterpret_cast<float*>(take(4 * rows_h * kD));
+  w.head_ml = reinterpret_cast<float*>(take(4 * rows_h * 3));
+  w.tail_o = reinterpret_cast<float*>(take(4 * rows_t * kD));
+  w.tail_ml = reinterpret_cast<float*>(take(4 * rows_t * 3));
+  w.gate = reinterpret_cast<int32_t*>(take(4));
+  w.decode_bytes = cs_ccpe_decode_workspace_bytes(batch, hq, max_nk, split);
+  w.decode = take(w.decode_bytes);
+  w.bytes = off;
+  return w;
+}
+
+}  // namespace
+
+extern "C" int64_t cs_ccpe_decode_shared_workspace_bytes(int32_t batch, int32_t hq, int32_t head_items,
+                                                         int32_t max_nk, int32_t split) {
+  if (batch < 0 || hq <= 0 || head_items < 0 || max_nk < 0 || split <= 0) return 0;
+  return carve_shared(nullptr, batch, hq, head_items, max_nk, split).bytes;
+}
+
+extern "C" int cs_ccpe_decode_shared_bf16(const cs_decode_shared_args* a, void* workspace, int64_t workspace_bytes,
+                                          void* stream) {
+  CS_REQUIRE(a != nullptr && a->kv != nullptr, "null arguments");
+  CS_REQUIRE(a->kv->block_table != nullptr && a->kv->slots == nullptr,
+             "the shared-run decode reads the cache through block tables");
+  CS_REQUIRE(a->head_table && a->head_nk && a->head_qpos && a->tail_table && a->tail_nk && a->tail_qpos,
+             "null shared-run arguments");
+  CS_REQUIRE(a->head_items >= 0 && a->head_blocks > 0 && a->tail_cols > 0 && a->tail_stride >= a->tail_cols,
+             "bad shared-run shapes");
+  CS_REQUIRE(a->batch >= 0 && a->hq > 0 && a->hkv > 0 && a->hq % a->hkv == 0 && a->hq / a->hkv <= 8,
+             "bad head counts");
+  // the exact fallback, prepared first: it validates the call as cs_ccpe_decode_bf16 does
+  decode_params p{};
+  int st = prepare_decode(a->q, a->q_s_batch, a->q_s_head, a->batch, a->hq, a->hkv, a->nk, a->max_nk, a->kv, a->e,
+                          a->max_positions, a->split, a->out, a->flags, &p);
+  if (st) return st;
+  const shared_ws need = carve_shared(nullptr, a->batch, a->hq, a->head_items, a->max_nk, a->split);
+  CS_REQUIRE(workspace != nullptr && workspace_bytes >= need.bytes &&
+                 (reinterpret_cast<uintptr_t>(workspace) % 256) == 0,
+             "shared-run decode workspace holds %lld bytes, the call needs %lld (256-byte aligned)",
+             static_cast<long long>(workspace_bytes), static_cast<long long>(need.bytes));
+  if (a->batch == 0) return CS_OK;
+  const shared_ws w = carve_shared(static_cast<char*>(workspace), a->batch, a->hq, a->head_items, a->max_nk,
+                                   a->split);
+  hipStream_t s = as_stream(stream);
+  // head: every run once for all requests (rows = requests), positions P-1
+  if (a->head_items > 0) {
+    cs_kv_source kh = *a->kv;
+    kh.block_table = a->head_table;
+    kh.bt_stride = a->head_blocks;
+    kh.bt_cols = a->head_blocks;
+    st = cs::launch_prefill_states(a->q, 0, a->q_s_batch, a->q_s_head, a->head_qpos, a->batch, a->head_items,
+                                   a->batch, a->hq, a->hkv, a->head_nk, &kh, a->e, a->max_positions, 1, 8,
+                                   w.head_o, w.head_ml, nullptr, a->flags, s);
+    if (st) return st;
+  }
+  // tail: one query row per request, exact positions, narrow workgroups;
+  // the launch also clears the fallback's gate word
+  cs_kv_source kt = *a->kv;
+  kt.block_table = a->tail_table;
+  kt.bt_stride = a->tail_stride;
+  kt.bt_cols = a->tail_cols;
+  st = cs::launch_prefill_states(a->q, a->q_s_batch, 0, a->q_s_head, a->tail_qpos, 1, a->batch, 1, a->hq, a->hkv,
+                                 a->tail_nk, &kt, a->e, a->max_positions, 0, 2, w.tail_o, w.tail_ml, w.gate,
+                                 a->flags, s);
+  if (st) return st;
+  const int group = a->hq / a->hkv;
+  hipLaunchKernelGGL(shared_merge_kernel, dim3(static_cast<uint32_t>(a->batch) * a->hkv), dim3(kD * group), 0, s,
+                     w.tail_o, w.tail_ml, w.head_o, w.head_ml, a->batch, a->hq, group, a->head_items,
+                     static_cast<float>(a->max_positions - 1), static_cast<uint16_t*>(a->out), w.gate);
+  CS_LAUNCH_CHECK("ccpe_decode_shared_merge");
+  // the exact decode over the full block table, run only when some tail left a
+  // head's positions below P-1
+  p.gate = w.gate;
+  return launch_decode(p, w.decode, stream);
 }

@@ -108,4 +108,17 @@ struct policy_check_args {
 
 int launch_policy_check(const policy_check_args& a, hipStream_t stream);
 
+// The paged MFMA prefill (ccpe_prefill.hip) writing per (batch item, row,
+// head) softmax states: fp32 state_o [B, nq, Hq, 128] (the output
+// unnormalised against the running max of the raw scores q.k, with the
+// positional bias shifted so that a saturated key adds 0) and state_ml
+// [B, nq, Hq, 3] (max, sum, carry: the gate mass counted from the row's key,
+// >= P-1 once saturated).  saturated != 0: every position taken as P-1.
+// zero_word (may be null): set to 0 by the launch.
+int launch_prefill_states(const void* q, int64_t q_s_batch, int64_t q_s_tok, int64_t q_s_head,
+                          const int64_t* qpos, int64_t qpos_s_batch, int32_t batch, int32_t nq, int32_t hq,
+                          int32_t hkv, const int32_t* nk, const cs_kv_source* kv, const float* e,
+                          int32_t max_positions, int32_t saturated, int max_waves, float* state_o,
+                          float* state_ml, int32_t* zero_word, int32_t* flags, hipStream_t s);
+
 }  // namespace cs

@@ -155,6 +155,7 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
   }
 
   if (tid == 0) wg_max_pos = 0;
+  if (tid == 0 && blockIdx.x == 0 && p.zero_word != nullptr) *p.zero_word = 0;
   __syncthreads();
   int64_t wmax = qp, wmin = row_ok ? qp : INT64_MAX;
   for (int off = 32; off > 0; off >>= 1) {
@@ -440,8 +441,8 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
   // ---- per-tile compute -------------------------------------------------------
   const float top = static_cast<float>(p.npos - 1);
   // padded columns count as saturated, and so do the columns of a split part
-  // below the keys next to the diagonals
-  float carry = !row_ok ? 3.0e38f : (part > 0 ? top : 0.f);
+  // below the keys next to the diagonals and those of a saturated call
+  float carry = !row_ok ? 3.0e38f : (part > 0 || p.saturated ? top : 0.f);
   // Running max of the column's raw scores q.k.  S^T accumulates onto minit =
   // -m_base in every register (m_base = m_run once finite, 0 before), so the
   // scores arrive shifted by the running max: exp2 of a score is one multiply
@@ -809,6 +810,29 @@ walk_done:
 
   // ---- epilogue: O^T lane holds column n, dims 32 db + 8 (v/4) + 4h + v%4 ----------
   const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  if (p.state_o != nullptr) {
+    // the column's softmax state, for a merge with states over other keys
+    if (bad_block) atomicOr(p.flags, CS_FLAG_BLOCK_INVALID);
+    if (row_ok) {
+      const int64_t rh = (static_cast<int64_t>(b) * p.nq + row) * p.hq + head;
+      float* so = p.state_o + rh * kD;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int j4 = 0; j4 < 4; ++j4) {
+          floatx4 w;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) w[e] = o[db][4 * j4 + e];
+          *reinterpret_cast<floatx4*>(so + 32 * db + 8 * j4 + 4 * h) = w;
+        }
+      if (h == 0) {
+        p.state_ml[3 * rh] = m_run;
+        p.state_ml[3 * rh + 1] = l_tot;
+        p.state_ml[3 * rh + 2] = carry;
+      }
+    }
+    return;
+  }
   if (nparts > 1) {
     // a part's softmax state for policy_split_merge_kernel: O unnormalised
     // against the part's running max, that max, the sum and the carry
@@ -965,7 +989,7 @@ int prepare_prefill(const void* q, int64_t q_s_batch, int64_t q_s_tok, int64_t q
                     const int64_t* qpos, int64_t qpos_s_batch, int32_t batch, int32_t nq, int32_t hq,
                     int32_t hkv, const int32_t* nk, const cs_kv_source* kv, const float* e,
                     int32_t max_positions, void* out, int32_t* flags, cs::prefill_params* pp,
-                    int* waves_out, size_t* smem_out) {
+                    int* waves_out, size_t* smem_out, int max_waves = 8) {
   CS_REQUIRE(q && qpos && nk && e && out && flags, "null arguments");
   CS_REQUIRE(batch >= 0 && nq >= 0 && hq > 0 && hkv > 0 && hq % hkv == 0, "bad head counts");
   CS_REQUIRE(max_positions >= 2 && max_positions <= kMaxPos, "max_positions must be in [2, %d]",
@@ -1020,6 +1044,8 @@ int prepare_prefill(const void* q, int64_t q_s_batch, int64_t q_s_tok, int64_t q
   if (static_cast<int64_t>(batch) * hkv * ceil_div(nq, kCols * 4 / group) < 2 * device_cus() &&
       2 * (tab_bytes(2) + kStaticLds) <= kLdsLimit)
     waves = 2;
+  // a caller with few rows per workgroup (one per request) asks for narrow ones
+  while (waves > max_waves && waves > 2) waves /= 2;
   p.rows_per_wg = kCols * waves / group;
   p.row_blocks = static_cast<int32_t>(ceil_div(nq, p.rows_per_wg));
   p.nk = nk;
@@ -1440,6 +1466,44 @@ extern "C" int cs_ccpe_prefill_bf16(const void* q, int64_t q_s_batch, int64_t q_
   CS_LAUNCH_CHECK("ccpe_prefill");
   return CS_OK;
 }
+
+namespace cs {
+
+// The paged MFMA prefill writing softmax states (state_o, state_ml: see
+// prefill_params) instead of output rows; saturated: every position taken as
+// P-1; zero_word (may be null) is set to 0.  Workgroups of at most max_waves
+// wavefronts.
+int launch_prefill_states(const void* q, int64_t q_s_batch, int64_t q_s_tok, int64_t q_s_head,
+                          const int64_t* qpos, int64_t qpos_s_batch, int32_t batch, int32_t nq, int32_t hq,
+                          int32_t hkv, const int32_t* nk, const cs_kv_source* kv, const float* e,
+                          int32_t max_positions, int32_t saturated, int max_waves, float* state_o,
+                          float* state_ml, int32_t* zero_word, int32_t* flags, hipStream_t s) {
+  CS_REQUIRE(state_o && state_ml, "null state buffers");
+  cs::prefill_params p{};
+  int waves = 4;
+  size_t smem = 0;
+  const int st = prepare_prefill(q, q_s_batch, q_s_tok, q_s_head, qpos, qpos_s_batch, batch, nq, hq, hkv, nk, kv,
+                                 e, max_positions, state_o, flags, &p, &waves, &smem, max_waves);
+  if (st) return st;
+  if (batch == 0 || nq == 0) return CS_OK;
+  p.state_o = state_o;
+  p.state_ml = state_ml;
+  p.saturated = saturated ? 1 : 0;
+  p.zero_word = zero_word;
+  const dim3 grid(p.total_wg), block(64 * waves);
+  const int mode = p.kv.slots ? 2 : (p.kv.block_table ? 1 : 0);
+  CS_REQUIRE(mode == 1, "softmax states are written for block-table calls only");
+  if (waves == 8)
+    hipLaunchKernelGGL((ccpe_prefill_kernel<1, 8>), grid, block, smem, s, p);
+  else if (waves == 2)
+    hipLaunchKernelGGL((ccpe_prefill_kernel<1, 2>), grid, block, smem, s, p);
+  else
+    hipLaunchKernelGGL((ccpe_prefill_kernel<1, 4>), grid, block, smem, s, p);
+  CS_LAUNCH_CHECK("ccpe_prefill_states");
+  return CS_OK;
+}
+
+}  // namespace cs
 
 extern "C" int cs_prepare_device(void) {
   std::lock_guard<std::mutex> lock(g_side_mutex);

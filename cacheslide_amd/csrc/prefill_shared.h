@@ -71,6 +71,15 @@ struct prefill_params {
   const int32_t* split_blocks;  // logical workgroups that are split
   float* part_o;                // [slot][128 dims][256 columns] unnormalised output
   float* part_ml;               // [slot][3][256 columns] running max, sum, carry
+  // Softmax states instead of output rows (state_o non-null): per (batch
+  // item, row, head) the output unnormalised against the running max of the
+  // raw scores q.k, and (max, sum, carry).  saturated: every position is
+  // taken as P-1 (the carry starts there), for keys whose positions the
+  // caller has shown to be saturated.
+  float* state_o;   // [B, nq, Hq, 128]
+  float* state_ml;  // [B, nq, Hq, 3]
+  int32_t saturated;
+  int32_t* zero_word;  // when non-null, set to 0 by the launch (a flag a later launch raises)
 };
 
 namespace {

@@ -27,7 +27,8 @@ import torch.nn.functional as F
 from torch import Tensor
 
 from . import _hip
-from .ccpe import ccpe_decode_paged, decode_workspace, raise_flags
+from .ccpe import (SharedRuns, ccpe_decode_paged, ccpe_decode_shared, decode_shared_workspace, decode_workspace,
+                   raise_flags)
 from .position import CoPE
 
 HEAD_DIM = 128
@@ -113,11 +114,14 @@ class PagedDecoder:
 
     def step(self, ids: Tensor, positions: Tensor, caches: list[Tensor], block_table: Tensor, *,
              max_context: int, workspace: Tensor, flags: Tensor, split: int = 1024,
-             attn_out: Tensor | None = None) -> Tensor:
+             attn_out: Tensor | None = None, shared: SharedRuns | None = None) -> Tensor:
         """One token per request: ``ids`` [B] at ``positions`` [B] (int64, the
         request's key count before this token) -> logits [B, vocab].  Writes the
         token's K/V to slot ``block_table[b, p // bs] * bs + p % bs`` of every
-        layer's cache; ``max_context`` bounds positions + 1."""
+        layer's cache; ``max_context`` bounds positions + 1.  With ``shared``
+        (runs of blocks the requests share, built on ``block_table``) the
+        attention reads each run once for the batch (``ccpe_decode_shared``,
+        whose ``workspace`` this then is)."""
         s = self.shape
         b = ids.shape[0]
         bs = caches[0].shape[2]
@@ -127,6 +131,7 @@ class PagedDecoder:
             attn_out = torch.empty((b, s.heads, HEAD_DIM), dtype=self.dtype, device=self.device)
         stream = _hip.stream_of(self.device)
         lib = _hip.load()
+        tail = shared.tail_lens(context) if shared is not None else None
         q_end, k_end = s.heads * HEAD_DIM, (s.heads + s.kv_heads) * HEAD_DIM
         x, residual = self.embed[ids], None
         for layer, cache in zip(self.layers, caches):
@@ -143,8 +148,13 @@ class PagedDecoder:
                                          _hip.ptr(None), b, _hip.vref(k), _hip.vref(v), stream)
             if status:
                 _hip.check(status, "cs_slot_scatter")
-            ccpe_decode_paged(q, cache, block_table, context, layer.cope, max_context=max_context, split=split,
-                              workspace=workspace, out=attn_out, flags=flags, check=False)
+            if shared is not None:
+                ccpe_decode_shared(q, cache, block_table, context, layer.cope, shared, max_context=max_context,
+                                   split=split, tail=tail, workspace=workspace, out=attn_out, flags=flags,
+                                   check=False)
+            else:
+                ccpe_decode_paged(q, cache, block_table, context, layer.cope, max_context=max_context,
+                                  split=split, workspace=workspace, out=attn_out, flags=flags, check=False)
             residual = attn_out.view(b, s.hidden) @ layer.o.T + residual
             h = self._rms(residual, layer.post_norm)
             gate, up = (h @ layer.gate_up.T).split(s.ffn, dim=-1)
@@ -152,18 +162,23 @@ class PagedDecoder:
         return self._rms(x + residual, self.norm) @ self.lm_head.T
 
     def generate(self, first_ids: Tensor, lengths: Tensor, caches: list[Tensor], block_table: Tensor,
-                 steps: int, *, max_context: int, split: int = 1024, check: bool = True) -> Tensor:
+                 steps: int, *, max_context: int, split: int = 1024, check: bool = True,
+                 shared: SharedRuns | None = None) -> Tensor:
         """Greedy decoding of ``steps`` tokens per request after contexts of
-        ``lengths`` keys -> token ids [steps, B] (on the device)."""
+        ``lengths`` keys -> token ids [steps, B] (on the device); ``shared`` as
+        in ``step``."""
         b = first_ids.shape[0]
-        workspace = decode_workspace(b, self.shape.heads, max_context, split, self.device)
+        if shared is not None:
+            workspace = decode_shared_workspace(b, self.shape.heads, shared, max_context, split, self.device)
+        else:
+            workspace = decode_workspace(b, self.shape.heads, max_context, split, self.device)
         flags = _hip.new_flags(self.device)
         attn_out = torch.empty((b, self.shape.heads, HEAD_DIM), dtype=self.dtype, device=self.device)
         out = torch.empty((steps, b), dtype=torch.long, device=self.device)
         ids, positions = first_ids, lengths.to(torch.long).clone()
         for t in range(steps):
             logits = self.step(ids, positions, caches, block_table, max_context=max_context,
-                               workspace=workspace, flags=flags, split=split, attn_out=attn_out)
+                               workspace=workspace, flags=flags, split=split, attn_out=attn_out, shared=shared)
             ids = logits.argmax(dim=-1)
             out[t] = ids
             positions += 1

@@ -321,6 +321,53 @@ int cs_ccpe_decode_bf16(const void* q, int64_t q_s_batch, int64_t q_s_head, int3
                         int32_t split, void* workspace, int64_t workspace_bytes, void* out,
                         int32_t* flags, void* stream);
 
+/* The decode step of cs_ccpe_decode_bf16 over a paged cache whose requests
+ * share runs of blocks (reused chunks that several requests' contexts hold,
+ * in any order), with the same result: cope_attention at one query row
+ * (position.py:404-560, the decode call of runtime.py:489-508).
+ *   The keys of request b are split into a head, read from the shared runs,
+ * and a tail of its own blocks (the keys nearest the query, and the request's
+ * newer tokens).  Head: run i (head_table row i, head_nk[i] keys) is read
+ * once for every request; request b attends to its keys up to head_qpos[i, b]
+ * (int64, -1: none), with every position taken as P-1.  Tail (tail_table
+ * row b, tail_nk[b] keys, query at tail_qpos[b] = tail_nk[b] - 1): exact
+ * contextual positions.  The head and tail softmax states are merged per
+ * (request, head).  The head's positions are P-1 exactly when the tail's gate
+ * mass reaches P-1; where it does not, for any request and head, the call
+ * runs cs_ccpe_decode_bf16 over the full block table (kv) instead, so the
+ * result is always that call's.
+ *   The caller states that each request's head keys and tail keys are
+ * together its nk[b] keys, each once, the tail's in key order; the shared
+ * blocks' keys carry no position (saturated keys need none), the tail's do.
+ * workspace: cs_ccpe_decode_shared_workspace_bytes(batch, hq, head_items,
+ * max_nk, split) bytes, 256-byte aligned.  No counterpart in the reference:
+ * its decode gathers each request's keys (paged.py:433-472). */
+typedef struct cs_decode_shared_args {
+  const void* q;              /* [B, Hq, 128] bf16 */
+  int64_t q_s_batch, q_s_head;
+  int32_t batch, hq, hkv;
+  const int32_t* nk;          /* [B] key counts; the query is key nk[b] - 1 */
+  int32_t max_nk;
+  const cs_kv_source* kv;     /* the cache and every request's full block table */
+  const float* e;             /* [128, P] fp32 */
+  int32_t max_positions, split;
+  const int32_t* head_table;  /* [head_items, head_blocks] */
+  int32_t head_items, head_blocks;
+  const int32_t* head_nk;     /* [head_items] */
+  const int64_t* head_qpos;   /* [head_items, B] */
+  const int32_t* tail_table;  /* [B, tail_cols], rows tail_stride apart */
+  int64_t tail_stride;
+  int32_t tail_cols;
+  const int32_t* tail_nk;     /* [B] */
+  const int64_t* tail_qpos;   /* [B] */
+  void* out;                  /* [B, Hq, 128] bf16 */
+  int32_t* flags;
+} cs_decode_shared_args;
+int64_t cs_ccpe_decode_shared_workspace_bytes(int32_t batch, int32_t hq, int32_t head_items, int32_t max_nk,
+                                              int32_t split);
+int cs_ccpe_decode_shared_bf16(const cs_decode_shared_args* a, void* workspace, int64_t workspace_bytes,
+                               void* stream);
+
 /* Bytes of the static device scratch behind cs_ccpe_decode_bf16_noalloc. */
 #define CS_DECODE_SCRATCH_BYTES (64ll << 20)
 
