@@ -1113,70 +1113,68 @@ namespace {
 // One workgroup per (request, KV head), one thread per (head of the group,
 // dim): the tail state and the head_items run states of each head combined
 // against their common maximum (raw scores q.k, shifted bias: the two
-// launches share the convention).  The (max, sum) pairs go through LDS first,
-// so that each thread's output loads are independent of each other.  A head
-// whose tail gate mass is below P-1 (or NaN) sets *gate: the caller's exact
-// fallback then runs.
-constexpr int kMergeItems = 64;  // run pieces merged at once
+// launches share the convention).  Thread t of a head reads the (max, sum)
+// of state t - 1 (state -1: the tail), 128 at a time, so the maximum and the
+// weights come from LDS reductions; the output loads of a thread are then
+// independent of each other.  A head whose tail gate mass is below P-1 (or
+// NaN) sets *gate: the caller's exact fallback then runs.
 __global__ void __launch_bounds__(1024) shared_merge_kernel(const float* tail_o, const float* tail_ml,
                                                             const float* head_o, const float* head_ml,
                                                             int32_t batch, int32_t hq, int32_t group,
                                                             int32_t items, float top, uint16_t* out,
                                                             int32_t* gate) {
-  __shared__ float wgt[8][kMergeItems + 1];
-  __shared__ float sums[8];
+  __shared__ float wgt[8][kD];
+  __shared__ float red[8][2];
   const int b = blockIdx.x / (hq / group), kvh = blockIdx.x % (hq / group);
-  const int hl = threadIdx.x / kD, d = threadIdx.x % kD;
-  const bool live = hl < group;
-  const int h = kvh * group + (live ? hl : 0);
+  const int hl = threadIdx.x / kD, d = threadIdx.x % kD;  // blockDim = group * 128
+  const int lane = threadIdx.x & 63, half = d >> 6;
+  const int h = kvh * group + hl;
   constexpr float kC = kInvSqrtD * kLog2e;
   const int64_t th = static_cast<int64_t>(b) * hq + h;  // tail state [B, 1, Hq]
-  float o = 0.f, l_all = 0.f;
+  auto state = [&](int i) -> int64_t { return (static_cast<int64_t>(i) * batch + b) * hq + h; };
+  if (d == 0 && !(tail_ml[3 * th + 2] >= top)) atomicOr(gate, 1);
+  // the common maximum
   float mx = -INFINITY;
-  // the common maximum over the tail and every piece
-  if (live && d == 0) {
-    mx = tail_ml[3 * th];
-    for (int i = 0; i < items; ++i) mx = fmaxf(mx, head_ml[3 * ((static_cast<int64_t>(i) * batch + b) * hq + h)]);
-    if (!(tail_ml[3 * th + 2] >= top)) atomicOr(gate, 1);
-  }
-  for (int i0 = -1; i0 < items; i0 += kMergeItems) {
-    // weights of states i0 .. i0 + kMergeItems - 1 (state -1: the tail)
-    if (live && d == 0) {
-      float lsum = 0.f;
-      for (int j = 0; j < kMergeItems && i0 + j < items; ++j) {
-        const int i = i0 + j;
-        const float* ml = i < 0 ? tail_ml + 3 * th : head_ml + 3 * ((static_cast<int64_t>(i) * batch + b) * hq + h);
-        const float w = mx == -INFINITY || ml[0] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((ml[0] - mx) * kC);
-        wgt[hl][j] = w;
-        lsum += w * ml[1];
-      }
-      sums[hl] = lsum;
-      wgt[hl][kMergeItems] = mx;
+  for (int t = d; t <= items; t += kD) mx = fmaxf(mx, t == 0 ? tail_ml[3 * th] : head_ml[3 * state(t - 1)]);
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  if (lane == 0) red[hl][half] = mx;
+  __syncthreads();
+  mx = fmaxf(red[hl][0], red[hl][1]);
+  __syncthreads();
+  float l_all = 0.f, o = 0.f;
+  for (int t0 = 0; t0 <= items; t0 += kD) {
+    // weights of states t0 - 1 .. t0 + 126
+    float w = 0.f, lw = 0.f;
+    const int t = t0 + d;
+    if (t <= items && mx != -INFINITY) {
+      const float* ml = t == 0 ? tail_ml + 3 * th : head_ml + 3 * state(t - 1);
+      w = ml[0] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((ml[0] - mx) * kC);
+      lw = w * ml[1];
     }
+    wgt[hl][d] = w;
+    for (int off = 32; off > 0; off >>= 1) lw += __shfl_xor(lw, off, 64);
+    if (lane == 0) red[hl][half] = lw;
     __syncthreads();
-    if (live) {
-      l_all += sums[hl];
-      mx = wgt[hl][kMergeItems];
-      const int n = items - i0 < kMergeItems ? items - i0 : kMergeItems;
-      int j = 0;
-      for (; j + 8 <= n; j += 8) {
-        float a[8];
+    l_all += red[hl][0] + red[hl][1];
+    const int n = items + 1 - t0 < kD ? items + 1 - t0 : kD;
+    int j = 0;
+    for (; j + 16 <= n; j += 16) {
+      float a[16];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int i = i0 + j + u;
-          a[u] = i < 0 ? tail_o[th * kD + d] : head_o[((static_cast<int64_t>(i) * batch + b) * hq + h) * kD + d];
-        }
+      for (int u = 0; u < 16; ++u) {
+        const int s2 = t0 + j + u;
+        a[u] = s2 == 0 ? tail_o[th * kD + d] : head_o[state(s2 - 1) * kD + d];
+      }
 #pragma unroll
-        for (int u = 0; u < 8; ++u) o += wgt[hl][j + u] * a[u];
-      }
-      for (; j < n; ++j) {
-        const int i = i0 + j;
-        o += wgt[hl][j] * (i < 0 ? tail_o[th * kD + d] : head_o[((static_cast<int64_t>(i) * batch + b) * hq + h) * kD + d]);
-      }
+      for (int u = 0; u < 16; ++u) o += wgt[hl][j + u] * a[u];
+    }
+    for (; j < n; ++j) {
+      const int s2 = t0 + j;
+      o += wgt[hl][j] * (s2 == 0 ? tail_o[th * kD + d] : head_o[state(s2 - 1) * kD + d]);
     }
     __syncthreads();
   }
-  if (live) out[th * kD + d] = float_to_bf16(l_all > 0.f ? o / l_all : 0.f);
+  out[th * kD + d] = float_to_bf16(l_all > 0.f ? o / l_all : 0.f);
 }
 
 struct shared_ws {
