@@ -183,3 +183,39 @@ def test_generate_is_greedy_over_step_and_checks_flags_once(device):
     # a context beyond max_context is reported once, at the end of the loop
     with pytest.raises(ValueError, match="exceeds max_context"):
         model.generate(first, lengths, caches, table, 2, max_context=100)
+
+
+@pytest.mark.gpu
+def test_step_over_shared_runs_matches_per_request_decode(device):
+    """``PagedDecoder.step`` with ``shared`` (the batch's reused chunks read once
+    per layer, ccpe_decode_shared) against the same step with the per-request
+    decode, from the same state: 4 requests holding 3 of 4 shared runs of 512
+    keys in their own orders and 20-50 keys of their own; logits within 3e-2
+    of the largest logit."""
+    from cacheslide_amd.ccpe import SharedRuns, decode_shared_workspace
+
+    b, n_runs, run_blocks, slots = 4, 4, 32, 3
+    model = PagedDecoder(SHAPE, device, seed=77)
+    own = [20 + 10 * i for i in range(b)]
+    own_blocks = max((n + 1 + BS - 1) // BS for n in own)
+    shared_blocks = n_runs * run_blocks
+    caches = model.new_caches(shared_blocks + b * own_blocks, BS)
+    gen = torch.Generator(device=device).manual_seed(78)
+    for cache in caches:
+        cache.normal_(generator=gen)
+    runs = torch.arange(shared_blocks, dtype=torch.int32).view(n_runs, run_blocks)
+    order = torch.tensor([[(i + j) % n_runs for j in range(slots)] for i in range(b)])
+    table = torch.cat([runs[order].reshape(b, -1),
+                       shared_blocks + torch.arange(b * own_blocks, dtype=torch.int32).view(b, own_blocks)], 1)
+    table = table.to(device)
+    lengths = torch.tensor([slots * run_blocks * BS + n for n in own], device=device)
+    max_context = int(lengths.max()) + 1
+    shared = SharedRuns(table, runs, order, BS, margin=256)
+    ids = torch.tensor([5, 17, 301, 999], device=device)
+    flags = _hip.new_flags(device)
+    la = model.step(ids, lengths, caches, table, max_context=max_context, flags=flags,
+                    workspace=decode_workspace(b, SHAPE.heads, max_context, 1024, device)).float()
+    lb = model.step(ids, lengths, caches, table, max_context=max_context, flags=flags, shared=shared,
+                    workspace=decode_shared_workspace(b, SHAPE.heads, shared, max_context, 1024, device)).float()
+    raise_flags(flags)
+    assert float((la - lb).abs().max()) <= 3e-2 * float(la.abs().max())

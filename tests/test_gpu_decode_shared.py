@@ -61,18 +61,20 @@ def gathered(cache, table, n):
     return rec[..., :128], rec[..., 128:]
 
 
+@pytest.mark.parametrize("margin", [256, 1024])
 @pytest.mark.parametrize("low_gates", [False, True])
-def test_shared_runs_decode_matches_paged_and_oracle(device, low_gates):
+def test_shared_runs_decode_matches_paged_and_oracle(device, low_gates, margin):
     """Saturating positions: the merged states equal the exact decode within
     the bf16 tolerance (and are not its bits: the shared path ran).  Low
     gates: every tail stays below P-1, the exact decode runs, and the result
-    is that decode's, bit for bit."""
+    is that decode's, bit for bit.  Margins of 256 and 1024 keys (tails of up
+    to 345 and 1113 keys)."""
     table, runs, request_runs, lens, q, cache = layout(91 + int(low_gates), low_gates)
     e = seeded((128, P), 95, scale=0.1)
     cope = cope_on(device, 128, P, table=e)
     dtable, dcache, dq = table.to(device), cache.to(device), q.to(device)
     ctx = torch.tensor(lens, dtype=torch.int32, device=device)
-    shared = SharedRuns(dtable, runs, request_runs, BS, margin=256, pieces=2)
+    shared = SharedRuns(dtable, runs, request_runs, BS, margin=margin, pieces=2)
     out = ccpe_decode_shared(dq, dcache, dtable, ctx, cope, shared, max_context=max(lens), split=256)
     ref = ccpe_decode_paged(dq, dcache, dtable, ctx, cope, max_context=max(lens), split=256)
     if low_gates:
