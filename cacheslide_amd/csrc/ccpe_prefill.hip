@@ -184,7 +184,9 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
   uint16_t* ehi = reinterpret_cast<uint16_t*>(&st0);  // [64 pos][128 dims], 16 KB
   uint16_t* elo = reinterpret_cast<uint16_t*>(&st1);
   float* tcol = tab + c * p.tab_stride;
-  for (int pc = 0; pc < p.npos; pc += kPosChunk) {
+  // (a saturated call never reads the table: no gate, suffix sum or lerp)
+  const int table_npos = p.saturated ? 0 : p.npos;
+  for (int pc = 0; pc < table_npos; pc += kPosChunk) {
     // item (position pc + i % 64, dims 8 (i / 64) .. + 7) for i = tid + kThreads r:
     // its 8 values become one 16-byte chunk of E^T hi and one of lo.  All of a
     // thread's loads are issued before any is used.
