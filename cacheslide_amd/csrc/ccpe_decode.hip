@@ -823,6 +823,75 @@ __device__ void combine_pair(const decode_params& p, smem_t<G>& s, int b, int ha
   if (live) p.out[static_cast<int64_t>(b) * p.hq * kD + h * kD + d] = float_to_bf16(L > 0.f ? O / L : 0.f);
 }
 
+// The finish of a group of at most 16 * NCH splits when no split needs
+// recomputing.  Every split partial of the group's heads is loaded before the
+// carries are planned, so the whole merge waits for one round of loads, not
+// one per head pair and split chunk: thread (half, d) owns output dim d of
+// heads half, half + 2, ..., holds the accumulators of all their splits in
+// registers (indices past the last split repeat the last one, so every load
+// is issued unconditionally; their weights are 0), and lane r of each wave
+// holds split r's max and sum, whose weight reaches every lane through
+// v_readlane.  Returns false, with the plan in s.fix_end and nothing
+// written, when some split must be recomputed first; the value is the same
+// in every thread.
+template <int G>
+constexpr int fast_chunks() { return (G + 1) / 2 > 2 ? 2 : 4; }
+
+template <int G, int NCH>
+__device__ bool merge_fast(const decode_params& p, smem_t<G>& s, int b, int h0, int splits) {
+  constexpr int NH = (G + 1) / 2;
+  constexpr int R = 16 * NCH;
+  static_assert(R <= 64 && NH * R <= 128, "partials held per thread");
+  const int half = threadIdx.x >> 7, d = threadIdx.x & (kD - 1), lane = threadIdx.x & 63;
+  const int last = splits - 1;
+  float a[NH][R], mv[NH], lv[NH];
+#pragma unroll
+  for (int j = 0; j < NH; ++j) {
+    // a thread without a j-th head reads head 0's partials and drops them
+    const int h = half + 2 * j < G ? half + 2 * j : 0;
+    const int64_t w0 = ws_index(p, b, h0 + h, 0);
+    const float* acc = p.acc + w0 * kD + d;
+#pragma unroll
+    for (int r = 0; r < R; ++r) a[j][r] = acc[static_cast<int64_t>(r < last ? r : last) * kD];
+    const int rl = lane < last ? lane : last;
+    mv[j] = p.mx[w0 + rl];
+    lv[j] = p.sm[w0 + rl];
+  }
+  plan_group<G>(p, s, b, h0, splits);
+  __syncthreads();
+  if (__builtin_amdgcn_readfirstlane(s.fix_end) > 1) return false;
+#pragma unroll
+  for (int j = 0; j < NH; ++j) {
+    const int h = half + 2 * j;
+    const float m = lane < splits ? mv[j] : -INFINITY;
+    const float M = wave_max(m);
+    const float f = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
+    const float L = wave_sum(lane < splits ? lv[j] * f : 0.f);
+    const int fb = __float_as_int(f);
+    float O = 0.f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) O += __int_as_float(__builtin_amdgcn_readlane(fb, r)) * a[j][r];
+    if (h < G)
+      p.out[static_cast<int64_t>(b) * p.hq * kD + (h0 + h) * kD + d] = float_to_bf16(L > 0.f ? O / L : 0.f);
+  }
+  return true;
+}
+
+template <int G>
+__device__ bool merge_fast_any(const decode_params& p, smem_t<G>& s, int b, int h0, int splits) {
+  switch ((splits + 15) >> 4) {
+    case 1: return merge_fast<G, 1>(p, s, b, h0, splits);
+    case 2: return merge_fast<G, 2>(p, s, b, h0, splits);
+    case 3: if constexpr (fast_chunks<G>() >= 3) return merge_fast<G, 3>(p, s, b, h0, splits); break;
+    case 4: if constexpr (fast_chunks<G>() >= 4) return merge_fast<G, 4>(p, s, b, h0, splits); break;
+    default: break;
+  }
+  // no key, or more splits than the registers hold: plan only
+  plan_group<G>(p, s, b, h0, splits);
+  __syncthreads();
+  return false;
+}
+
 // Split 0 of every (request, KV head) exactly, then the speculative splits;
 // the grid is ordered split-major so the exact workgroups start first.
 template <int G, bool PAGED>
@@ -862,8 +931,7 @@ __global__ void __launch_bounds__(kThreads) decode_finish_kernel(decode_params p
   if (splits > p.smax) splits = p.smax;
   if (splits < 0) splits = 0;  // no key: zero rows (the call is flagged)
   bool bad = false;
-  plan_group<G>(p, s, b, h0, splits);
-  __syncthreads();
+  if (merge_fast_any<G>(p, s, b, h0, splits)) return;
   fixup_group<G, PAGED>(p, s, b, kvh, bad);
   for (int h = 0; h < G; h += 2) combine_pair<G>(p, s, b, h0 + h, h + 1 < G ? h0 + h + 1 : -1, splits);
   if (bad) atomicOr(p.flags, CS_FLAG_BLOCK_INVALID);

@@ -653,6 +653,39 @@ def test_decode_group_and_block_sizes(device, hq, hkv, bs, split):
         assert_close_bf16(out[b:b + 1], expected)
 
 
+@pytest.mark.parametrize("hq, hkv, splits", [
+    (8, 2, [16, 17, 32, 33]), (8, 2, [48, 49, 64, 65]), (16, 2, [31, 32, 33]), (2, 2, [1, 64, 65]),
+])
+def test_decode_finish_split_counts(device, hq, hkv, splits):
+    """Split counts on both sides of each 16-split chunk of the finishing
+    workgroup's register merge and of its limit (64 splits for GQA groups up
+    to 4, 32 for a group of 8), past which the merge reads its partials in
+    rounds.  Splits of 256 keys, the last one partly filled; the right-most
+    split's gate mass reaches P-1 in every head, so no split is recomputed
+    and the register merge (or, past its limit, the merge in rounds) forms
+    every output row."""
+    split, bs = 256, 16
+    lens = [split * (s - 1) + 1 + (7 * s) % (split - 1) for s in splits]
+    assert [(n + split - 1) // split for n in lens] == splits
+    nb, table, rows = paged_layout(lens, hkv, bs, 128, seed=hq + len(lens))
+    cache = seeded((nb, hkv, bs, 256), 290 + hq, dtype=torch.bfloat16)
+    keys = [seeded((n, hkv, 128), 300 + i + hq, dtype=torch.bfloat16) for i, n in enumerate(lens)]
+    vals = [seeded((n, hkv, 128), 310 + i + hq, dtype=torch.bfloat16) for i, n in enumerate(lens)]
+    fill_paged(cache, rows, keys, vals)
+    e = seeded((128, 64), 320 + hq, scale=0.02)
+    q = seeded((len(lens), hq, 128), 321 + hq, dtype=torch.bfloat16)
+    cope = cope_on(device, 128, 64, table=e)
+    out = ccpe_decode_paged(q.to(device), cache.to(device), table.to(device),
+                            torch.tensor(lens, dtype=torch.int32, device=device), cope, split=split)
+    for b, n in enumerate(lens):
+        if n > split:  # split 0 saturates every head: no recomputation
+            right = orc.sigmoid(orc.logits(acc_np(q[b:b + 1]), acc_np(keys[b][-split:]))).sum(axis=-1)
+            assert right.min() >= 63
+        expected = orc.cope_attention(acc_np(q[b:b + 1]), acc_np(keys[b]), acc_np(vals[b]), e.numpy(),
+                                      np.array([n - 1]))
+        assert_close_bf16(out[b:b + 1], expected)
+
+
 def test_zero_query_tokens_give_an_empty_result(device):
     # position.py:117-150 requires one key and one head, not one query token
     cope = CoPE(16, 8, device=device)
