@@ -136,7 +136,35 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
   const int head = kvh * p.group + c % p.group;
   const bool row_ok = row < p.nq;
   const int nk = p.nk[b];
-  const int64_t qp = row_ok ? p.qpos[b * p.qpos_sb + row] : -1;
+  // The prologue's loads -- the row's position, its Q row and the first 64
+  // positions of E -- go out together and unconditionally, from clamped
+  // addresses (a row past nq reads row 0, a position past P reads position
+  // 0; select drops the values), so their latencies overlap instead of
+  // following one another behind the reduction of the positions.
+  const int row_c = row_ok ? row : 0;
+  const int64_t qp_raw = p.qpos[b * p.qpos_sb + row_c];
+  uint4 qraw[8];
+  {
+    const uint16_t* qrow = p.q + b * p.q_sb + static_cast<int64_t>(row_c) * p.q_st + head * p.q_sh;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) qraw[ks] = *reinterpret_cast<const uint4*>(qrow + 16 * ks + 8 * h);
+  }
+  // item (position pc + i % 64, dims 8 (i / 64) .. + 7) for i = tid + kThreads r:
+  // its 8 values become one 16-byte chunk of E^T hi and one of lo
+  constexpr int kItems = kPosChunk * kChunks / kThreads;
+  float ev[kItems][8];
+  auto load_e = [&](int pc) {
+#pragma unroll
+    for (int r = 0; r < kItems; ++r) {
+      const int i = tid + kThreads * r;
+      const int pos = i % kPosChunk, dg = i / kPosChunk;
+      const int pp = pc + pos < p.npos ? pc + pos : 0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ev[r][e] = p.e[(8 * dg + e) * p.npos + pp];
+    }
+  };
+  load_e(0);
+  const int64_t qp = row_ok ? qp_raw : -1;
   bool sel_col = false;   // the column's row is selected: fixed keys other than its own are invisible
   float canon_self = 0.f;  // canonical position of the column's own key (NaN: contextual)
   // a fixed row that is not selected: its profile row, canonical positions
@@ -169,14 +197,8 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
 
   // ---- Q^T as the B operand of S^T: 8 k-steps of 16 dims ---------------------
   bf16x8 qb[8];
-  {
-    const uint16_t* qrow = p.q + b * p.q_sb + static_cast<int64_t>(row_ok ? row : 0) * p.q_st + head * p.q_sh;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-      const uint4 u = row_ok ? *reinterpret_cast<const uint4*>(qrow + 16 * ks + 8 * h) : make_uint4(0, 0, 0, 0);
-      qb[ks] = as_bf16x8(u);
-    }
-  }
+  for (int ks = 0; ks < 8; ++ks) qb[ks] = as_bf16x8(row_ok ? qraw[ks] : make_uint4(0, 0, 0, 0));
 
   // ---- QE table: QE^T = E^T Q^T on MFMA, E split into bf16 hi + lo ------------
   // E^T hi / lo for kPosChunk positions are staged in the (still unused) K / V
@@ -187,29 +209,19 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
   // (a saturated call never reads the table: no gate, suffix sum or lerp)
   const int table_npos = p.saturated ? 0 : p.npos;
   for (int pc = 0; pc < table_npos; pc += kPosChunk) {
-    // item (position pc + i % 64, dims 8 (i / 64) .. + 7) for i = tid + kThreads r:
-    // its 8 values become one 16-byte chunk of E^T hi and one of lo.  All of a
-    // thread's loads are issued before any is used.
-    constexpr int kItems = kPosChunk * kChunks / kThreads;
-    float ev[kItems][8];
-#pragma unroll
-    for (int r = 0; r < kItems; ++r) {
-      const int i = tid + kThreads * r;
-      const int pos = i % kPosChunk, dg = i / kPosChunk;
-      const bool pos_ok = pc + pos < p.npos;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ev[r][e] = pos_ok ? p.e[(8 * dg + e) * p.npos + pc + pos] : 0.f;
-    }
+    if (pc > 0) load_e(pc);  // the first chunk was loaded with Q
     __syncthreads();  // the previous chunk's MFMAs have read the stage
 #pragma unroll
     for (int r = 0; r < kItems; ++r) {
       const int i = tid + kThreads * r;
       const int pos = i % kPosChunk, dg = i / kPosChunk;
+      const bool pos_ok = pc + pos < p.npos;
       bf16x8 hv, lv;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        hv[e] = static_cast<__bf16>(ev[r][e]);
-        lv[e] = static_cast<__bf16>(ev[r][e] - static_cast<float>(hv[e]));
+        const float x = pos_ok ? ev[r][e] : 0.f;
+        hv[e] = static_cast<__bf16>(x);
+        lv[e] = static_cast<__bf16>(x - static_cast<float>(hv[e]));
       }
       const int slot = pos * kChunks + (dg ^ (pos & 15));
       *reinterpret_cast<bf16x8*>(ehi + slot * 8) = hv;
@@ -246,7 +258,21 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
   {
     const float top_qe = tcol[p.npos - 1];
     __syncthreads();  // both lanes of every column hold it before any entry moves
-    for (int j = h; j <= p.npos; j += 2) tcol[j] = j < p.npos - 1 ? tcol[j] - top_qe : 0.f;
+    // eight entries of the lane (j = h, h + 2, ...) per round: their reads go
+    // out together (indices past P-1 read entry P-1 and are dropped)
+    for (int j0 = h; j0 <= p.npos; j0 += 16) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int j = j0 + 2 * u;
+        v[u] = tcol[j < p.npos - 1 ? j : p.npos - 1];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int j = j0 + 2 * u;
+        if (j <= p.npos) tcol[j] = j < p.npos - 1 ? v[u] - top_qe : 0.f;
+      }
+    }
   }
   __syncthreads();
 

@@ -94,6 +94,48 @@ def test_prefill_8x4096_paged_matches_oracle(device):
         assert np.array_equal(kk[rows], kb[rows])
 
 
+def test_prefill_odd_row_block_count_writes_every_row(device):
+    """An odd number of row blocks (8 requests x 8 KV heads x 33 blocks of 64
+    rows) through the C-ABI into an output pre-filled with NaN: every row is
+    written, and sampled rows of the first, middle and last blocks and at
+    block edges equal the oracle's."""
+    from cacheslide_amd import _hip
+    from cacheslide_amd.ccpe import _paged_source
+
+    B, N = 8, 33 * 64
+    say(f"prefill B={B} N={N} (33 row blocks)")
+    gen = torch.Generator(device=device).manual_seed(2010)
+    q = torch.randn((B, N, HQ, D), generator=gen, device=device).to(torch.bfloat16)
+    k = torch.randn((B, N, HKV, D), generator=gen, device=device).to(torch.bfloat16)
+    v = torch.randn((B, N, HKV, D), generator=gen, device=device).to(torch.bfloat16)
+    cope, e = cope_from(device, gen)
+    nblocks = B * N // BS
+    table = torch.randperm(nblocks, generator=torch.Generator().manual_seed(2011)).to(torch.int32)
+    table = table.view(B, N // BS).to(device)
+    cache = torch.empty((nblocks, HKV, BS, 2 * D), dtype=torch.bfloat16, device=device)
+    place(cache, table, k, v)
+    qpos = torch.arange(N, device=device).repeat(B, 1).contiguous()
+    lens = torch.full((B,), N, dtype=torch.int32, device=device)
+    out = torch.full((B, N, HQ, D), float("nan"), dtype=torch.bfloat16, device=device)
+    flags = _hip.new_flags(device)
+    lib = _hip.load()
+    status = lib.cs_ccpe_prefill_bf16(
+        _hip.ptr(q), q.stride(0), q.stride(1), q.stride(2), _hip.ptr(qpos), qpos.stride(0), B, N, HQ, HKV,
+        _hip.ptr(lens), _paged_source(cache, table), _hip.ptr(cope.position_embeddings.detach().contiguous()),
+        P, _hip.ptr(out), _hip.ptr(flags), _hip.stream_of(device))
+    assert status == 0
+    torch.cuda.synchronize()
+    assert int(flags[0].item()) == 0
+    assert bool(torch.isfinite(out.float()).all())
+    rows = np.array([0, 63, 64, 15 * 64 + 7, 16 * 64, 16 * 64 + 37, 16 * 64 + 63, 17 * 64, 17 * 64 + 5,
+                     31 * 64 + 9, 32 * 64, N - 1])
+    for b in (0, 5, B - 1):
+        kb, vb = k[b].float().cpu().numpy(), v[b].float().cpu().numpy()
+        qb = q[b, torch.from_numpy(rows).to(device)].float().cpu().numpy()
+        expected = orc.cope_attention(qb, kb, vb, e, rows)
+        assert_close_bf16(out[b, torch.from_numpy(rows).to(device)], expected)
+
+
 def test_decode_64x32769_paged_matches_oracle(device):
     B, CTX = 64, 32769
     say(f"decode B={B} ctx={CTX}")
