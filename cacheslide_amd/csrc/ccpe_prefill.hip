@@ -208,7 +208,14 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
   float* tcol = tab + c * p.tab_stride;
   // (a saturated call never reads the table: no gate, suffix sum or lerp)
   const int table_npos = p.saturated ? 0 : p.npos;
-  for (int pc = 0; pc < table_npos; pc += kPosChunk) {
+  // the column's QE for positions 32 k + 8 (v / 4) + 4 h + v % 4 in qe[k][v]
+  constexpr int kPb = kMaxPos / 32;
+  floatx16 qe[kPb];
+#pragma unroll
+  for (int k = 0; k < kPb; ++k) qe[k] = floatx16{};
+#pragma unroll
+  for (int pc = 0; pc < kMaxPos; pc += kPosChunk) {
+    if (pc >= table_npos) break;
     if (pc > 0) load_e(pc);  // the first chunk was loaded with Q
     __syncthreads();  // the previous chunk's MFMAs have read the stage
 #pragma unroll
@@ -241,38 +248,41 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
         acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, qb[ks], acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, qb[ks], acc, 0, 0, 0);
       }
-      // raw-score units; finite (clamped to +-1e30, NaN to -1e30), so
-      // bias + (-inf) stays -inf
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int pv = pc + 32 * pb + 8 * (v >> 2) + 4 * h + (v & 3);
-        if (pv < p.npos) tcol[pv] = fminf(fmaxf(acc[v] * kSqrtD, -1e30f), 1e30f);
-      }
+      qe[pc / 32 + pb] = acc;
     }
   }
-  // Shift every entry by the column's QE[P-1] (the bias of saturated keys;
-  // softmax is invariant to it) and repeat entry P-1 as entry P: a position p
-  // then reads entries lo = floor(min(p, P-1)) and lo + 1 with no clamp, and
-  // a saturated key adds 0.
-  __syncthreads();
-  {
-    const float top_qe = tcol[p.npos - 1];
-    __syncthreads();  // both lanes of every column hold it before any entry moves
-    // eight entries of the lane (j = h, h + 2, ...) per round: their reads go
-    // out together (indices past P-1 read entry P-1 and are dropped)
-    for (int j0 = h; j0 <= p.npos; j0 += 16) {
-      float v[8];
+  // Entries in raw-score units, finite (clamped to +-1e30, NaN to -1e30, so
+  // bias + (-inf) stays -inf), each shifted by the column's QE[P-1] (the bias
+  // of saturated keys; softmax is invariant to it), and entry P repeating
+  // entry P-1: a position p reads entries lo = floor(min(p, P-1)) and lo + 1
+  // with no clamp, and a saturated key adds 0.  QE[P-1] comes from the
+  // registers of the lane of the column that holds it, so every entry is
+  // written once, already shifted.
+  if (table_npos > 0) {
+    auto clamp_qe = [](float x) { return fminf(fmaxf(x * kSqrtD, -1e30f), 1e30f); };
+    const int p1 = p.npos - 1;
+    const int kt = p1 >> 5, rt = p1 & 31;
+    const int vt = 4 * (rt >> 3) + (rt & 3), ht = (rt >> 2) & 1;
+    float t = 0.f;
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int j = j0 + 2 * u;
-        v[u] = tcol[j < p.npos - 1 ? j : p.npos - 1];
-      }
+    for (int k = 0; k < kPb; ++k)
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int j = j0 + 2 * u;
-        if (j <= p.npos) tcol[j] = j < p.npos - 1 ? v[u] - top_qe : 0.f;
+      for (int v = 0; v < 16; ++v) t = k == kt && v == vt ? qe[k][v] : t;
+    const float t_other = __shfl_xor(t, 32, 64);
+    const float top_qe = clamp_qe(h == ht ? t : t_other);
+    // every register of the chunks that start below entry P is stored,
+    // without a branch: entries from P-1 up are 0, and indices past P store
+    // entry P (which the last line stores in any case)
+#pragma unroll
+    for (int k = 0; k < kPb; ++k) {
+      if (32 * k >= p.npos) break;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int pv = 32 * k + 8 * (v >> 2) + 4 * h + (v & 3);
+        tcol[pv < p.npos ? pv : p.npos] = pv < p1 ? clamp_qe(qe[k][v]) - top_qe : 0.f;
       }
     }
+    if (h == 0) tcol[p.npos] = 0.f;
   }
   __syncthreads();
 
